@@ -1,0 +1,323 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X Qwen3-ASR decoder self-attention path.
+
+Headline (BASELINE.json metric, config 3): one decode step of the 1.7B decoder
+shape (16 q / 8 kv heads, head_dim 128) for 16 slots with ragged contexts
+U[400, 2400], across 28 layers.  Each layer is one launch of the fused stage
+(a)+(b) kernel (q/k RMSNorm + MRoPE + KV append + split-K GQA attention) on
+its own KV cache, so the working set (~2.6 GB of K/V) is far beyond the
+256 MB Infinity Cache.  The 28 launches are captured in one HIP graph and
+replayed; the timed region is K replays bracketed by events and syncs.
+
+value = algorithmic bytes / time (GB/s), bytes per slot-layer =
+  4096*(L+1) (K+V rows) + 8192 (Q, O) + 16384 (stage (a) row in/out).
+Also reported: configs 1, 2, 4, 5 (us/layer, GB/s, TFLOP/s with causal-exact
+FLOPs 4*hd*nqh*sum_r(kv_start+r+1)), the roofline of the dominant kernel, and
+the reference CPU path (the C++ restatement of cpu_decoder.rs in oracle/)
+timed on a bounded sample of config 3 on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+                       [--only decode3|decode1|decode4|decode5|prefill2|prefill4]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "qwen3-asr-wgpu_amd")
+sys.path.insert(0, PKG)
+
+METRIC = "decode attn µs/layer + HBM GB/s; prefill attn TFLOP/s (1.7B shape, 1 GPU)"
+NQH, NKVH, HD, LAYERS = 16, 8, 128, 28
+TOT = (NQH + 2 * NKVH) * HD
+QDIM = NQH * HD
+SEED_BASE = 0x51A50000
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, vendor figure
+MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA, vendor figure
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def splitmix_lengths(seed: int, n: int, lo: int, hi: int):
+    """Per-slot lengths U[lo, hi] from SplitMix64 (the tests' generator)."""
+    state = seed & 0xFFFFFFFFFFFFFFFF
+    out = []
+    for _ in range(n):
+        state = (state + 0x9E3779B97F4A7C15) & 0xFFFFFFFFFFFFFFFF
+        z = state
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & 0xFFFFFFFFFFFFFFFF
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & 0xFFFFFFFFFFFFFFFF
+        z ^= z >> 31
+        out.append(lo + z % (hi - lo + 1))
+    return out
+
+
+def decode_bytes(lengths):
+    """Algorithmic bytes of one decode layer: lengths = keys attended (pos+1)."""
+    return sum(4096 * L + 8192 + 16384 for L in lengths)
+
+
+def prefill_flops(s: int, kv_start: int) -> float:
+    return 4.0 * HD * NQH * sum(kv_start + r + 1 for r in range(s))
+
+
+def cap_for(need: int) -> int:
+    return max(1024, (need + 255) // 256 * 256)
+
+
+class Setup:
+    def __init__(self, slots: int, cap: int, layers: int = LAYERS):
+        import torch
+
+        import qasr_attn
+
+        self.torch = torch
+        self.q = qasr_attn
+        self.ctx = qasr_attn.Context(NQH, NKVH, HD, layers, 1e-6, 16384, 0)
+        c, s = qasr_attn.mrope_text_tables(16384)
+        self.ctx.set_rope_tables(c, s)
+        self.kv = qasr_attn.KVPool(self.ctx, slots, cap)
+        pool = self.kv.tensor()
+        g = torch.Generator(device="cuda")
+        g.manual_seed(1234)
+        for sl in range(pool.shape[0]):  # synthetic cache contents, N(0,1) f16
+            pool[sl].normal_(generator=g)
+        self.layers = layers
+        gains = torch.randn((layers, 2, HD), device="cuda", generator=g) * 0.1 + 1.0
+        self.gains = gains.half().contiguous()
+
+    def close(self):
+        self.kv.close()
+        self.ctx.close()
+
+
+def graph_time(torch, fn_step, steps: int, warmup: int):
+    """Capture fn_step (a sequence of launches on the current stream) in a HIP
+    graph, replay `warmup` times, then time `steps` replays with events."""
+    fn_step()  # eager: argument checks, lazy workspace growth
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn_step()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    return ms, graph
+
+
+def bench_decode(slots: int, lengths, steps: int, warmup: int, layers: int = LAYERS):
+    """Fused stage (a)+(b) decode step over `layers` layers; lengths = cached
+    positions per slot before the step (the step attends lengths[i]+1 keys)."""
+    import torch
+
+    st = Setup(slots, cap_for(max(lengths) + 1), layers)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(99)
+    qkv = torch.randn((layers, slots, TOT), device="cuda", generator=g).half()
+    out = torch.empty((layers, slots, QDIM), device="cuda", dtype=torch.float16)
+    pos = list(lengths)
+
+    def step():
+        for l in range(layers):
+            st.q.decode_step(st.ctx, st.kv, l, pos, qkv[l], st.gains[l, 0], st.gains[l, 1], out[l])
+
+    ms, graph = graph_time(torch, step, steps, warmup)
+    del graph
+    nbytes = decode_bytes([L + 1 for L in lengths]) * layers
+    st.close()
+    return {"ms_per_step": ms, "us_per_layer": ms * 1e3 / layers,
+            "bytes_per_step": nbytes, "GBps": nbytes / (ms * 1e-3) / 1e9}
+
+
+def bench_prefill(s: int, kv_start: int, steps: int, warmup: int, layers: int = LAYERS):
+    """Stage (c) prefill attention of s rows at kv_start, per layer on its own
+    cache; stage (a) timed separately."""
+    import torch
+
+    st = Setup(1, cap_for(kv_start + s), layers)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(98)
+    q = torch.randn((layers, s, QDIM), device="cuda", generator=g).half()
+    qkv = torch.randn((layers, s, TOT), device="cuda", generator=g).half()
+    out = torch.empty((layers, s, QDIM), device="cuda", dtype=torch.float16)
+    qw = torch.empty((layers, s, QDIM), device="cuda", dtype=torch.float16)
+
+    def attn():
+        for l in range(layers):
+            st.q.prefill_attn(st.ctx, st.kv, l, 0, kv_start, s, q[l], out[l])
+
+    def stage_a():
+        for l in range(layers):
+            st.q.qk_norm_rope_append(st.ctx, st.kv, l, [(0, kv_start, s)], qkv[l],
+                                     st.gains[l, 0], st.gains[l, 1], qw[l])
+
+    ms_a, g1 = graph_time(torch, attn, steps, warmup)
+    ms_s, g2 = graph_time(torch, stage_a, steps, warmup)
+    del g1, g2
+    fl = prefill_flops(s, kv_start)
+    st.close()
+    us = ms_a * 1e3 / layers
+    return {"us_per_layer": us, "TFLOPs": fl / (us * 1e-6) / 1e12, "flops_per_layer": fl,
+            "stage_a_us_per_layer": ms_s * 1e3 / layers}
+
+
+def cpu_baseline(lengths, budget_s: float = 10.0):
+    """Reference CPU path (C++ restatement of cpu_decoder.rs, oracle/) on config
+    3: stage (a) + attention for each of the 16 slots, one layer at a time,
+    repeated until `budget_s` of CPU time is spent.  Returns GB/s-equivalent
+    (same algorithmic bytes) and us/layer."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or O.hardware_threads()
+    threads = max(1, min(threads, O.hardware_threads()))
+    cap = cap_for(max(lengths) + 1)
+    sh = O.make_shape()
+    rng = O.Rng(SEED_BASE + 3)
+    tab_c, tab_s = O.text_rope_tables_f16(cap)
+    cos, sin = O.f32_from_f16(tab_c), O.f32_from_f16(tab_s)
+    qg = rng.normal_f16((HD,), 1.0, 0.1)
+    kg = rng.normal_f16((HD,), 1.0, 0.1)
+    caches = []
+    for L in lengths:
+        k = np.zeros((NKVH, cap, HD), np.float32)
+        v = np.zeros((NKVH, cap, HD), np.float32)
+        k[:, :L] = O.f32_from_f16(rng.normal_f16((NKVH, L, HD)))
+        v[:, :L] = O.f32_from_f16(rng.normal_f16((NKVH, L, HD)))
+        caches.append((k, v))
+    rows = rng.normal_f16((len(lengths), TOT))
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        for i, L in enumerate(lengths):
+            O.layer_attn(sh, cap, rows[i:i + 1], L, qg, kg, cos, sin, caches[i][0], caches[i][1],
+                         nthreads=threads)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    nbytes = decode_bytes([L + 1 for L in lengths])
+    return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_layer": med * 1e6,
+            "sample": f"config 3 decode layer-steps (16 slots, lengths as the GPU run), "
+                      f"{len(times)} reps over ~{budget_s:.0f} s, median; oracle/oracle.cpp "
+                      f"(C++ restatement of cpu_decoder.rs:274-423, f32), {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="headline config only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", default="", help="run one workload (for profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(no multi-GPU path is built; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import qasr_attn
+
+    qasr_attn.load()
+    assert torch.cuda.is_available(), "bench.py needs an MI355X"
+    K, W = args.steps, args.warmup
+    lens3 = splitmix_lengths(SEED_BASE + 3, 16, 400, 2400)
+
+    only = args.only
+    if only:
+        runs = {
+            "decode3": lambda: bench_decode(16, lens3, K, W),
+            "decode1": lambda: bench_decode(1, [511], K, W),
+            "decode4": lambda: bench_decode(1, [8192], K, W),
+            "decode5": lambda: bench_decode(64, splitmix_lengths(SEED_BASE + 5, 64, 64, 4096), K, W),
+            "prefill2": lambda: bench_prefill(420, 0, K, W),
+            "prefill4": lambda: bench_prefill(512, 7680, K, W),
+        }
+        log(json.dumps({only: runs[only]()}))
+        return
+
+    log(f"[bench] config 3: 16 slots, lengths {lens3}")
+    d3 = bench_decode(16, lens3, K, W)
+    log(f"[bench] config 3: {d3['us_per_layer']:.2f} us/layer, {d3['GBps']:.0f} GB/s")
+    extra = {}
+    if not args.quick:
+        log("[bench] config 1")
+        extra["config1_decode"] = bench_decode(1, [511], K, W)
+        log("[bench] config 2")
+        extra["config2_prefill"] = bench_prefill(420, 0, K, W)
+        log("[bench] config 4 (last 512-row chunk at kv_start 7680; decode at 8192)")
+        extra["config4_prefill_last_chunk"] = bench_prefill(512, 7680, K, W)
+        extra["config4_decode"] = bench_decode(1, [8192], K, W)
+        log("[bench] config 5")
+        lens5 = splitmix_lengths(SEED_BASE + 5, 64, 64, 4096)
+        extra["config5_decode"] = bench_decode(64, lens5, max(5, K // 5), W)
+        for k, v in extra.items():
+            log(f"[bench] {k}: {json.dumps(v)}")
+
+    us = d3["us_per_layer"]
+    per_launch_bytes = decode_bytes([L + 1 for L in lens3])
+    achieved = per_launch_bytes / (us * 1e-6) / 1e9
+    traffic = None
+    tf = os.path.join(REPO, "profiles", "decode_attn_traffic.json")
+    if os.path.exists(tf):
+        try:
+            traffic = json.load(open(tf)).get("config3_hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+    roofline = {"bound": "hbm", "kernel": "decode_attn_kernel<true> (fused stage a+b)",
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "bytes_per_launch": per_launch_bytes, "avg_launch_us": round(us, 3)}
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline (oracle) ...")
+        cpu = cpu_baseline(lens3)
+        log(f"[bench] cpu baseline {cpu['us_per_layer']:.0f} us/layer on {cpu['cores']} threads")
+    line = {
+        "metric": METRIC,
+        "value": round(d3["GBps"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(d3["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "config3: decode step of the 1.7B decoder shape (16 q / 8 kv "
+                               "heads, hd 128), 16 slots, ragged contexts U[400,2400], 28 "
+                               "layers (fused q/k-norm+MRoPE+KV append+GQA attention per "
+                               "layer, HIP-graph replay)",
+                   "global_batch": 16, "seq_len": int(max(lens3) + 1), "parallelism": "none (1 GPU)",
+                   "decode_us_per_layer": round(us, 3)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    if extra:
+        line["extra"] = extra
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,176 @@
+/*
+ * qasr_attn.h -- C ABI of the MI355X (gfx950) Qwen3-ASR decoder self-attention
+ * path: fused q/k-RMSNorm + MRoPE + fp16 KV append, GQA decode attention over
+ * ragged per-slot contexts, and causal (chunked) prefill attention.
+ *
+ * The reference (eclipse005/qwen3-asr-wgpu, Rust + WGSL) has no plugin or FFI
+ * around attention: its seam is the `TextBackend` enum (src/inference.rs:
+ * 213-269) whose GPU arm runs the attention blocks inside WgpuTextDecoder.
+ * Each entry point below names the reference code it replaces.  A Rust host
+ * binds these with `extern "C"` declarations, the way src/mel.rs:544-566 binds
+ * the vendored soxr C library.
+ *
+ * Conventions
+ *  - Every function returns an int status (QASR_OK == 0); on failure
+ *    qasr_last_error() returns a thread-local message.  Nothing throws across
+ *    the ABI.
+ *  - Tensor arguments named `*_dev` are device pointers (f16 stored as raw
+ *    binary16 bits).  Arrays of slot ids, positions and lengths are HOST
+ *    pointers: the host plans the launch from them, as the reference's host
+ *    writes its per-step uniforms (decoder.rs:1674-1714, 3348-3379).
+ *  - Work is stream-ordered and asynchronous on `stream` (a hipStream_t; NULL
+ *    is the null stream).  A context and its KV pools are not thread-safe: one
+ *    host thread drives a context, as the reference serialises decoder calls
+ *    behind a Mutex (inference.rs:307-323).  Calls that share a KV pool must
+ *    be ordered on one stream (they share its split-K workspace).
+ *  - Head layout: head_dim must be 128 and num_attention_heads must be twice
+ *    num_key_value_heads (both Qwen3-ASR sizes: 16 q heads, 8 kv heads).
+ */
+#ifndef QASR_ATTN_H
+#define QASR_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QASR_ABI_VERSION 1
+
+/* Status codes. */
+#define QASR_OK 0
+#define QASR_EINVAL 1   /* bad argument or unsupported shape */
+#define QASR_ERANGE 2   /* position / length beyond capacity, max_seq or tables */
+#define QASR_ENOMEM 3   /* device allocation failed */
+#define QASR_EDEVICE 4  /* HIP runtime error */
+#define QASR_ESTATE 5   /* call out of order (e.g. no RoPE tables yet) */
+
+/* KV_INITIAL_CAP / KV_STEP (decoder.rs:716-725), DECODER_MAX_SEQ (inference.rs:19). */
+#define QASR_KV_INITIAL_CAP 1024
+#define QASR_KV_STEP 256
+#define QASR_DECODER_MAX_SEQ 16384
+
+/* Text decoder attention hyper-parameters (TextConfig, decoder.rs:164-174). */
+typedef struct qasr_attn_cfg {
+    int32_t num_attention_heads; /* 16 */
+    int32_t num_key_value_heads; /* 8 */
+    int32_t head_dim;            /* 128 */
+    int32_t num_hidden_layers;   /* 28 */
+    float rms_norm_eps;          /* 1e-6 */
+    int32_t max_seq;             /* ceiling on positions (DECODER_MAX_SEQ) */
+} qasr_attn_cfg;
+
+typedef struct qasr_ctx qasr_ctx;
+typedef struct qasr_kv qasr_kv;
+
+/* A run of consecutive positions of one slot: rows pos0 .. pos0+rows-1.
+ * A decode batch is one 1-row segment per slot; a prefill is one segment. */
+typedef struct qasr_segment {
+    int32_t slot;
+    int32_t pos0;
+    int32_t rows;
+} qasr_segment;
+
+/* Device layout of a KV pool, for callers that read or seed the cache.
+ * Element (slot, layer, kv, head, pos, d), kv 0 = K and 1 = V, f16 at
+ *   base + ((((slot*layers + layer)*2 + kv)*nkvh + head)*cap + pos)*head_dim + d
+ * i.e. each (slot, layer) holds the reference's per-layer K and V buffers,
+ * [nkvh][cap][head_dim] f16 (decoder.rs:1270-1271, index (kvh*cap+pos)*hd). */
+typedef struct qasr_kv_info {
+    void* base_dev;
+    int32_t slots;
+    int32_t layers;
+    int32_t nkvh;
+    int32_t cap;
+    int32_t head_dim;
+    int64_t slot_stride;  /* elements */
+    int64_t layer_stride; /* elements */
+    int64_t kv_stride;    /* elements, K block -> V block */
+    int64_t head_stride;  /* elements (= cap * head_dim) */
+    size_t bytes;
+} qasr_kv_info;
+
+int qasr_abi_version(void);
+const char* qasr_last_error(void);
+
+/* Context: binds a device and the shape.  Replaces WgpuTextDecoder::load's
+ * attention-side setup (decoder.rs:977-1246). */
+int qasr_ctx_create(const qasr_attn_cfg* cfg, int device, qasr_ctx** out);
+void qasr_ctx_destroy(qasr_ctx* ctx);
+
+/* MRoPE cos/sin tables for text positions 0..rows-1, rounded to f16
+ * ([rows][head_dim] each).  Host-only.  Replaces compute_mrope_cos_sin +
+ * text_positions + the f16 cast (mrope.rs:5-80, inference.rs:1038-1049). */
+int qasr_mrope_text_tables(int rows, int head_dim, double rope_theta,
+                           const int32_t* mrope_section, int nsec, int interleaved,
+                           uint16_t* cos_f16, uint16_t* sin_f16);
+
+/* Upload f16 tables ([rows][head_dim], host).  Replaces set_rope_tables
+ * (decoder.rs:1664-1667; cpu_decoder.rs:215-221). */
+int qasr_set_rope_tables(qasr_ctx* ctx, const uint16_t* cos_f16, const uint16_t* sin_f16,
+                         int rows);
+
+/* KV pool of `slots` sequences x all layers, capacity rounded up to KV_STEP.
+ * Replaces the per-layer k_cache/v_cache buffers and fork_capped's per-slot
+ * KV (decoder.rs:1270-1271, 1422-1423, 2453-2457). */
+int qasr_kv_create(qasr_ctx* ctx, int slots, int cap, qasr_kv** out);
+void qasr_kv_destroy(qasr_kv* kv);
+int qasr_kv_get_info(const qasr_kv* kv, qasr_kv_info* out);
+
+/* Grow-only capacity change, KV_STEP granular, clamped to max_seq; rows
+ * 0..keep_rows-1 of every (slot, layer, head) are preserved.  Synchronous.
+ * Replaces WgpuTextDecoder::ensure_capacity (decoder.rs:1604-1661). */
+int qasr_kv_ensure_capacity(qasr_kv* kv, int need, int keep_rows, int* cap_out);
+
+/* Stage (a): per row, RMSNorm each q and k head (gain q_gain / k_gain, f16
+ * [head_dim]), rotate-half RoPE at the row's position, round to f16; roped Q
+ * -> q_out_dev [rows][nqh*hd]; roped K and raw V -> the pool at (slot, layer,
+ * pos).  qkv_dev holds the segments' rows back to back, fused [q | k | v]
+ * ((nqh + 2*nkvh)*hd f16 per row).  Bit-identical to cpu_decoder.rs:274-290 +
+ * 398-423.  Replaces qkv_extract / qkv_extract_slots (shaders.rs:1376-1635,
+ * dispatched at decoder.rs:1813-1817, 3414-3421, 4871-4873). */
+int qasr_qk_norm_rope_append(qasr_ctx* ctx, qasr_kv* kv, int layer,
+                             const qasr_segment* segs, int nseg,
+                             const void* qkv_dev, const void* q_gain_dev,
+                             const void* k_gain_dev, void* q_out_dev, void* stream);
+
+/* Stage (b): decode attention.  Batch entry b reads roped q_dev[b] ([nqh][hd])
+ * against keys 0..cur_len[b]-1 of slot slots[b] (NULL: slot b) and writes
+ * out_dev[b] ([nqh*hd] f16).  Split-K over the context with an in-kernel
+ * merge.  Replaces encode_gqa / gqa_decode_single[_slots] /
+ * gqa_decode_split_p1_pair / gqa_split_merge (decoder.rs:1959-2025, 3426-3451;
+ * shaders.rs:1881-2905); semantics of cpu_decoder.rs:292-365 with rows = 1. */
+int qasr_decode_attn(qasr_ctx* ctx, qasr_kv* kv, int layer, int batch, const int32_t* slots,
+                     const int32_t* cur_len, const void* q_dev, void* out_dev, void* stream);
+
+/* Stages (a)+(b) fused into one launch for one decode step of one layer:
+ * batch entry b takes the raw qkv row qkv_dev[b] at position pos[b] of slot
+ * slots[b], appends its roped K and raw V at pos[b], and attends keys
+ * 0..pos[b].  Replaces the Extract + Gqa blocks of encode_into
+ * (decoder.rs:1813-1829) and of BatchProjections::step (decoder.rs:3412-3451). */
+int qasr_decode_step(qasr_ctx* ctx, qasr_kv* kv, int layer, int batch, const int32_t* slots,
+                     const int32_t* pos, const void* qkv_dev, const void* q_gain_dev,
+                     const void* k_gain_dev, void* out_dev, void* stream);
+
+/* Stage (c): causal prefill attention of s rows at positions kv_start ..
+ * kv_start+s-1 of one slot, against cache rows 0..kv_start+s-1 (rows written
+ * by stage (a) beforehand).  q_dev [s][nqh*hd] roped, out_dev [s][nqh*hd].
+ * kv_start > 0 is chunked prefill / KV-prefix reuse (stream.rs:366-376).
+ * Replaces repeat_kv + prefill_gemm_causal + softmax_causal +
+ * prefill_gemm_causal_av and the slab path (decoder.rs:4856-5098,
+ * 3860-4005; shaders.rs:3058-4184). */
+int qasr_prefill_attn(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, int s,
+                      const void* q_dev, void* out_dev, void* stream);
+
+/* Stages (a)+(c) for one layer of one slot's prefill: stage (a) on s raw qkv
+ * rows (q_work_dev receives the roped Q, [s][nqh*hd]), then stage (c).
+ * Replaces prefill_impl's attention block (decoder.rs:4856-5098). */
+int qasr_prefill_layer(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, int s,
+                       const void* qkv_dev, const void* q_gain_dev, const void* k_gain_dev,
+                       void* q_work_dev, void* out_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QASR_ATTN_H */

@@ -1,0 +1,110 @@
+// kernels.hpp -- launch-plan structs and launchers shared by the C ABI
+// (qasr_attn.hip) and the kernel translation units.
+#pragma once
+
+#include "common.hpp"
+
+namespace qasr {
+
+// Where one KV pool lives: element (slot, layer, kv, head, pos, d) is at
+// base + slot*slot_stride + layer*layer_stride + kv*kv_stride + head*head_stride
+//      + pos*kHeadDim + d.
+struct CacheGeom {
+    f16* base;
+    int64_t slot_stride;
+    int64_t layer_stride;
+    int64_t kv_stride;
+    int64_t head_stride;
+    int32_t nkvh;
+    int32_t cap;
+};
+
+// Stage (a) plan: up to kMaxBatch segments of consecutive rows.
+struct SegPlan {
+    int32_t nseg;
+    int32_t nqh;
+    float eps;
+    int32_t slot[kMaxBatch];
+    int32_t pos0[kMaxBatch];
+    int32_t row_base[kMaxBatch + 1];  // prefix sum of rows; row_base[nseg] = total
+};
+
+// Stage (b) plan: one workgroup per (batch entry, kv head, chunk of keys).
+// Workgroups of entry b are wg_base[b] .. wg_base[b+1]-1, kv-head major.
+struct DecodePlan {
+    int32_t batch;
+    int32_t chunk;  // keys per workgroup, multiple of kDecodeWgKeys
+    int32_t nqh;
+    float scale_log2;  // softmax scale * log2(e): scores live in the exp2 domain
+    float eps;
+    int32_t slot[kMaxBatch];
+    int32_t len[kMaxBatch];  // keys attended; the fused step appends key len-1
+    int32_t wg_base[kMaxBatch + 1];
+};
+
+constexpr int kDecodeWaves = 4;
+constexpr int kDecodeTileKeys = 32;                           // keys per wave pass
+constexpr int kDecodeWgKeys = kDecodeWaves * kDecodeTileKeys;  // 128
+
+// Split-K workspace of one launch: per workgroup the unnormalised partial
+// output of both q heads (2 x 128 f32) and (max, sum) per head, plus one
+// arrival counter per (batch entry, kv head).  Counters start at zero and the
+// merging workgroup puts them back to zero.
+struct DecodeWs {
+    float* acc;         // [items][2][128]
+    float* ml;          // [items][4]: m0, m1, l0, l1
+    uint32_t* counters; // [kMaxBatch * nkvh]
+    int64_t items;
+};
+
+hipError_t launch_norm_rope_append(const CacheGeom& g, int layer, const SegPlan& P,
+                                   const f16* qkv, const f16* q_gain, const f16* k_gain,
+                                   const f16* cos_tab, const f16* sin_tab, f16* q_out,
+                                   hipStream_t stream);
+
+hipError_t launch_decode_attn(bool fused, const CacheGeom& g, int layer, const DecodePlan& P,
+                              int total_wgs, const f16* q_or_qkv, const f16* q_gain,
+                              const f16* k_gain, const f16* cos_tab, const f16* sin_tab,
+                              f16* out, const DecodeWs& ws, hipStream_t stream);
+
+struct PrefillArgs {
+    const f16* q;   // [s][nqh*128], roped
+    f16* out;       // [s][nqh*128]
+    const f16* k;   // K block of (slot, layer): [nkvh][cap][128]
+    const f16* v;   // V block
+    int64_t head_stride;
+    int32_t nqh;
+    int32_t nkvh;
+    int32_t s;
+    int32_t kv_start;
+    float scale_log2;
+};
+
+// Stage (c) plan: row blocks of 64 rows; row block rb's key tiles (64 keys)
+// are split into ceil(tiles / tps) pieces.  Items of a kv head are laid out
+// rb-major: item = kvh*items_per_kvh + sp_base[rb] + split.
+constexpr int kMaxRowBlocks = 64;  // 4096 rows per launch
+constexpr int kPrefillRows = 64;
+struct PrefillPlan {
+    int32_t nrb;
+    int32_t tps;
+    int32_t items_per_kvh;
+    int32_t sp_base[kMaxRowBlocks + 1];
+};
+
+// Split workspace: per item 4 waves x 32 rows of (unnormalised O[128], m, l);
+// one counter per (kv head, row block), zero at rest.
+struct PrefillWs {
+    float* o;
+    float* ml;
+    uint32_t* counters;  // [nkvh * kMaxRowBlocks]
+    int64_t items;
+};
+constexpr int64_t kPrefillItemFloats = 4 * 32 * kHeadDim;
+constexpr int64_t kPrefillItemMl = 4 * 32 * 2;
+
+PrefillPlan plan_prefill(int s, int kv_start, int nkvh, int tiles_per_split);
+hipError_t launch_prefill_attn(const PrefillArgs& a, const PrefillPlan& P, const PrefillWs& ws,
+                               hipStream_t stream);
+
+}  // namespace qasr

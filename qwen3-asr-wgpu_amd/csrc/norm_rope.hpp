@@ -1,0 +1,46 @@
+// norm_rope.hpp -- per-head q/k RMSNorm + rotate-half RoPE, bit-identical to
+// the reference CPU decoder's norm_rope_head (src/cpu_decoder.rs:274-290).
+//
+// Every float operation is written in the reference's order with contraction
+// off, so each product and sum rounds exactly once, as in Rust:
+//   sum2 = sequential sum over j of x_j*x_j            (277-281)
+//   inv  = 1 / sqrt(sum2 / hd + eps)                   (282, IEEE div + sqrt)
+//   xj   = (x_j * inv) * g_j ; xp = (x_pj * inv) * g_pj (284, 286)
+//   out  = f16(xj*c_j + sign*xp*s_j)                   (288, RNE)
+// HIP's default -fhip-fp32-correctly-rounded-divide-sqrt makes '/' and sqrtf
+// correctly rounded; v_cvt_f16_f32 rounds to nearest even.
+#pragma once
+
+#include "common.hpp"
+
+namespace qasr {
+
+// The one serial chain of the stage: 128 dependent adds in ascending j.  Each
+// f16 square is exact in f32, so only the adds round -- in the reference's order.
+__device__ __forceinline__ float head_inv_rms_serial(const f16* raw, float eps) {
+#pragma clang fp contract(off)
+    float sum2 = 0.0f;
+#pragma unroll 16
+    for (int j = 0; j < kHeadDim; ++j) {
+        float f = h2f(raw[j]);
+        sum2 += f * f;
+    }
+    return 1.0f / sqrtf(sum2 / (float)kHeadDim + eps);
+}
+
+// One roped element j of a head whose raw values, gains and cos/sin rows are
+// given (all f16).  `inv` is the head's inverse RMS.
+__device__ __forceinline__ f16 rope_elem(const f16* raw, const f16* gain, const f16* cos_row,
+                                         const f16* sin_row, float inv, int j) {
+#pragma clang fp contract(off)
+    constexpr int half = kHeadDim / 2;
+    const int pj = j < half ? j + half : j - half;
+    const float xj = (h2f(raw[j]) * inv) * h2f(gain[j]);
+    const float xp = (h2f(raw[pj]) * inv) * h2f(gain[pj]);
+    const float a = xj * h2f(cos_row[j]);
+    const float b = xp * h2f(sin_row[j]);
+    // sign * xp * s with sign = -1 for j < half: (-xp)*s == -(xp*s) exactly.
+    return f2h(j < half ? a - b : a + b);
+}
+
+}  // namespace qasr

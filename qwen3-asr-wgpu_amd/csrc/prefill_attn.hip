@@ -1,0 +1,295 @@
+// prefill_attn.hip -- stage (c): causal GQA prefill attention on fp16 MFMA
+// (v_mfma_f32_32x32x16_f16, gfx950) with online softmax, for s rows at
+// positions kv_start.. against cache rows 0..kv_start+s-1 (chunked prefill /
+// KV-prefix reuse when kv_start > 0).
+//
+// Replaces the reference's repeat_kv -> prefill_gemm_causal -> softmax_causal
+// -> prefill_gemm_causal_av pipeline and its slab variant (src/shaders.rs:
+// 3058-4184, orchestrated in src/decoder.rs:4856-5098): no K/V expansion, no
+// f16 score or probability matrix in memory.  Semantics: src/cpu_decoder.rs:
+// 292-365 with rows = s, q0 = kv_start.
+//
+// Work item = (kv head, block of 64 query rows, split of the key range).
+// 4 waves: wave w takes q head 2*kvh + (w&1) and rows (w>>1)*32..+32 of the
+// block, so both q heads of a kv head share each K/V tile staged in LDS.
+// Each wave computes S^T = K Q^T (keys on the MFMA M axis, queries on N), so a
+// lane owns one query column: row max / row sum need one cross-half shuffle,
+// and the probabilities are already in the B-operand layout of O^T += V^T P^T.
+// V is transposed into LDS ([dim][key]) while it is staged.
+// When the key range of a row block is split, each item writes its partial
+// (max, sum, unnormalised O) and the last to arrive merges (agent-scope
+// ticket), as in the decode kernel.
+
+#include "kernels.hpp"
+
+#include <algorithm>
+
+namespace qasr {
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kRowsPerBlock = 64;
+constexpr int kTileKeys = 64;
+constexpr int kKPad = kHeadDim + 8;     // Ks row stride (halves)
+constexpr int kVPad = kTileKeys + 8;    // Vt row stride (halves)
+constexpr float kNegInf = -__builtin_inff();
+
+__device__ __forceinline__ float16v mfma32(const half8v& a, const half8v& b, const float16v& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(kWaves * 64, 2) void prefill_attn_kernel(
+    PrefillArgs a, PrefillPlan P, float* __restrict__ ws_o, float* __restrict__ ws_ml,
+    uint32_t* __restrict__ counters) {
+    __shared__ __attribute__((aligned(16))) f16 Ks[kTileKeys * kKPad];
+    __shared__ __attribute__((aligned(16))) f16 Vt[kHeadDim * kVPad];
+    __shared__ int s_last;
+
+    const int item = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n = lane & 31;  // query column within the wave's 32 rows
+    const int g = lane >> 5;  // k-slot group of the MFMA operands
+
+    const int kvh = item / P.items_per_kvh;
+    const int rem = item - kvh * P.items_per_kvh;
+    int rb = 0;
+    {
+        int lo = 0, hi = P.nrb - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (P.sp_base[mid] <= rem) lo = mid; else hi = mid - 1;
+        }
+        rb = lo;
+    }
+    const int sp = rem - P.sp_base[rb];
+    const int nsp = P.sp_base[rb + 1] - P.sp_base[rb];
+    const int row0 = rb * kRowsPerBlock;
+    const int kend = a.kv_start + min(row0 + kRowsPerBlock, a.s);
+    const int ntiles = (kend + kTileKeys - 1) / kTileKeys;
+    const int t_begin = sp * P.tps;
+    const int t_end = min(t_begin + P.tps, ntiles);
+
+    const int hh = wave & 1;
+    const int head = kvh * kRep + hh;
+    const int r = row0 + (wave >> 1) * 32 + n;  // this lane's query row
+    const bool row_ok = r < a.s;
+    const int qpos = a.kv_start + r;
+    const int ldq = a.nqh * kHeadDim;
+
+    // Q^T as B operand: k-step ks covers dims ks*16 + g*8 .. +8.
+    half8v qb[8];
+    {
+        const f16* qrow = a.q + (int64_t)(row_ok ? r : 0) * ldq + head * kHeadDim + g * 8;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            H8 t;
+            t.u = row_ok ? *(const uint4*)(qrow + ks * 16) : make_uint4(0, 0, 0, 0);
+            qb[ks] = t.h;
+        }
+    }
+
+    const f16* Kg = a.k + kvh * a.head_stride;
+    const f16* Vg = a.v + kvh * a.head_stride;
+    float m = kNegInf, lsum = 0.0f;
+    float16v o[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db] = (float16v){};
+
+    for (int t = t_begin; t < t_end; ++t) {
+        const int k0 = t * kTileKeys;
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int idx = c * (kWaves * 64) + tid;
+            const int key = idx >> 4, dseg = (idx & 15) * 8;
+            const int gk = k0 + key;
+            H8 kv, vv;
+            if (gk < kend) {
+                kv.u = *(const uint4*)(Kg + (int64_t)gk * kHeadDim + dseg);
+                vv.u = *(const uint4*)(Vg + (int64_t)gk * kHeadDim + dseg);
+            } else {
+                kv.u = make_uint4(0, 0, 0, 0);
+                vv.u = make_uint4(0, 0, 0, 0);
+            }
+            *(uint4*)&Ks[key * kKPad + dseg] = kv.u;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) Vt[(dseg + e) * kVPad + key] = vv.e[e];
+        }
+        __syncthreads();
+
+        // S^T: keys kb*32 + (8*(i/4) + 4*g + i%4) x query n, accumulated over dims.
+        float16v st[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            st[kb] = (float16v){};
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                const half8v ka = *(const half8v*)&Ks[(kb * 32 + n) * kKPad + ks * 16 + g * 8];
+                st[kb] = mfma32(ka, qb[ks], st[kb]);
+            }
+        }
+        float mx = kNegInf;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = k0 + kb * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+                float v = st[kb][i] * a.scale_log2;
+                if (key > qpos) v = kNegInf;
+                st[kb][i] = v;
+                mx = fmaxf(mx, v);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        const float mu = mn == kNegInf ? 0.0f : mn;
+        const float alpha = fast_exp2(m - mu);
+        m = mn;
+        float ps = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const float p = fast_exp2(st[kb][i] - mu);
+                st[kb][i] = p;
+                ps += p;
+            }
+        }
+        ps += __shfl_xor(ps, 32);
+        lsum = lsum * alpha + ps;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[db] *= alpha;
+
+        // O^T += V^T P^T; k-step w4 covers tile keys 16*w4 + 4*g + {0..3, 8..11}.
+#pragma unroll
+        for (int w4 = 0; w4 < 4; ++w4) {
+            half8v pb;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pb[j] = (f16)st[w4 >> 1][8 * (w4 & 1) + j];
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const f16* vrow = &Vt[(db * 32 + n) * kVPad + 16 * w4 + 4 * g];
+                const half4v lo = *(const half4v*)vrow;
+                const half4v hi = *(const half4v*)(vrow + 8);
+                const half8v va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                o[db] = mfma32(va, pb, o[db]);
+            }
+        }
+    }
+
+    // o[db][i] holds dim db*32 + 8*(i/4) + 4*g + i%4 of query row r.
+    f16* orow = a.out + (int64_t)r * ldq + head * kHeadDim;
+    if (nsp == 1) {
+        if (row_ok) {
+            const float inv = 1.0f / lsum;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    half4v h4;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) h4[e] = (f16)(o[db][q4 * 4 + e] * inv);
+                    *(half4v*)(orow + db * 32 + 8 * q4 + 4 * g) = h4;
+                }
+            }
+        }
+        return;
+    }
+
+    // Partial: [item][wave][n][128] unnormalised O, [item][wave][n] (m, l).
+    const int64_t slot_id = ((int64_t)item * kWaves + wave) * 32 + n;
+    float* po = ws_o + slot_id * kHeadDim;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4)
+            *(float4v*)(po + db * 32 + 8 * q4 + 4 * g) =
+                (float4v){o[db][q4 * 4], o[db][q4 * 4 + 1], o[db][q4 * 4 + 2], o[db][q4 * 4 + 3]};
+    if (g == 0) {
+        ws_ml[slot_id * 2] = m;
+        ws_ml[slot_id * 2 + 1] = lsum;
+    }
+    __threadfence();
+    __syncthreads();
+    uint32_t* ctr = &counters[kvh * P.nrb + rb];
+    if (tid == 0) {
+        const uint32_t prev =
+            __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (prev == (uint32_t)(nsp - 1));
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    const int it0 = kvh * P.items_per_kvh + P.sp_base[rb];
+    float M = kNegInf;
+    for (int i = 0; i < nsp; ++i)
+        M = fmaxf(M, ws_ml[(((int64_t)(it0 + i) * kWaves + wave) * 32 + n) * 2]);
+    float Ls = 0.0f;
+    float acc[4][16];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[db][e] = 0.0f;
+    for (int i = 0; i < nsp; ++i) {
+        const int64_t sid = ((int64_t)(it0 + i) * kWaves + wave) * 32 + n;
+        const float mi = ws_ml[sid * 2];
+        const float w = mi == kNegInf ? 0.0f : fast_exp2(mi - M);
+        Ls = fmaf(ws_ml[sid * 2 + 1], w, Ls);
+        const float* pi = ws_o + sid * kHeadDim;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4v v = *(const float4v*)(pi + db * 32 + 8 * q4 + 4 * g);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[db][q4 * 4 + e] = fmaf(v[e], w, acc[db][q4 * 4 + e]);
+            }
+    }
+    if (row_ok) {
+        const float inv = 1.0f / Ls;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                half4v h4;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) h4[e] = (f16)(acc[db][q4 * 4 + e] * inv);
+                *(half4v*)(orow + db * 32 + 8 * q4 + 4 * g) = h4;
+            }
+    }
+    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace
+
+
+
+PrefillPlan plan_prefill(int s, int kv_start, int nkvh, int tiles_per_split) {
+    PrefillPlan P{};
+    P.nrb = (s + kRowsPerBlock - 1) / kRowsPerBlock;
+    P.tps = tiles_per_split;
+    P.sp_base[0] = 0;
+    for (int rb = 0; rb < P.nrb; ++rb) {
+        const int kend = kv_start + std::min((rb + 1) * kRowsPerBlock, s);
+        const int ntiles = (kend + kTileKeys - 1) / kTileKeys;
+        P.sp_base[rb + 1] = P.sp_base[rb] + (ntiles + P.tps - 1) / P.tps;
+    }
+    P.items_per_kvh = P.sp_base[P.nrb];
+    (void)nkvh;
+    return P;
+}
+
+hipError_t launch_prefill_attn(const PrefillArgs& a, const PrefillPlan& P, const PrefillWs& ws,
+                               hipStream_t stream) {
+    const int items = P.items_per_kvh * a.nkvh;
+    if (items <= 0) return hipSuccess;
+    if (items > ws.items || P.nrb > kMaxRowBlocks) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(prefill_attn_kernel, dim3(items), dim3(kWaves * 64), 0, stream, a, P, ws.o,
+                       ws.ml, ws.counters);
+    return hipGetLastError();
+}
+
+}  // namespace qasr

@@ -1,0 +1,670 @@
+// qasr_attn.hip -- the C ABI (include/qasr_attn.h): contexts, KV pools, RoPE
+// tables, argument checking, launch planning and dispatch of the stage (a),
+// (b) and (c) kernels.
+//
+// Host-side mirror of the reference's attention plumbing inside
+// WgpuTextDecoder (src/decoder.rs): load-time buffers (977-1246),
+// ensure_capacity (1604-1661), set_rope_tables (1664-1667), per-step planning
+// (1674-1714, 1932-2025, 3348-3451) and the prefill attention block
+// (4856-5098).  Errors follow the reference's bounds checks
+// (src/cpu_decoder.rs:489-495, 520; src/decoder.rs:4500-4530) but come back as
+// status codes.
+
+#include "qasr_attn.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+
+using qasr::f16;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(e == hipErrorOutOfMemory ? QASR_ENOMEM : QASR_EDEVICE, "%s: %s", what,
+                hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                     \
+    do {                                        \
+        hipError_t e_ = (expr);                 \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+// Makes `dev` current for the scope of an ABI call and restores the caller's.
+struct DeviceScope {
+    int prev = -1;
+    hipError_t err = hipSuccess;
+    explicit DeviceScope(int dev) {
+        err = hipGetDevice(&prev);
+        if (err == hipSuccess && prev != dev) err = hipSetDevice(dev);
+    }
+    ~DeviceScope() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+// f32 -> IEEE binary16 bits, round to nearest even, subnormals kept: the
+// conversion of half::f16::from_f32 (inference.rs:1046-1047).  Written out on
+// the bit level because the host pass's _Float16 cast is not RNE-exact.
+uint16_t f16_bits(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
+    if (ax >= 0x47800000u) return (uint16_t)(sign | 0x7c00u);
+    const int e = (int)(ax >> 23) - 127;
+    uint32_t m = ax & 0x7fffffu;
+    if (e >= -14) {
+        uint32_t h = ((uint32_t)(e + 15) << 10) | (m >> 13);
+        const uint32_t rem = m & 0x1fffu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;
+        return (uint16_t)(sign | h);
+    }
+    if (e < -25) return sign;
+    m |= 0x800000u;
+    const int shift = -e - 1;
+    uint32_t h = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1u), halfway = 1u << (shift - 1);
+    if (rem > halfway || (rem == halfway && (h & 1u))) ++h;
+    return (uint16_t)(sign | h);
+}
+
+int env_int(const char* name, int dflt) {
+    const char* v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    return std::atoi(v);
+}
+
+}  // namespace
+
+struct qasr_ctx {
+    qasr_attn_cfg cfg;
+    int device;
+    f16* cos = nullptr;
+    f16* sin = nullptr;
+    int rope_rows = 0;
+    float scale_log2;
+};
+
+struct qasr_kv {
+    qasr_ctx* ctx;
+    int slots;
+    int cap;
+    f16* base = nullptr;
+    size_t bytes = 0;
+    // decode split-K workspace
+    float* dws_acc = nullptr;
+    float* dws_ml = nullptr;
+    uint32_t* dws_ctr = nullptr;
+    int64_t dws_items = 0;
+    // prefill split workspace (grown on demand)
+    float* pws_o = nullptr;
+    float* pws_ml = nullptr;
+    uint32_t* pws_ctr = nullptr;
+    int64_t pws_items = 0;
+};
+
+namespace {
+
+qasr::CacheGeom geom(const qasr_kv* kv) {
+    const qasr_attn_cfg& c = kv->ctx->cfg;
+    qasr::CacheGeom g;
+    g.base = kv->base;
+    g.head_stride = (int64_t)kv->cap * qasr::kHeadDim;
+    g.kv_stride = g.head_stride * c.num_key_value_heads;
+    g.layer_stride = 2 * g.kv_stride;
+    g.slot_stride = g.layer_stride * c.num_hidden_layers;
+    g.nkvh = c.num_key_value_heads;
+    g.cap = kv->cap;
+    return g;
+}
+
+int target_cap(int need, int cap, int max_seq) {
+    int64_t t = ((int64_t)need + QASR_KV_STEP - 1) / QASR_KV_STEP * QASR_KV_STEP;
+    t = std::min<int64_t>(t, max_seq);
+    t = std::max<int64_t>(t, cap);
+    return (int)t;
+}
+
+void free_decode_ws(qasr_kv* kv) {
+    if (kv->dws_acc) (void)hipFree(kv->dws_acc);
+    if (kv->dws_ml) (void)hipFree(kv->dws_ml);
+    if (kv->dws_ctr) (void)hipFree(kv->dws_ctr);
+    kv->dws_acc = kv->dws_ml = nullptr;
+    kv->dws_ctr = nullptr;
+    kv->dws_items = 0;
+}
+
+void free_prefill_ws(qasr_kv* kv) {
+    if (kv->pws_o) (void)hipFree(kv->pws_o);
+    if (kv->pws_ml) (void)hipFree(kv->pws_ml);
+    if (kv->pws_ctr) (void)hipFree(kv->pws_ctr);
+    kv->pws_o = kv->pws_ml = nullptr;
+    kv->pws_ctr = nullptr;
+    kv->pws_items = 0;
+}
+
+// Decode workspace: every launch plans at most kMaxBatch entries with chunks of
+// >= 128 keys over <= cap keys.
+int alloc_decode_ws(qasr_kv* kv) {
+    const int nkvh = kv->ctx->cfg.num_key_value_heads;
+    const int64_t items = (int64_t)std::min(kv->slots, qasr::kMaxBatch) * nkvh *
+                          ((kv->cap + qasr::kDecodeWgKeys - 1) / qasr::kDecodeWgKeys);
+    HIP_TRY(hipMalloc(&kv->dws_acc, items * 2 * qasr::kHeadDim * sizeof(float)), "decode workspace");
+    HIP_TRY(hipMalloc(&kv->dws_ml, items * 4 * sizeof(float)), "decode workspace");
+    const size_t cbytes = (size_t)qasr::kMaxBatch * nkvh * sizeof(uint32_t);
+    HIP_TRY(hipMalloc(&kv->dws_ctr, cbytes), "decode counters");
+    HIP_TRY(hipMemset(kv->dws_ctr, 0, cbytes), "decode counters");
+    kv->dws_items = items;
+    return QASR_OK;
+}
+
+int ensure_prefill_ws(qasr_kv* kv, int64_t items) {
+    if (items <= kv->pws_items) return QASR_OK;
+    HIP_TRY(hipDeviceSynchronize(), "prefill workspace sync");
+    free_prefill_ws(kv);
+    const int nkvh = kv->ctx->cfg.num_key_value_heads;
+    HIP_TRY(hipMalloc(&kv->pws_o, items * qasr::kPrefillItemFloats * sizeof(float)),
+            "prefill workspace");
+    HIP_TRY(hipMalloc(&kv->pws_ml, items * qasr::kPrefillItemMl * sizeof(float)),
+            "prefill workspace");
+    const size_t cbytes = (size_t)nkvh * qasr::kMaxRowBlocks * sizeof(uint32_t);
+    HIP_TRY(hipMalloc(&kv->pws_ctr, cbytes), "prefill counters");
+    HIP_TRY(hipMemset(kv->pws_ctr, 0, cbytes), "prefill counters");
+    kv->pws_items = items;
+    return QASR_OK;
+}
+
+// Keys per decode workgroup: the largest power-of-two multiple of 128 that
+// still leaves >= kDecodeMinWgs workgroups, so that short batches spread over
+// all 256 CUs and long ones avoid merge traffic.
+int pick_decode_chunk(const int32_t* len, int n, int nkvh) {
+    const int forced = env_int("QASR_DECODE_CHUNK", 0);
+    if (forced >= qasr::kDecodeWgKeys && forced % qasr::kDecodeWgKeys == 0) return forced;
+    const int64_t min_wgs = env_int("QASR_DECODE_MIN_WGS", 2048);
+    auto wgs = [&](int chunk) {
+        int64_t t = 0;
+        for (int i = 0; i < n; ++i) t += (int64_t)nkvh * ((len[i] + chunk - 1) / chunk);
+        return t;
+    };
+    int chunk = qasr::kDecodeWgKeys;
+    while (chunk < 2048 && wgs(chunk * 2) >= min_wgs) chunk *= 2;
+    return chunk;
+}
+
+int check_common(qasr_ctx* ctx, qasr_kv* kv, int layer) {
+    if (!ctx || !kv) return fail(QASR_EINVAL, "null context or KV pool");
+    if (kv->ctx != ctx) return fail(QASR_EINVAL, "KV pool belongs to another context");
+    if (layer < 0 || layer >= ctx->cfg.num_hidden_layers)
+        return fail(QASR_EINVAL, "layer %d outside [0, %d)", layer, ctx->cfg.num_hidden_layers);
+    return QASR_OK;
+}
+
+int run_decode(bool fused, qasr_ctx* ctx, qasr_kv* kv, int layer, int batch, const int32_t* slots,
+               const int32_t* lens, const void* qin, const void* q_gain, const void* k_gain,
+               void* out, void* stream) {
+    const qasr_attn_cfg& c = ctx->cfg;
+    const int nqh = c.num_attention_heads, nkvh = c.num_key_value_heads;
+    const int64_t in_row = fused ? (int64_t)(nqh + 2 * nkvh) * qasr::kHeadDim
+                                 : (int64_t)nqh * qasr::kHeadDim;
+    const int64_t out_row = (int64_t)nqh * qasr::kHeadDim;
+    const qasr::CacheGeom g = geom(kv);
+    qasr::DecodeWs ws{kv->dws_acc, kv->dws_ml, kv->dws_ctr, kv->dws_items};
+    for (int b0 = 0; b0 < batch; b0 += qasr::kMaxBatch) {
+        const int nb = std::min(qasr::kMaxBatch, batch - b0);
+        qasr::DecodePlan P{};
+        P.batch = nb;
+        P.nqh = nqh;
+        P.eps = c.rms_norm_eps;
+        P.scale_log2 = ctx->scale_log2;
+        for (int i = 0; i < nb; ++i) {
+            P.slot[i] = slots ? slots[b0 + i] : b0 + i;
+            P.len[i] = lens[b0 + i];
+        }
+        P.chunk = pick_decode_chunk(P.len, nb, nkvh);
+        P.wg_base[0] = 0;
+        for (int i = 0; i < nb; ++i)
+            P.wg_base[i + 1] = P.wg_base[i] + nkvh * ((P.len[i] + P.chunk - 1) / P.chunk);
+        const f16* qp = (const f16*)qin + b0 * in_row;
+        f16* op = (f16*)out + b0 * out_row;
+        hipError_t e = qasr::launch_decode_attn(fused, g, layer, P, P.wg_base[nb], qp,
+                                                (const f16*)q_gain, (const f16*)k_gain, ctx->cos,
+                                                ctx->sin, op, ws, (hipStream_t)stream);
+        if (e != hipSuccess) return hip_fail(e, "decode attention launch");
+    }
+    return QASR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qasr_abi_version(void) { return QASR_ABI_VERSION; }
+
+const char* qasr_last_error(void) { return g_err.c_str(); }
+
+int qasr_ctx_create(const qasr_attn_cfg* cfg, int device, qasr_ctx** out) {
+    if (!cfg || !out) return fail(QASR_EINVAL, "null argument");
+    *out = nullptr;
+    const qasr_attn_cfg& c = *cfg;
+    if (c.head_dim != qasr::kHeadDim)
+        return fail(QASR_EINVAL, "head_dim %d unsupported (this build is specialised for 128)",
+                    c.head_dim);
+    if (c.num_key_value_heads <= 0 || c.num_attention_heads != qasr::kRep * c.num_key_value_heads)
+        return fail(QASR_EINVAL, "%d q heads / %d kv heads: the kernels need exactly 2 q heads per "
+                    "kv head", c.num_attention_heads, c.num_key_value_heads);
+    if (c.num_attention_heads + c.num_key_value_heads > 48)
+        return fail(QASR_EINVAL, "too many heads (%d + %d)", c.num_attention_heads,
+                    c.num_key_value_heads);
+    if (c.num_hidden_layers <= 0) return fail(QASR_EINVAL, "num_hidden_layers must be > 0");
+    if (c.max_seq <= 0) return fail(QASR_EINVAL, "max_seq must be > 0");
+    if (!(c.rms_norm_eps >= 0.0f) || !std::isfinite(c.rms_norm_eps))
+        return fail(QASR_EINVAL, "rms_norm_eps must be finite and >= 0");
+    int ndev = 0;
+    HIP_TRY(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
+    if (device < 0 || device >= ndev)
+        return fail(QASR_EINVAL, "device %d outside [0, %d)", device, ndev);
+    qasr_ctx* ctx = new qasr_ctx();
+    ctx->cfg = c;
+    ctx->device = device;
+    // scale = 1/sqrt(hd) in f32 (decoder.rs:204-206), folded with log2(e) so the
+    // kernels exponentiate with exp2.
+    const float scale = 1.0f / std::sqrt((float)c.head_dim);
+    ctx->scale_log2 = (float)((double)scale * 1.4426950408889634073599246810019);
+    *out = ctx;
+    return QASR_OK;
+}
+
+void qasr_ctx_destroy(qasr_ctx* ctx) {
+    if (!ctx) return;
+    DeviceScope ds(ctx->device);
+    if (ctx->cos) (void)hipFree(ctx->cos);
+    if (ctx->sin) (void)hipFree(ctx->sin);
+    delete ctx;
+}
+
+int qasr_mrope_text_tables(int rows, int head_dim, double rope_theta,
+                           const int32_t* mrope_section, int nsec, int interleaved,
+                           uint16_t* cos_f16, uint16_t* sin_f16) {
+    if (rows < 0 || head_dim <= 0 || head_dim % 2 || !cos_f16 || !sin_f16 || !mrope_section ||
+        nsec <= 0)
+        return fail(QASR_EINVAL, "bad table arguments");
+    const int half = head_dim / 2;
+    // build_dim_map (mrope.rs:5-41): axis per frequency.
+    std::vector<int> dm;
+    if (interleaved) {
+        std::vector<int> used(nsec, 0);
+        while ((int)dm.size() < half) {
+            const size_t before = dm.size();
+            for (int d = 0; d < nsec && (int)dm.size() < half; ++d)
+                if (used[d] < mrope_section[d]) {
+                    dm.push_back(d);
+                    ++used[d];
+                }
+            if (dm.size() == before) break;
+        }
+    } else {
+        for (int d = 0; d < nsec; ++d)
+            for (int i = 0; i < mrope_section[d] && (int)dm.size() < half; ++i) dm.push_back(d);
+        while ((int)dm.size() < half) dm.push_back(nsec - 1);
+    }
+    if ((int)dm.size() != half) return fail(QASR_EINVAL, "mrope_section quotas cover fewer than %d "
+                                            "frequencies", half);
+    for (int d : dm)
+        if (d > 2) return fail(QASR_EINVAL, "mrope_section has more than 3 axes");
+    // Text positions put the same t on all three axes (mrope.rs:77-80), so
+    // angle = t * theta^(-2j/hd) whatever the axis map; f64 -> f32 -> f16 RNE
+    // (mrope.rs:55-71, inference.rs:1046-1047).
+    std::vector<double> inv(half);
+    for (int j = 0; j < half; ++j) inv[j] = 1.0 / std::pow(rope_theta, 2.0 * j / (double)head_dim);
+    for (int t = 0; t < rows; ++t) {
+        for (int j = 0; j < half; ++j) {
+            const double angle = (double)t * inv[j];
+            const uint16_t cb = f16_bits((float)std::cos(angle));
+            const uint16_t sb = f16_bits((float)std::sin(angle));
+            const int64_t o = (int64_t)t * head_dim + j;
+            cos_f16[o] = cos_f16[o + half] = cb;
+            sin_f16[o] = sin_f16[o + half] = sb;
+        }
+    }
+    return QASR_OK;
+}
+
+int qasr_set_rope_tables(qasr_ctx* ctx, const uint16_t* cos_f16, const uint16_t* sin_f16,
+                         int rows) {
+    if (!ctx || !cos_f16 || !sin_f16 || rows <= 0) return fail(QASR_EINVAL, "bad table arguments");
+    DeviceScope ds(ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    const size_t bytes = (size_t)rows * ctx->cfg.head_dim * sizeof(uint16_t);
+    if (ctx->cos) (void)hipFree(ctx->cos);
+    if (ctx->sin) (void)hipFree(ctx->sin);
+    ctx->cos = ctx->sin = nullptr;
+    ctx->rope_rows = 0;
+    HIP_TRY(hipMalloc(&ctx->cos, bytes), "rope tables");
+    HIP_TRY(hipMalloc(&ctx->sin, bytes), "rope tables");
+    HIP_TRY(hipMemcpy(ctx->cos, cos_f16, bytes, hipMemcpyHostToDevice), "rope upload");
+    HIP_TRY(hipMemcpy(ctx->sin, sin_f16, bytes, hipMemcpyHostToDevice), "rope upload");
+    ctx->rope_rows = rows;
+    return QASR_OK;
+}
+
+int qasr_kv_create(qasr_ctx* ctx, int slots, int cap, qasr_kv** out) {
+    if (!ctx || !out) return fail(QASR_EINVAL, "null argument");
+    *out = nullptr;
+    if (slots <= 0) return fail(QASR_EINVAL, "slots must be > 0");
+    if (cap <= 0) return fail(QASR_EINVAL, "cap must be > 0");
+    DeviceScope ds(ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    qasr_kv* kv = new qasr_kv();
+    kv->ctx = ctx;
+    kv->slots = slots;
+    kv->cap = target_cap(cap, 0, ctx->cfg.max_seq);
+    const qasr::CacheGeom g = geom(kv);
+    kv->bytes = (size_t)g.slot_stride * slots * sizeof(f16);
+    hipError_t e = hipMalloc(&kv->base, kv->bytes);
+    if (e == hipSuccess) e = hipMemset(kv->base, 0, kv->bytes);
+    if (e != hipSuccess) {
+        if (kv->base) (void)hipFree(kv->base);
+        delete kv;
+        return hip_fail(e, "KV pool allocation");
+    }
+    int rc = alloc_decode_ws(kv);
+    if (rc != QASR_OK) {
+        qasr_kv_destroy(kv);
+        return rc;
+    }
+    *out = kv;
+    return QASR_OK;
+}
+
+void qasr_kv_destroy(qasr_kv* kv) {
+    if (!kv) return;
+    DeviceScope ds(kv->ctx->device);
+    (void)hipDeviceSynchronize();
+    if (kv->base) (void)hipFree(kv->base);
+    free_decode_ws(kv);
+    free_prefill_ws(kv);
+    delete kv;
+}
+
+int qasr_kv_get_info(const qasr_kv* kv, qasr_kv_info* out) {
+    if (!kv || !out) return fail(QASR_EINVAL, "null argument");
+    const qasr::CacheGeom g = geom(kv);
+    out->base_dev = kv->base;
+    out->slots = kv->slots;
+    out->layers = kv->ctx->cfg.num_hidden_layers;
+    out->nkvh = g.nkvh;
+    out->cap = kv->cap;
+    out->head_dim = qasr::kHeadDim;
+    out->slot_stride = g.slot_stride;
+    out->layer_stride = g.layer_stride;
+    out->kv_stride = g.kv_stride;
+    out->head_stride = g.head_stride;
+    out->bytes = kv->bytes;
+    return QASR_OK;
+}
+
+int qasr_kv_ensure_capacity(qasr_kv* kv, int need, int keep_rows, int* cap_out) {
+    if (!kv) return fail(QASR_EINVAL, "null KV pool");
+    if (need < 0 || keep_rows < 0) return fail(QASR_EINVAL, "negative need / keep_rows");
+    const int target = target_cap(need, kv->cap, kv->ctx->cfg.max_seq);
+    if (target == kv->cap) {
+        if (cap_out) *cap_out = kv->cap;
+        return QASR_OK;
+    }
+    DeviceScope ds(kv->ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    const int prev = kv->cap;
+    const qasr::CacheGeom og = geom(kv);
+    qasr_kv tmp = *kv;
+    tmp.cap = target;
+    const qasr::CacheGeom ng = geom(&tmp);
+    const size_t nbytes = (size_t)ng.slot_stride * kv->slots * sizeof(f16);
+    f16* nb = nullptr;
+    HIP_TRY(hipMalloc(&nb, nbytes), "KV pool growth");
+    hipError_t e = hipMemset(nb, 0, nbytes);
+    // Keep rows 0..keep_rows-1 of every (slot, layer, K/V, head): one pitched
+    // copy, as the reference copies each head's prefix (decoder.rs:1617-1650).
+    const int rows = std::min(keep_rows, prev);
+    if (e == hipSuccess && rows > 0) {
+        const size_t height = (size_t)kv->slots * kv->ctx->cfg.num_hidden_layers * 2 * og.nkvh;
+        e = hipMemcpy2D(nb, (size_t)ng.head_stride * sizeof(f16), kv->base,
+                        (size_t)og.head_stride * sizeof(f16),
+                        (size_t)rows * qasr::kHeadDim * sizeof(f16), height,
+                        hipMemcpyDeviceToDevice);
+    }
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipFree(nb);
+        return hip_fail(e, "KV pool growth copy");
+    }
+    (void)hipFree(kv->base);
+    kv->base = nb;
+    kv->bytes = nbytes;
+    kv->cap = target;
+    free_decode_ws(kv);
+    int rc = alloc_decode_ws(kv);
+    if (rc != QASR_OK) return rc;
+    if (cap_out) *cap_out = kv->cap;
+    return QASR_OK;
+}
+
+int qasr_qk_norm_rope_append(qasr_ctx* ctx, qasr_kv* kv, int layer, const qasr_segment* segs,
+                             int nseg, const void* qkv_dev, const void* q_gain_dev,
+                             const void* k_gain_dev, void* q_out_dev, void* stream) {
+    int rc = check_common(ctx, kv, layer);
+    if (rc) return rc;
+    if (nseg < 0 || (nseg > 0 && !segs)) return fail(QASR_EINVAL, "bad segment list");
+    if (nseg == 0) return QASR_OK;
+    if (!qkv_dev || !q_gain_dev || !k_gain_dev || !q_out_dev)
+        return fail(QASR_EINVAL, "null device pointer");
+    if (!ctx->cos) return fail(QASR_ESTATE, "RoPE tables not set (qasr_set_rope_tables)");
+    for (int i = 0; i < nseg; ++i) {
+        const qasr_segment& s = segs[i];
+        if (s.slot < 0 || s.slot >= kv->slots)
+            return fail(QASR_EINVAL, "segment %d: slot %d outside [0, %d)", i, s.slot, kv->slots);
+        if (s.pos0 < 0 || s.rows < 0) return fail(QASR_EINVAL, "segment %d: negative pos/rows", i);
+        const int64_t end = (int64_t)s.pos0 + s.rows;
+        if (end > kv->cap)
+            return fail(QASR_ERANGE, "segment %d: positions up to %lld exceed KV capacity %d", i,
+                        (long long)end, kv->cap);
+        if (end > ctx->cfg.max_seq)
+            return fail(QASR_ERANGE, "segment %d: %lld positions exceed max_seq %d", i,
+                        (long long)end, ctx->cfg.max_seq);
+        if (end > ctx->rope_rows)
+            return fail(QASR_ERANGE, "segment %d: positions beyond the %d RoPE table rows", i,
+                        ctx->rope_rows);
+    }
+    DeviceScope ds(ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    const qasr_attn_cfg& c = ctx->cfg;
+    const int64_t in_row = (int64_t)(c.num_attention_heads + 2 * c.num_key_value_heads) * 128;
+    const int64_t q_row = (int64_t)c.num_attention_heads * 128;
+    const qasr::CacheGeom g = geom(kv);
+    int64_t row_off = 0;
+    for (int s0 = 0; s0 < nseg; s0 += qasr::kMaxBatch) {
+        const int ns = std::min(qasr::kMaxBatch, nseg - s0);
+        qasr::SegPlan P{};
+        P.nseg = ns;
+        P.nqh = c.num_attention_heads;
+        P.eps = c.rms_norm_eps;
+        P.row_base[0] = 0;
+        for (int i = 0; i < ns; ++i) {
+            P.slot[i] = segs[s0 + i].slot;
+            P.pos0[i] = segs[s0 + i].pos0;
+            P.row_base[i + 1] = P.row_base[i] + segs[s0 + i].rows;
+        }
+        hipError_t e = qasr::launch_norm_rope_append(
+            g, layer, P, (const f16*)qkv_dev + row_off * in_row, (const f16*)q_gain_dev,
+            (const f16*)k_gain_dev, ctx->cos, ctx->sin, (f16*)q_out_dev + row_off * q_row,
+            (hipStream_t)stream);
+        if (e != hipSuccess) return hip_fail(e, "stage (a) launch");
+        row_off += P.row_base[ns];
+    }
+    return QASR_OK;
+}
+
+static int check_batch(qasr_ctx* ctx, qasr_kv* kv, int batch, const int32_t* slots,
+                       bool distinct) {
+    if (batch < 0) return fail(QASR_EINVAL, "negative batch");
+    if (batch > kv->slots && distinct)
+        return fail(QASR_EINVAL, "batch %d larger than the pool's %d slots", batch, kv->slots);
+    if (slots) {
+        std::vector<char> seen(kv->slots, 0);
+        for (int b = 0; b < batch; ++b) {
+            if (slots[b] < 0 || slots[b] >= kv->slots)
+                return fail(QASR_EINVAL, "entry %d: slot %d outside [0, %d)", b, slots[b],
+                            kv->slots);
+            if (distinct && seen[slots[b]]++)
+                return fail(QASR_EINVAL, "entry %d: slot %d appears twice", b, slots[b]);
+        }
+    } else if (batch > kv->slots) {
+        return fail(QASR_EINVAL, "batch %d larger than the pool's %d slots", batch, kv->slots);
+    }
+    (void)ctx;
+    return QASR_OK;
+}
+
+int qasr_decode_attn(qasr_ctx* ctx, qasr_kv* kv, int layer, int batch, const int32_t* slots,
+                     const int32_t* cur_len, const void* q_dev, void* out_dev, void* stream) {
+    int rc = check_common(ctx, kv, layer);
+    if (rc) return rc;
+    rc = check_batch(ctx, kv, batch, slots, false);
+    if (rc) return rc;
+    if (batch == 0) return QASR_OK;
+    if (!cur_len || !q_dev || !out_dev) return fail(QASR_EINVAL, "null argument");
+    for (int b = 0; b < batch; ++b) {
+        if (cur_len[b] <= 0) return fail(QASR_EINVAL, "entry %d: cur_len %d must be > 0", b, cur_len[b]);
+        if (cur_len[b] > kv->cap)
+            return fail(QASR_ERANGE, "entry %d: cur_len %d exceeds KV capacity %d", b, cur_len[b],
+                        kv->cap);
+        if (cur_len[b] > ctx->cfg.max_seq)
+            return fail(QASR_ERANGE, "entry %d: cur_len %d exceeds max_seq %d", b, cur_len[b],
+                        ctx->cfg.max_seq);
+    }
+    DeviceScope ds(ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    return run_decode(false, ctx, kv, layer, batch, slots, cur_len, q_dev, nullptr, nullptr, out_dev,
+                      stream);
+}
+
+int qasr_decode_step(qasr_ctx* ctx, qasr_kv* kv, int layer, int batch, const int32_t* slots,
+                     const int32_t* pos, const void* qkv_dev, const void* q_gain_dev,
+                     const void* k_gain_dev, void* out_dev, void* stream) {
+    int rc = check_common(ctx, kv, layer);
+    if (rc) return rc;
+    rc = check_batch(ctx, kv, batch, slots, true);
+    if (rc) return rc;
+    if (batch == 0) return QASR_OK;
+    if (!pos || !qkv_dev || !q_gain_dev || !k_gain_dev || !out_dev)
+        return fail(QASR_EINVAL, "null argument");
+    if (!ctx->cos) return fail(QASR_ESTATE, "RoPE tables not set (qasr_set_rope_tables)");
+    std::vector<int32_t> lens(batch);
+    for (int b = 0; b < batch; ++b) {
+        if (pos[b] < 0) return fail(QASR_EINVAL, "entry %d: negative position", b);
+        if (pos[b] >= kv->cap)
+            return fail(QASR_ERANGE, "entry %d: position %d beyond KV capacity %d", b, pos[b],
+                        kv->cap);
+        if (pos[b] >= ctx->cfg.max_seq)
+            return fail(QASR_ERANGE, "entry %d: decode past max_seq %d", b, ctx->cfg.max_seq);
+        if (pos[b] >= ctx->rope_rows)
+            return fail(QASR_ERANGE, "entry %d: position %d beyond the %d RoPE table rows", b,
+                        pos[b], ctx->rope_rows);
+        lens[b] = pos[b] + 1;
+    }
+    DeviceScope ds(ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    return run_decode(true, ctx, kv, layer, batch, slots, lens.data(), qkv_dev, q_gain_dev,
+                      k_gain_dev, out_dev, stream);
+}
+
+int qasr_prefill_attn(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, int s,
+                      const void* q_dev, void* out_dev, void* stream) {
+    int rc = check_common(ctx, kv, layer);
+    if (rc) return rc;
+    if (slot < 0 || slot >= kv->slots)
+        return fail(QASR_EINVAL, "slot %d outside [0, %d)", slot, kv->slots);
+    if (kv_start < 0 || s < 0) return fail(QASR_EINVAL, "negative kv_start / s");
+    if (s == 0) return QASR_OK;
+    if (!q_dev || !out_dev) return fail(QASR_EINVAL, "null device pointer");
+    const int64_t end = (int64_t)kv_start + s;
+    if (end > ctx->cfg.max_seq)
+        return fail(QASR_ERANGE, "prefill needs %lld positions, max_seq is %d", (long long)end,
+                    ctx->cfg.max_seq);
+    if (end > kv->cap)
+        return fail(QASR_ERANGE, "prefill needs %lld positions, KV capacity is %d",
+                    (long long)end, kv->cap);
+    DeviceScope ds(ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    const qasr_attn_cfg& c = ctx->cfg;
+    const int nqh = c.num_attention_heads, nkvh = c.num_key_value_heads;
+    const qasr::CacheGeom g = geom(kv);
+    const int64_t ld = (int64_t)nqh * qasr::kHeadDim;
+    const int rows_per_launch = qasr::kMaxRowBlocks * qasr::kPrefillRows;
+    const int tps_forced = env_int("QASR_PREFILL_TPS", 0);
+    for (int r0 = 0; r0 < s; r0 += rows_per_launch) {
+        const int rows = std::min(rows_per_launch, s - r0);
+        const int ks = kv_start + r0;
+        // Tiles per split: enough items to give every CU work, without
+        // splitting row blocks whose key range is short.
+        int tps = tps_forced;
+        if (tps <= 0) {
+            const int nrb = (rows + qasr::kPrefillRows - 1) / qasr::kPrefillRows;
+            const int64_t tiles_all = (int64_t)nrb * ((ks + rows + 63) / 64);
+            const int64_t want = std::max<int64_t>(1, 512 / nkvh);
+            tps = (int)std::max<int64_t>(4, (tiles_all + want - 1) / want);
+        }
+        qasr::PrefillPlan P = qasr::plan_prefill(rows, ks, nkvh, tps);
+        rc = ensure_prefill_ws(kv, (int64_t)P.items_per_kvh * nkvh);
+        if (rc) return rc;
+        qasr::PrefillArgs a;
+        a.q = (const f16*)q_dev + r0 * ld;
+        a.out = (f16*)out_dev + r0 * ld;
+        a.k = g.base + slot * g.slot_stride + layer * g.layer_stride;
+        a.v = a.k + g.kv_stride;
+        a.head_stride = g.head_stride;
+        a.nqh = nqh;
+        a.nkvh = nkvh;
+        a.s = rows;
+        a.kv_start = ks;
+        a.scale_log2 = ctx->scale_log2;
+        qasr::PrefillWs ws{kv->pws_o, kv->pws_ml, kv->pws_ctr, kv->pws_items};
+        hipError_t e = qasr::launch_prefill_attn(a, P, ws, (hipStream_t)stream);
+        if (e != hipSuccess) return hip_fail(e, "prefill attention launch");
+    }
+    return QASR_OK;
+}
+
+int qasr_prefill_layer(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, int s,
+                       const void* qkv_dev, const void* q_gain_dev, const void* k_gain_dev,
+                       void* q_work_dev, void* out_dev, void* stream) {
+    qasr_segment seg{slot, kv_start, s};
+    int rc = qasr_qk_norm_rope_append(ctx, kv, layer, &seg, 1, qkv_dev, q_gain_dev, k_gain_dev,
+                                      q_work_dev, stream);
+    if (rc) return rc;
+    return qasr_prefill_attn(ctx, kv, layer, slot, kv_start, s, q_work_dev, out_dev, stream);
+}
+
+}  // extern "C"

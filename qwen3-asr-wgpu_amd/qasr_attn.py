@@ -1,0 +1,366 @@
+"""Python binding of libqasr_attn.so (ctypes) and a host-side mirror of the
+reference decoder's backend contract for the attention path.
+
+The reference's seam is `TextBackend` (src/inference.rs:213-269):
+`prefill(hidden, s, kv_start)`, `step()`, `max_seq()`, `ensure_capacity(need)`,
+`set_rope_tables(cos, sin)`.  `AttnBackend` below keeps those names and their
+argument meaning for the attention part of one decoder layer, on a pooled
+per-slot KV cache (`--batch N` slots, src/decoder.rs:2453-2457, 2856-2883).
+Errors raise `QasrError` carrying the library's status code, as the reference
+returns `Err` from the same bounds checks (src/cpu_decoder.rs:489-495, 520).
+
+Device tensors are torch tensors (torch supplies device memory and streams;
+every computation runs in the HIP library).  Calls are enqueued on torch's
+current stream.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libqasr_attn.so")
+
+QASR_OK, QASR_EINVAL, QASR_ERANGE, QASR_ENOMEM, QASR_EDEVICE, QASR_ESTATE = range(6)
+KV_INITIAL_CAP = 1024
+KV_STEP = 256
+DECODER_MAX_SEQ = 16384
+
+# Every symbol include/qasr_attn.h declares.
+ABI_SYMBOLS = (
+    "qasr_abi_version", "qasr_last_error", "qasr_ctx_create", "qasr_ctx_destroy",
+    "qasr_mrope_text_tables", "qasr_set_rope_tables", "qasr_kv_create", "qasr_kv_destroy",
+    "qasr_kv_get_info", "qasr_kv_ensure_capacity", "qasr_qk_norm_rope_append",
+    "qasr_decode_attn", "qasr_decode_step", "qasr_prefill_attn", "qasr_prefill_layer",
+)
+
+
+class QasrError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[qasr status {code}] {message}")
+        self.code = code
+
+
+class AttnCfg(ctypes.Structure):
+    _fields_ = [
+        ("num_attention_heads", ctypes.c_int32),
+        ("num_key_value_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("num_hidden_layers", ctypes.c_int32),
+        ("rms_norm_eps", ctypes.c_float),
+        ("max_seq", ctypes.c_int32),
+    ]
+
+
+class Segment(ctypes.Structure):
+    _fields_ = [("slot", ctypes.c_int32), ("pos0", ctypes.c_int32), ("rows", ctypes.c_int32)]
+
+
+class KvInfo(ctypes.Structure):
+    _fields_ = [
+        ("base_dev", ctypes.c_void_p),
+        ("slots", ctypes.c_int32),
+        ("layers", ctypes.c_int32),
+        ("nkvh", ctypes.c_int32),
+        ("cap", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("slot_stride", ctypes.c_int64),
+        ("layer_stride", ctypes.c_int64),
+        ("kv_stride", ctypes.c_int64),
+        ("head_stride", ctypes.c_int64),
+        ("bytes", ctypes.c_size_t),
+    ]
+
+
+_lib = None
+_vp = ctypes.c_void_p
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+
+
+def load(path: str = LIB_PATH):
+    """Load the HIP library; raises if it has not been built (no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{path} is missing: build it with `python qwen3-asr-wgpu_amd/build.py` "
+            "(there is no CPU fallback for the attention path)")
+    L = ctypes.CDLL(path)
+    L.qasr_abi_version.restype = ctypes.c_int
+    L.qasr_last_error.restype = ctypes.c_char_p
+    L.qasr_ctx_create.argtypes = [ctypes.POINTER(AttnCfg), ctypes.c_int, ctypes.POINTER(_vp)]
+    L.qasr_ctx_destroy.argtypes = [_vp]
+    L.qasr_ctx_destroy.restype = None
+    L.qasr_mrope_text_tables.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_double, _i32p,
+                                         ctypes.c_int, ctypes.c_int, _u16p, _u16p]
+    L.qasr_set_rope_tables.argtypes = [_vp, _u16p, _u16p, ctypes.c_int]
+    L.qasr_kv_create.argtypes = [_vp, ctypes.c_int, ctypes.c_int, ctypes.POINTER(_vp)]
+    L.qasr_kv_destroy.argtypes = [_vp]
+    L.qasr_kv_destroy.restype = None
+    L.qasr_kv_get_info.argtypes = [_vp, ctypes.POINTER(KvInfo)]
+    L.qasr_kv_ensure_capacity.argtypes = [_vp, ctypes.c_int, ctypes.c_int, _i32p]
+    L.qasr_qk_norm_rope_append.argtypes = [_vp, _vp, ctypes.c_int, ctypes.POINTER(Segment),
+                                           ctypes.c_int, _vp, _vp, _vp, _vp, _vp]
+    L.qasr_decode_attn.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, _i32p, _i32p, _vp, _vp,
+                                   _vp]
+    L.qasr_decode_step.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, _i32p, _i32p, _vp, _vp,
+                                   _vp, _vp, _vp]
+    L.qasr_prefill_attn.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int, _vp, _vp, _vp]
+    L.qasr_prefill_layer.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp]
+    _lib = L
+    return L
+
+
+def _check(rc: int):
+    if rc != QASR_OK:
+        msg = load().qasr_last_error()
+        raise QasrError(rc, msg.decode() if msg else "")
+
+
+def _i32(seq) -> ctypes.Array:
+    a = (ctypes.c_int32 * len(seq))()
+    for i, v in enumerate(seq):
+        a[i] = int(v)
+    return a
+
+
+def mrope_text_tables(rows: int, head_dim: int = 128, rope_theta: float = 1e6,
+                      section: Sequence[int] = (24, 20, 20), interleaved: bool = True):
+    """f16 cos/sin tables ([rows][head_dim] uint16 bit patterns) for text
+    positions, as src/inference.rs:1038-1049 builds them."""
+    c = np.empty((rows, head_dim), dtype=np.uint16)
+    s = np.empty((rows, head_dim), dtype=np.uint16)
+    sec = _i32(section)
+    _check(load().qasr_mrope_text_tables(rows, head_dim, rope_theta, sec, len(section),
+                                         int(interleaved), c.ctypes.data_as(_u16p),
+                                         s.ctypes.data_as(_u16p)))
+    return c, s
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is not None:
+        return int(stream)
+    import torch
+
+    return int(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev(t, name: str, dtype=None) -> int:
+    """Device pointer of a contiguous CUDA tensor (f16 unless `dtype`)."""
+    import torch
+
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must live on the GPU")
+    want = dtype or torch.float16
+    if t.dtype != want:
+        raise ValueError(f"{name} must be {want}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t.data_ptr()
+
+
+class Context:
+    """Device + shape binding (qasr_ctx)."""
+
+    def __init__(self, nqh: int = 16, nkvh: int = 8, head_dim: int = 128, layers: int = 28,
+                 eps: float = 1e-6, max_seq: int = DECODER_MAX_SEQ, device: int = 0):
+        self.cfg = AttnCfg(nqh, nkvh, head_dim, layers, eps, max_seq)
+        self.device = device
+        h = _vp()
+        _check(load().qasr_ctx_create(ctypes.byref(self.cfg), device, ctypes.byref(h)))
+        self.handle = h
+
+    @property
+    def nqh(self):
+        return self.cfg.num_attention_heads
+
+    @property
+    def nkvh(self):
+        return self.cfg.num_key_value_heads
+
+    @property
+    def layers(self):
+        return self.cfg.num_hidden_layers
+
+    def set_rope_tables(self, cos_u16: np.ndarray, sin_u16: np.ndarray):
+        cos_u16 = np.ascontiguousarray(cos_u16, dtype=np.uint16)
+        sin_u16 = np.ascontiguousarray(sin_u16, dtype=np.uint16)
+        if cos_u16.shape != sin_u16.shape or cos_u16.ndim != 2:
+            raise ValueError("cos/sin must be equal [rows][head_dim] arrays")
+        _check(load().qasr_set_rope_tables(self.handle, cos_u16.ctypes.data_as(_u16p),
+                                           sin_u16.ctypes.data_as(_u16p), cos_u16.shape[0]))
+
+    def close(self):
+        if self.handle:
+            load().qasr_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class KVPool:
+    """Pooled per-slot KV cache (qasr_kv): [slot][layer][K|V][kvh][cap][hd] f16."""
+
+    def __init__(self, ctx: Context, slots: int, cap: int = KV_INITIAL_CAP):
+        self.ctx = ctx
+        h = _vp()
+        _check(load().qasr_kv_create(ctx.handle, slots, cap, ctypes.byref(h)))
+        self.handle = h
+
+    def info(self) -> KvInfo:
+        inf = KvInfo()
+        _check(load().qasr_kv_get_info(self.handle, ctypes.byref(inf)))
+        return inf
+
+    @property
+    def cap(self) -> int:
+        return self.info().cap
+
+    @property
+    def slots(self) -> int:
+        return self.info().slots
+
+    def ensure_capacity(self, need: int, keep_rows: int) -> int:
+        out = ctypes.c_int32(0)
+        _check(load().qasr_kv_ensure_capacity(self.handle, need, keep_rows, ctypes.byref(out)))
+        return out.value
+
+    def tensor(self):
+        """A torch view of the whole pool, shaped [slot][layer][2][kvh][cap][hd]."""
+        import torch
+
+        inf = self.info()
+        n = inf.bytes // 2
+        storage = _DeviceView(inf.base_dev, inf.bytes, self.ctx.device)
+        t = torch.as_tensor(storage, device=f"cuda:{self.ctx.device}")
+        assert t.numel() == n
+        return t.view(inf.slots, inf.layers, 2, inf.nkvh, inf.cap, inf.head_dim)
+
+    def close(self):
+        if self.handle:
+            load().qasr_kv_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class _DeviceView:
+    """__cuda_array_interface__ over library-owned device memory (f16)."""
+
+    def __init__(self, ptr: int, nbytes: int, device: int):
+        self.__cuda_array_interface__ = {
+            "shape": (nbytes // 2,),
+            "typestr": "<f2",
+            "data": (int(ptr), False),
+            "version": 3,
+            "strides": None,
+            "stream": None,
+        }
+
+
+# ---- stage entry points (thin wrappers over the C ABI) --------------------
+
+def qk_norm_rope_append(ctx: Context, kv: KVPool, layer: int, segments, qkv, q_gain, k_gain,
+                        q_out, stream=None):
+    segs = (Segment * len(segments))(*[Segment(int(s), int(p), int(r)) for s, p, r in segments])
+    _check(load().qasr_qk_norm_rope_append(
+        ctx.handle, kv.handle, layer, segs, len(segments), _dev(qkv, "qkv"),
+        _dev(q_gain, "q_gain"), _dev(k_gain, "k_gain"), _dev(q_out, "q_out"), _stream(stream)))
+
+
+def decode_attn(ctx: Context, kv: KVPool, layer: int, cur_len, q, out, slots=None, stream=None):
+    b = len(cur_len)
+    _check(load().qasr_decode_attn(ctx.handle, kv.handle, layer, b,
+                                   _i32(slots) if slots is not None else None, _i32(cur_len),
+                                   _dev(q, "q"), _dev(out, "out"), _stream(stream)))
+
+
+def decode_step(ctx: Context, kv: KVPool, layer: int, pos, qkv, q_gain, k_gain, out, slots=None,
+                stream=None):
+    b = len(pos)
+    _check(load().qasr_decode_step(ctx.handle, kv.handle, layer, b,
+                                   _i32(slots) if slots is not None else None, _i32(pos),
+                                   _dev(qkv, "qkv"), _dev(q_gain, "q_gain"),
+                                   _dev(k_gain, "k_gain"), _dev(out, "out"), _stream(stream)))
+
+
+def prefill_attn(ctx: Context, kv: KVPool, layer: int, slot: int, kv_start: int, s: int, q, out,
+                 stream=None):
+    _check(load().qasr_prefill_attn(ctx.handle, kv.handle, layer, slot, kv_start, s,
+                                    _dev(q, "q"), _dev(out, "out"), _stream(stream)))
+
+
+def prefill_layer(ctx: Context, kv: KVPool, layer: int, slot: int, kv_start: int, s: int, qkv,
+                  q_gain, k_gain, q_work, out, stream=None):
+    _check(load().qasr_prefill_layer(ctx.handle, kv.handle, layer, slot, kv_start, s,
+                                     _dev(qkv, "qkv"), _dev(q_gain, "q_gain"),
+                                     _dev(k_gain, "k_gain"), _dev(q_work, "q_work"),
+                                     _dev(out, "out"), _stream(stream)))
+
+
+class AttnBackend:
+    """The attention half of the reference's TextBackend (src/inference.rs:
+    213-269) on one GPU: the same method names, over a pooled KV cache of
+    `slots` sequences (`--batch N`).  `prefill` and `step` take the fused qkv
+    projection rows ([rows][(nqh+2*nkvh)*hd] f16) where the reference takes
+    hidden states, since the projections sit outside this path; they return
+    the attention output rows ([rows][nqh*hd] f16) that feed o_proj.
+    """
+
+    def __init__(self, nqh=16, nkvh=8, head_dim=128, layers=28, eps=1e-6,
+                 max_seq=DECODER_MAX_SEQ, slots=1, device=0, cap=KV_INITIAL_CAP):
+        self.ctx = Context(nqh, nkvh, head_dim, layers, eps, max_seq, device)
+        self.kv = KVPool(self.ctx, slots, min(cap, max_seq))
+        self.max_seq = max_seq
+        self.pos = [0] * slots  # positions already in each slot's cache
+
+    def set_rope_tables(self, cos_u16, sin_u16):
+        self.ctx.set_rope_tables(cos_u16, sin_u16)
+
+    def ensure_capacity(self, need: int) -> int:
+        """Grow-only, KV_STEP granular; keeps every row already written."""
+        return self.kv.ensure_capacity(need, max(self.pos))
+
+    def prefill(self, layer: int, qkv, s: int, kv_start: int, q_gain, k_gain, slot: int = 0,
+                last_layer: bool = True):
+        import torch
+
+        nq = self.ctx.nqh * 128
+        q_work = torch.empty((s, nq), dtype=torch.float16, device=qkv.device)
+        out = torch.empty((s, nq), dtype=torch.float16, device=qkv.device)
+        prefill_layer(self.ctx, self.kv, layer, slot, kv_start, s, qkv, q_gain, k_gain, q_work,
+                      out)
+        if last_layer:
+            self.pos[slot] = kv_start + s
+        return out
+
+    def step(self, layer: int, qkv_rows, q_gain, k_gain, slots: Optional[Sequence[int]] = None,
+             last_layer: bool = True):
+        import torch
+
+        slots = list(range(qkv_rows.shape[0])) if slots is None else list(slots)
+        pos = [self.pos[s] for s in slots]
+        out = torch.empty((len(slots), self.ctx.nqh * 128), dtype=torch.float16,
+                          device=qkv_rows.device)
+        decode_step(self.ctx, self.kv, layer, pos, qkv_rows, q_gain, k_gain, out, slots=slots)
+        if last_layer:
+            for s in slots:
+                self.pos[s] += 1
+        return out

@@ -1,0 +1,180 @@
+"""Stage (b) decode attention on the GPU against the oracle
+(cpu_decoder.rs:292-365 with one row; stage (a) per 398-423), at the BASELINE
+decode configs and at edge lengths, plus invariants: fused step == stage (a)
+then attention (bitwise), chunk-size independence, slot-permutation
+invariance, appended rows bit-exact."""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+from workloads import (NKVH, QDIM, SEED_BASE, TOT, Layer, OracleSeq, assert_parity, cap_for,
+                       decode_lengths, tables)
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(O, rng, lay, lengths, cap, g, layer=0):
+    """Fill each slot's cache with positions 0..L-1 (GPU by stage (a), oracle by
+    its restatement) from the same raw rows; returns the oracle sequences."""
+    from gpu_helpers import say
+
+    refs = []
+    for sl, L in enumerate(lengths):
+        ref = OracleSeq(O, cap, lay, tables(O))
+        if L > 0:
+            rows = rng.normal_f16((L, TOT))
+            ref.append(rows, 0)
+            say(f"fill slot {sl} L={L}")
+            g.append(layer, lay, [(sl, 0, L)], rows)
+        refs.append(ref)
+    return refs
+
+
+def _decode_step_check(O, rng, lay, g, refs, lengths, layer=0, slots=None):
+    """One fused step at pos = L per slot; compares with the oracle step."""
+    import qasr_attn
+    from gpu_helpers import dev, empty, host, say
+
+    b = len(lengths)
+    slots = list(range(b)) if slots is None else slots
+    rows = rng.normal_f16((b, TOT))
+    out = empty(b, QDIM)
+    qg, kg = g.gains(lay)
+    say(f"decode_step batch={b} lengths[:4]={lengths[:4]}")
+    qasr_attn.decode_step(g.ctx, g.kv, layer, [lengths[i] for i in range(b)], dev(rows), qg, kg,
+                          out, slots=slots)
+    got = host(out)
+    worst = (0.0, 0.0)
+    for i in range(b):
+        sl = slots[i]
+        _, want = refs[sl].step(rows[i:i + 1], lengths[i])
+        ma, mr = assert_parity(got[i:i + 1], want, f"entry {i} slot {sl} L={lengths[i] + 1}")
+        worst = (max(worst[0], ma), max(worst[1], mr))
+        # the appended row is bit-exact
+        k_gpu, v_gpu = g.cache(sl, layer, lengths[i] + 1)
+        k_ref, v_ref = refs[sl].cache_f16()
+        assert np.array_equal(k_gpu[:, -1], k_ref[:, lengths[i]])
+        assert np.array_equal(v_gpu[:, -1], v_ref[:, lengths[i]])
+    return got, rows, worst
+
+
+def test_config1_single_slot_decode(O, gpu):
+    from gpu_helpers import Gpu
+
+    from oracle import Rng
+
+    rng = Rng(SEED_BASE + 1)
+    lay = Layer(rng)
+    g = Gpu(slots=1, cap=1024)
+    refs = _setup(O, rng, lay, [511], 1024, g)
+    _, _, worst = _decode_step_check(O, rng, lay, g, refs, [511])
+    print("config1 max_abs/max_rel", worst)
+    g.close()
+
+
+def test_config3_batch16_ragged_decode(O, gpu):
+    from gpu_helpers import Gpu
+
+    from oracle import Rng
+
+    rng = Rng(SEED_BASE + 3)
+    lengths = decode_lengths(rng, 16, 400, 2400)  # drawn first, as bench.py does
+    lay = Layer(rng)
+    cap = cap_for(max(lengths) + 1)
+    g = Gpu(slots=16, cap=cap)
+    refs = _setup(O, rng, lay, lengths, cap, g)
+    _, _, worst = _decode_step_check(O, rng, lay, g, refs, lengths)
+    print("config3 max_abs/max_rel", worst)
+    g.close()
+
+
+@pytest.mark.parametrize("chunk", ["128", "256", "512", "1024"])
+def test_decode_chunk_sizes_and_unfused_equal_fused(O, gpu, chunk, monkeypatch):
+    """Every split-K chunking matches the oracle; the unfused path
+    (qasr_decode_attn on stage-(a) output) equals the fused step bitwise."""
+    import qasr_attn
+    from gpu_helpers import Gpu, dev, empty, host, say
+
+    from oracle import Rng
+
+    monkeypatch.setenv("QASR_DECODE_CHUNK", chunk)
+    rng = Rng(SEED_BASE + 200 + int(chunk))
+    lay = Layer(rng)
+    lengths = [1, 2, 127, 128, 129, 255, 256, 1023, 1024, 1500, 2047, 2048, 4095]
+    cap = cap_for(max(lengths) + 1)
+    n = len(lengths)
+    g = Gpu(slots=n, cap=cap)
+    refs = _setup(O, rng, lay, [L - 1 for L in lengths], cap, g)
+    got_fused, rows, _ = _decode_step_check(O, rng, lay, g, refs, [L - 1 for L in lengths])
+    # unfused: q from stage (a) (re-appending the same rows rewrites the same bits)
+    q = g.append(0, lay, [(i, lengths[i] - 1, 1) for i in range(n)], rows)
+    out = empty(n, QDIM)
+    say(f"decode_attn unfused chunk={chunk}")
+    qasr_attn.decode_attn(g.ctx, g.kv, 0, lengths, dev(q), out)
+    assert np.array_equal(host(out), got_fused)
+    g.close()
+
+
+def test_decode_cap_length_and_permuted_slots(O, gpu):
+    """cur_len == cap; slot order in the batch does not change any slot's output."""
+    import qasr_attn
+    from gpu_helpers import Gpu, dev, empty, host, say
+
+    from oracle import Rng
+
+    rng = Rng(SEED_BASE + 300)
+    lay = Layer(rng)
+    cap = 1280
+    lengths = [cap - 1, 5, 700, 1000]
+    g = Gpu(slots=4, cap=cap)
+    refs = _setup(O, rng, lay, lengths, cap, g)
+    got, rows, _ = _decode_step_check(O, rng, lay, g, refs, lengths)
+    q = g.append(0, lay, [(i, lengths[i], 1) for i in range(4)], rows)
+    perm = [2, 0, 3, 1]
+    out = empty(4, QDIM)
+    say("decode_attn permuted slots")
+    qasr_attn.decode_attn(g.ctx, g.kv, 0, [lengths[p] + 1 for p in perm], dev(q[perm]), out,
+                          slots=perm)
+    assert np.array_equal(host(out), got[perm])
+    g.close()
+
+
+def test_config5_64_slots_two_layers(O, gpu):
+    """Config 5's shape (64 slots, ragged [64, 4096]) on two layers."""
+    from gpu_helpers import Gpu
+
+    from oracle import Rng
+
+    rng = Rng(SEED_BASE + 5)
+    lengths = decode_lengths(rng, 64, 64, 4096)
+    cap = cap_for(max(lengths) + 1)
+    g = Gpu(slots=64, cap=cap, layers=2)
+    worst = (0.0, 0.0)
+    for layer in (0, 1):
+        lay = Layer(rng)
+        refs = _setup(O, rng, lay, lengths, cap, g, layer=layer)
+        _, _, w = _decode_step_check(O, rng, lay, g, refs, lengths, layer=layer)
+        worst = (max(worst[0], w[0]), max(worst[1], w[1]))
+        del refs
+    print("config5 max_abs/max_rel", worst)
+    g.close()
+
+
+def test_decode_long_context_split(O, gpu):
+    """Config 4's decode side: one slot at 8192+ keys, 3 consecutive steps."""
+    from gpu_helpers import Gpu
+
+    from oracle import Rng
+
+    rng = Rng(SEED_BASE + 4)
+    lay = Layer(rng)
+    L0 = 8192
+    cap = cap_for(L0 + 64)
+    g = Gpu(slots=1, cap=cap)
+    refs = _setup(O, rng, lay, [L0], cap, g)
+    for step in range(3):
+        _decode_step_check(O, rng, lay, g, refs, [L0 + step])
+    g.close()

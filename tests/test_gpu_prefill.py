@@ -1,0 +1,147 @@
+"""Stage (c) causal prefill attention on the GPU against the oracle
+(cpu_decoder.rs:292-365 with rows = s, q0 = kv_start), at config 2's shape,
+ragged row counts, chunked prefill against an existing cache (config 4), and
+the invariants: chunked == full prefill (stream.rs:366-376 / stream_api.rs:
+178-185) and prefill row r == a decode query at position kv_start + r."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from workloads import QDIM, SEED_BASE, TOT, Layer, OracleSeq, assert_parity, cap_for, tables
+
+pytestmark = pytest.mark.gpu
+
+
+def _prefill_gpu(g, layer, lay, slot, kv_start, qkv):
+    import qasr_attn
+    from gpu_helpers import dev, empty, host, say
+
+    s = qkv.shape[0]
+    q = empty(s, QDIM)
+    out = empty(s, QDIM)
+    qg, kg = g.gains(lay)
+    say(f"prefill slot={slot} kv_start={kv_start} s={s}")
+    qasr_attn.prefill_layer(g.ctx, g.kv, layer, slot, kv_start, s, dev(qkv), qg, kg, q, out)
+    return host(q), host(out)
+
+
+def test_config2_prefill_420(O, gpu):
+    from gpu_helpers import Gpu
+
+    from oracle import Rng
+
+    rng = Rng(SEED_BASE + 2)
+    lay = Layer(rng)
+    s = 420
+    qkv = rng.normal_f16((s, TOT))
+    g = Gpu(slots=1, cap=1024)
+    q_gpu, out_gpu = _prefill_gpu(g, 0, lay, 0, 0, qkv)
+    ref = OracleSeq(O, 1024, lay, tables(O))
+    q_ref, out_ref = ref.step(qkv, 0)
+    assert np.array_equal(q_gpu, q_ref)
+    ma, mr = assert_parity(out_gpu, out_ref, "config2")
+    print("config2 max_abs/max_rel", ma, mr)
+    g.close()
+
+
+@pytest.mark.parametrize("kv_start,s", [(0, 1), (0, 31), (0, 64), (0, 65), (0, 200), (5, 1),
+                                        (100, 3), (640, 129), (1000, 600), (3000, 64)])
+def test_prefill_ragged_against_oracle(O, gpu, kv_start, s):
+    from gpu_helpers import Gpu
+
+    from oracle import Rng
+
+    rng = Rng(SEED_BASE + 400 + kv_start + s)
+    lay = Layer(rng)
+    cap = cap_for(kv_start + s)
+    g = Gpu(slots=2, cap=cap)
+    ref = OracleSeq(O, cap, lay, tables(O))
+    if kv_start:
+        pre = rng.normal_f16((kv_start, TOT))
+        ref.append(pre, 0)
+        g.append(0, lay, [(1, 0, kv_start)], pre)
+    qkv = rng.normal_f16((s, TOT))
+    _, out_gpu = _prefill_gpu(g, 0, lay, 1, kv_start, qkv)
+    _, out_ref = ref.step(qkv, kv_start)
+    assert_parity(out_gpu, out_ref, f"kv_start={kv_start} s={s}")
+    g.close()
+
+
+@pytest.mark.parametrize("tps", ["1", "3", "1000"])
+def test_prefill_split_choices(O, gpu, tps, monkeypatch):
+    """Any split of the key range (1 tile per item .. no split) matches."""
+    from gpu_helpers import Gpu
+
+    from oracle import Rng
+
+    monkeypatch.setenv("QASR_PREFILL_TPS", tps)
+    rng = Rng(SEED_BASE + 500)
+    lay = Layer(rng)
+    s = 700
+    qkv = rng.normal_f16((s, TOT))
+    g = Gpu(slots=1, cap=1024)
+    _, out_gpu = _prefill_gpu(g, 0, lay, 0, 0, qkv)
+    ref = OracleSeq(O, 1024, lay, tables(O))
+    _, out_ref = ref.step(qkv, 0)
+    assert_parity(out_gpu, out_ref, f"tps={tps}")
+    g.close()
+
+
+def test_config4_chunked_prefill_long_context(O, gpu):
+    """Config 4: 16 chunks of 512 rows at kv_start = 0..7680.  Rows sampled from
+    the first and last chunks match the oracle; the chunked result equals a
+    single 8192-row prefill within tolerance, and re-running a chunk is
+    deterministic."""
+    from gpu_helpers import Gpu
+
+    from oracle import Rng
+
+    rng = Rng(SEED_BASE + 4)
+    lay = Layer(rng)
+    total, chunk = 8192, 512
+    cap = cap_for(total + 64)
+    qkv = rng.normal_f16((total, TOT))
+    g = Gpu(slots=2, cap=cap)
+    outs = []
+    for c in range(total // chunk):
+        _, o = _prefill_gpu(g, 0, lay, 0, c * chunk, qkv[c * chunk:(c + 1) * chunk])
+        outs.append(o)
+    chunked = np.concatenate(outs)
+    _, full = _prefill_gpu(g, 0, lay, 1, 0, qkv)
+    assert_parity(chunked, full, "chunked vs full")
+    _, again = _prefill_gpu(g, 0, lay, 0, total - chunk, qkv[total - chunk:])
+    assert np.array_equal(again, outs[-1])
+    # oracle on sampled rows: cache from stage (a) over all rows, attention for
+    # rows 0..31 and 8160..8191 only.
+    ref = OracleSeq(O, cap, lay, tables(O))
+    q_ref = ref.append(qkv, 0)
+    for r0 in (0, 7680, total - 32):
+        want = ref.attend(q_ref[r0:r0 + 32], r0)
+        assert_parity(chunked[r0:r0 + 32], want, f"rows {r0}..{r0 + 31}")
+    g.close()
+
+
+def test_prefill_row_equals_decode_query(O, gpu):
+    """Prefill row r attends exactly what a decode query at kv_start + r does."""
+    import qasr_attn
+    from gpu_helpers import Gpu, dev, empty, host
+
+    from oracle import Rng
+
+    rng = Rng(SEED_BASE + 600)
+    lay = Layer(rng)
+    kv_start, s = 300, 250
+    g = Gpu(slots=1, cap=1024)
+    pre = rng.normal_f16((kv_start, TOT))
+    g.append(0, lay, [(0, 0, kv_start)], pre)
+    qkv = rng.normal_f16((s, TOT))
+    q, out = _prefill_gpu(g, 0, lay, 0, kv_start, qkv)
+    rows = [0, 1, 63, 64, 127, 200, 249]
+    dq = empty(len(rows), QDIM)
+    dq.copy_(dev(q[rows]))
+    dout = empty(len(rows), QDIM)
+    qasr_attn.decode_attn(g.ctx, g.kv, 0, [kv_start + r + 1 for r in rows], dq, dout,
+                          slots=[0] * len(rows))
+    assert_parity(host(dout), out[rows], "prefill vs decode")
+    g.close()

@@ -1,0 +1,115 @@
+"""Seeded synthetic workloads of the five BASELINE configs, oracle-side
+helpers, and the parity metric shared by the tests.
+
+Inputs come from the oracle's SplitMix64 / Box-Muller generator (f64 -> f32 ->
+f16 RNE), seeded 0x51A50000 + config id.  Raw qkv rows are N(0,1); q/k RMSNorm
+gains are N(1, 0.1).  Cached positions are produced by running stage (a) on
+raw rows (the oracle for the reference cache, the HIP kernel for the GPU one).
+
+Parity metric (stated once, used everywhere): over all output elements,
+  max_abs = max |got - ref|
+  max_rel = max |got - ref| / max(|ref|, REL_FLOOR),  REL_FLOOR = ATOL / RTOL = 0.2
+with ATOL = 2e-3 and RTOL = 1e-2 from the north-star tolerance.  The floor
+keeps the relative figure meaningful where the reference is near zero (there
+an f16 output's own spacing dwarfs any relative bound).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+NQH, NKVH, HD = 16, 8, 128
+TOT = (NQH + 2 * NKVH) * HD
+QDIM = NQH * HD
+SEED_BASE = 0x51A50000
+MAX_SEQ = 16384
+EPS = 1e-6
+
+ATOL = 2e-3
+RTOL = 1e-2
+REL_FLOOR = ATOL / RTOL
+
+
+def errors(got_u16: np.ndarray, ref_u16: np.ndarray):
+    """(max_abs, max_rel) of f16 outputs given as uint16 bit patterns."""
+    g = np.asarray(got_u16, dtype=np.uint16).view(np.float16).astype(np.float64)
+    r = np.asarray(ref_u16, dtype=np.uint16).view(np.float16).astype(np.float64)
+    assert g.shape == r.shape
+    if g.size == 0:
+        return 0.0, 0.0
+    assert np.all(np.isfinite(r)), "reference has non-finite values"
+    if not np.all(np.isfinite(g)):
+        return float("inf"), float("inf")
+    d = np.abs(g - r)
+    return float(d.max()), float((d / np.maximum(np.abs(r), REL_FLOOR)).max())
+
+
+def assert_parity(got_u16, ref_u16, what: str = ""):
+    ma, mr = errors(got_u16, ref_u16)
+    assert ma <= ATOL and mr <= RTOL, f"{what}: max_abs {ma:.3e} (<= {ATOL}), max_rel {mr:.3e} (<= {RTOL})"
+    return ma, mr
+
+
+class Tables:
+    """f16 RoPE tables (as the decoder consumes them) and their f32 values."""
+
+    def __init__(self, O, rows: int = MAX_SEQ):
+        self.cos_u16, self.sin_u16 = O.text_rope_tables_f16(rows)
+        self.cos = O.f32_from_f16(self.cos_u16)
+        self.sin = O.f32_from_f16(self.sin_u16)
+
+
+_tables = {}
+
+
+def tables(O, rows: int = MAX_SEQ) -> Tables:
+    if rows not in _tables:
+        _tables[rows] = Tables(O, rows)
+    return _tables[rows]
+
+
+class Layer:
+    """One layer's seeded gains."""
+
+    def __init__(self, rng):
+        self.q_gain = rng.normal_f16((HD,), 1.0, 0.1)
+        self.k_gain = rng.normal_f16((HD,), 1.0, 0.1)
+
+
+class OracleSeq:
+    """One sequence's f32 K/V caches for one layer on the oracle side."""
+
+    def __init__(self, O, cap: int, layer: Layer, tab: Tables):
+        self.O = O
+        self.cap = cap
+        self.layer = layer
+        self.tab = tab
+        self.shape = O.make_shape(NQH, NKVH, HD, MAX_SEQ, EPS)
+        self.k = np.zeros((NKVH, cap, HD), dtype=np.float32)
+        self.v = np.zeros((NKVH, cap, HD), dtype=np.float32)
+
+    def append(self, qkv_rows: np.ndarray, q0: int) -> np.ndarray:
+        """Stage (a) on rows at positions q0..; returns the roped q rows (u16)."""
+        return self.O.qk_norm_rope_append(self.shape, self.cap, qkv_rows, q0, self.layer.q_gain,
+                                          self.layer.k_gain, self.tab.cos, self.tab.sin,
+                                          self.k, self.v)
+
+    def attend(self, q_u16: np.ndarray, q0: int, nthreads: int = 0) -> np.ndarray:
+        return self.O.attention(self.shape, self.cap, q_u16, q0, self.k, self.v, nthreads)
+
+    def step(self, qkv_rows: np.ndarray, q0: int):
+        """Stage (a) + attention (cpu_decoder.rs:398-427).  Returns (q, out)."""
+        return self.O.layer_attn(self.shape, self.cap, qkv_rows, q0, self.layer.q_gain,
+                                 self.layer.k_gain, self.tab.cos, self.tab.sin, self.k, self.v)
+
+    def cache_f16(self):
+        """The caches as f16 bit patterns (exact: they hold f16 values)."""
+        return self.O.f16_from_f32(self.k), self.O.f16_from_f32(self.v)
+
+
+def cap_for(need: int) -> int:
+    """KV_STEP-rounded capacity for `need` positions, at least KV_INITIAL_CAP."""
+    return max(1024, (need + 255) // 256 * 256)
+
+
+def decode_lengths(rng, n: int, lo: int, hi: int):
+    return [rng.uniform_int(lo, hi) for _ in range(n)]
