@@ -54,4 +54,34 @@ __device__ __forceinline__ float row_sum16(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---- publishing partial results to other workgroups ---------------------
+// MI355X has one L2 per XCD and they are not coherent with each other inside
+// a kernel.  An agent-scope release/acquire fence would write back and
+// invalidate the whole L2 (buffer_wbl2 / buffer_inv) in every workgroup, so
+// split-K partials are instead moved with device-scope ("sc1") accesses only:
+// relaxed agent-scope atomic stores write through to the device-coherent
+// level, relaxed agent-scope atomic loads miss in the non-coherent caches.
+// The writer waits for its stores to complete (vmcnt(0)) before the
+// workgroup bumps the arrival ticket; the reader issues its loads only after
+// the ticket says every partial has arrived.
+__device__ __forceinline__ void store_dev(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// All of this wave's memory operations complete, then a workgroup barrier.
+__device__ __forceinline__ void stores_done_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt unconstrained
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+}
+__device__ __forceinline__ uint32_t ticket_add(uint32_t* p) {
+    return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ticket_reset(uint32_t* p) {
+    __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace qasr

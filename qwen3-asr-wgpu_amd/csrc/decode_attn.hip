@@ -11,18 +11,23 @@
 //   Both q heads of the kv head (GQA 2:1) are computed from one K/V read.
 //   A wave pass covers 32 keys: 8 dwordx4 loads of K and 8 of V per lane, each
 //   load instruction reading 1 KiB contiguous (4 keys x 256 B, lane l -> key
-//   l/16, dims (l%16)*8..+8), so every instruction is fully coalesced.
+//   l/16, dims (l%16)*8..+8), so every instruction is fully coalesced.  Keys
+//   past the chunk end load a clamped (valid) row and are masked to -inf.
+//   The next pass's K loads are issued right after this pass's scores, and its
+//   V loads right after this pass's P.V, so memory stays busy during compute.
 //   q.k: v_dot2_f32_f16 on the lane's 8 dims, then a 16-lane DPP all-reduce
 //   inside the row (no LDS).  Softmax is online per 16-lane row (exp2 domain),
-//   P.V accumulates in f32 registers.  Rows and waves merge through LDS.
-//   When an entry needs more than one chunk, each workgroup writes its
-//   partial (max, sum, unnormalised output) and the last one to arrive (agent-
-//   scope ticket) merges them and writes the f16 output: no second launch.
+//   P.V accumulates in f32 registers (v_fma_mix).  Rows and waves merge through
+//   LDS.  When an entry needs more than one chunk, each workgroup publishes
+//   its partial (max, sum, unnormalised output) with device-scope stores and
+//   the last one to arrive (ticket) merges them: no second launch and no
+//   L2-wide cache maintenance.
 //
 // Fused variant (stage (a) + (b)): the workgroup recomputes its two q heads
 // from the raw qkv row (bit-identical to the stage-(a) kernel); the workgroup
 // owning the last chunk also ropes the new K row, appends K and V to the cache
-// and substitutes them for the cache load of that key.
+// and substitutes them for the cache load of that key.  The first K/V pass is
+// issued before this prologue so its latency overlaps it.
 
 #include "kernels.hpp"
 #include "norm_rope.hpp"
@@ -42,6 +47,17 @@ __device__ __forceinline__ float dot8(const H8& a, const H8& b) {
 
 constexpr float kNegInf = -__builtin_inff();
 
+// One wave pass of 8 loads (32 keys) of K or V starting at key t0; keys at or
+// past `kend` are clamped to row kend-1 (valid, masked later).
+__device__ __forceinline__ void load_pass(const f16* __restrict__ base, int t0, int kend, int row,
+                                          int seg, H8 (&r)[8]) {
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+        const int key = min(t0 + kk * 4 + row, kend - 1);
+        r[kk].u = *(const uint4*)(base + (int64_t)key * kHeadDim + seg * 8);
+    }
+}
+
 template <bool FUSED>
 __global__ __launch_bounds__(kDecodeWaves * 64) void decode_attn_kernel(
     CacheGeom g, int layer, DecodePlan P, const f16* __restrict__ qin,
@@ -52,6 +68,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_attn_kernel(
     __shared__ H8 s_q[2][16];
     __shared__ H8 s_knew[16];
     __shared__ H8 s_vnew[16];
+    __shared__ __attribute__((aligned(16))) f16 s_raw[4][kHeadDim];  // q0, q1, k, v raw heads
+    __shared__ __attribute__((aligned(16))) f16 s_tab[4][kHeadDim];  // q gain, k gain, cos, sin
     __shared__ float s_inv[3];
     __shared__ float s_m[kRows][2];
     __shared__ float s_l[kRows][2];
@@ -86,35 +104,49 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_attn_kernel(
     f16* Kc = g.base + P.slot[b] * g.slot_stride + layer * g.layer_stride + kvh * g.head_stride;
     f16* Vc = Kc + g.kv_stride;
 
-    H8 q0, q1;
-    int new_key = -1;
+    // Raw inputs of the fused prologue are requested before the first K/V pass
+    // so that waiting for them does not wait for the pass.
+    const int pos = L - 1;
+    const bool owner = FUSED && (c == nch - 1);
     if constexpr (FUSED) {
         const int64_t tot = (int64_t)(nqh + 2 * g.nkvh) * kHeadDim;
         const f16* qkv_row = qin + b * tot;
-        const int pos = L - 1;
-        const bool owner = (c == nch - 1);
-        const f16* qraw0 = qkv_row + h0 * kHeadDim;
-        const f16* qraw1 = qraw0 + kHeadDim;
-        const f16* kraw = qkv_row + (nqh + kvh) * kHeadDim;
-        const f16* vraw = qkv_row + (nqh + g.nkvh + kvh) * kHeadDim;
-        if (tid < 3 && (tid < 2 || owner))
-            s_inv[tid] = head_inv_rms_serial(tid == 0 ? qraw0 : tid == 1 ? qraw1 : kraw, P.eps);
+        if (tid < 64) {
+            const int which = tid >> 4;
+            const int hoff = which < 2 ? (h0 + which) : which == 2 ? (nqh + kvh) : (nqh + g.nkvh + kvh);
+            *(uint4*)&s_raw[which][seg * 8] = *(const uint4*)(qkv_row + hoff * kHeadDim + seg * 8);
+        } else if (tid < 128) {
+            const int which = (tid >> 4) & 3;
+            const f16* p = which == 0 ? q_gain
+                         : which == 1 ? k_gain
+                         : which == 2 ? cos_tab + (int64_t)pos * kHeadDim
+                                      : sin_tab + (int64_t)pos * kHeadDim;
+            *(uint4*)&s_tab[which][seg * 8] = *(const uint4*)(p + seg * 8);
+        }
+    }
+
+    H8 kr[8], vr[8];
+    int t0 = key0 + wave * kDecodeTileKeys;
+    load_pass(Kc, t0, key1, row, seg, kr);
+    load_pass(Vc, t0, key1, row, seg, vr);
+
+    H8 q0, q1;
+    if constexpr (FUSED) {
         __syncthreads();
-        const f16* crow = cos_tab + (int64_t)pos * kHeadDim;
-        const f16* srow = sin_tab + (int64_t)pos * kHeadDim;
+        if (tid < 3 && (tid < 2 || owner)) s_inv[tid] = head_inv_rms_serial(s_raw[tid], P.eps);
+        __syncthreads();
         const int h = tid >> 7, j = tid & 127;
-        ((f16*)s_q[h])[j] = rope_elem(h ? qraw1 : qraw0, q_gain, crow, srow, s_inv[h], j);
+        ((f16*)s_q[h])[j] = rope_elem(s_raw[h], s_tab[0], s_tab[2], s_tab[3], s_inv[h], j);
         if (owner) {
             if (h == 0) {
-                const f16 kv = rope_elem(kraw, k_gain, crow, srow, s_inv[2], j);
+                const f16 kv = rope_elem(s_raw[2], s_tab[1], s_tab[2], s_tab[3], s_inv[2], j);
                 ((f16*)s_knew)[j] = kv;
                 Kc[(int64_t)pos * kHeadDim + j] = kv;
             } else {
-                const f16 vv = vraw[j];
+                const f16 vv = s_raw[3][j];
                 ((f16*)s_vnew)[j] = vv;
                 Vc[(int64_t)pos * kHeadDim + j] = vv;
             }
-            new_key = pos;
         }
         __syncthreads();
         q0 = s_q[0][seg];
@@ -131,22 +163,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_attn_kernel(
     for (int d = 0; d < 8; ++d) a0[d] = a1[d] = 0.0f;
 
     const float sl2 = P.scale_log2;
-    for (int t0 = key0 + wave * kDecodeTileKeys; t0 < key1; t0 += kDecodeWgKeys) {
-        H8 kr[8], vr[8];
+    for (; t0 < key1; t0 += kDecodeWgKeys) {
+        if constexpr (FUSED) {
+            if (owner) {
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-            const int key = t0 + kk * 4 + row;
-            if (key < key1) {
-                kr[kk].u = *(const uint4*)(Kc + (int64_t)key * kHeadDim + seg * 8);
-                vr[kk].u = *(const uint4*)(Vc + (int64_t)key * kHeadDim + seg * 8);
-            } else {
-                kr[kk].u = make_uint4(0, 0, 0, 0);
-                vr[kk].u = make_uint4(0, 0, 0, 0);
-            }
-            if constexpr (FUSED) {
-                if (key == new_key) {
-                    kr[kk] = s_knew[seg];
-                    vr[kk] = s_vnew[seg];
+                for (int kk = 0; kk < 8; ++kk) {
+                    if (t0 + kk * 4 + row == pos) {
+                        kr[kk] = s_knew[seg];
+                        vr[kk] = s_vnew[seg];
+                    }
                 }
             }
         }
@@ -157,6 +182,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_attn_kernel(
             s1[kk] = row_sum16(dot8(q1, kr[kk])) * sl2;
             if (t0 + kk * 4 + row >= key1) s0[kk] = s1[kk] = kNegInf;
         }
+        const int tn = t0 + kDecodeWgKeys;
+        if (tn < key1) load_pass(Kc, tn, key1, row, seg, kr);
         float mt0 = s0[0], mt1 = s1[0];
 #pragma unroll
         for (int kk = 1; kk < 8; ++kk) {
@@ -193,6 +220,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_attn_kernel(
                 a1[d] = fmaf(s1[kk], v, a1[d]);
             }
         }
+        if (tn < key1) load_pass(Vc, tn, key1, row, seg, vr);
     }
 
     // Merge the 16 rows of the workgroup (each row saw a disjoint key subset).
@@ -227,34 +255,28 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_attn_kernel(
         return;
     }
 
-    ws_acc[(int64_t)wg * (2 * kHeadDim) + h * kHeadDim + j] = A;
+    store_dev(&ws_acc[(int64_t)wg * (2 * kHeadDim) + h * kHeadDim + j], A);
     if (j == 0) {
-        ws_ml[(int64_t)wg * 4 + h] = M;
-        ws_ml[(int64_t)wg * 4 + 2 + h] = Ls;
+        store_dev(&ws_ml[(int64_t)wg * 4 + h], M);
+        store_dev(&ws_ml[(int64_t)wg * 4 + 2 + h], Ls);
     }
-    __threadfence();
-    __syncthreads();
+    stores_done_barrier();
     uint32_t* ctr = &counters[b * g.nkvh + kvh];
-    if (tid == 0) {
-        const uint32_t prev =
-            __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == (uint32_t)(nch - 1));
-    }
+    if (tid == 0) s_last = (ticket_add(ctr) == (uint32_t)(nch - 1));
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
     const int64_t it0 = P.wg_base[b] + kvh * nch;
     float M2 = kNegInf;
-    for (int i = 0; i < nch; ++i) M2 = fmaxf(M2, ws_ml[(it0 + i) * 4 + h]);
+    for (int i = 0; i < nch; ++i) M2 = fmaxf(M2, load_dev(&ws_ml[(it0 + i) * 4 + h]));
     float L2 = 0.0f, A2 = 0.0f;
     for (int i = 0; i < nch; ++i) {
-        const float mi = ws_ml[(it0 + i) * 4 + h];
+        const float mi = load_dev(&ws_ml[(it0 + i) * 4 + h]);
         const float w = mi == kNegInf ? 0.0f : fast_exp2(mi - M2);
-        L2 = fmaf(ws_ml[(it0 + i) * 4 + 2 + h], w, L2);
-        A2 = fmaf(ws_acc[(it0 + i) * (2 * kHeadDim) + h * kHeadDim + j], w, A2);
+        L2 = fmaf(load_dev(&ws_ml[(it0 + i) * 4 + 2 + h]), w, L2);
+        A2 = fmaf(load_dev(&ws_acc[(it0 + i) * (2 * kHeadDim) + h * kHeadDim + j]), w, A2);
     }
     *ob = f2h(A2 / L2);
-    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) ticket_reset(ctr);
 }
 
 }  // namespace

@@ -199,34 +199,27 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attn_kernel(
         return;
     }
 
-    // Partial: [item][wave][n][128] unnormalised O, [item][wave][n] (m, l).
+    // Partial: [item][wave][n][128] unnormalised O, [item][wave][n] (m, l),
+    // published with device-scope stores (see stores_done_barrier).
     const int64_t slot_id = ((int64_t)item * kWaves + wave) * 32 + n;
     float* po = ws_o + slot_id * kHeadDim;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4)
-            *(float4v*)(po + db * 32 + 8 * q4 + 4 * g) =
-                (float4v){o[db][q4 * 4], o[db][q4 * 4 + 1], o[db][q4 * 4 + 2], o[db][q4 * 4 + 3]};
+        for (int i = 0; i < 16; ++i) store_dev(po + db * 32 + 8 * (i >> 2) + 4 * g + (i & 3), o[db][i]);
     if (g == 0) {
-        ws_ml[slot_id * 2] = m;
-        ws_ml[slot_id * 2 + 1] = lsum;
+        store_dev(&ws_ml[slot_id * 2], m);
+        store_dev(&ws_ml[slot_id * 2 + 1], lsum);
     }
-    __threadfence();
-    __syncthreads();
+    stores_done_barrier();
     uint32_t* ctr = &counters[kvh * P.nrb + rb];
-    if (tid == 0) {
-        const uint32_t prev =
-            __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == (uint32_t)(nsp - 1));
-    }
+    if (tid == 0) s_last = (ticket_add(ctr) == (uint32_t)(nsp - 1));
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
     const int it0 = kvh * P.items_per_kvh + P.sp_base[rb];
     float M = kNegInf;
     for (int i = 0; i < nsp; ++i)
-        M = fmaxf(M, ws_ml[(((int64_t)(it0 + i) * kWaves + wave) * 32 + n) * 2]);
+        M = fmaxf(M, load_dev(&ws_ml[(((int64_t)(it0 + i) * kWaves + wave) * 32 + n) * 2]));
     float Ls = 0.0f;
     float acc[4][16];
 #pragma unroll
@@ -235,18 +228,15 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attn_kernel(
         for (int e = 0; e < 16; ++e) acc[db][e] = 0.0f;
     for (int i = 0; i < nsp; ++i) {
         const int64_t sid = ((int64_t)(it0 + i) * kWaves + wave) * 32 + n;
-        const float mi = ws_ml[sid * 2];
+        const float mi = load_dev(&ws_ml[sid * 2]);
         const float w = mi == kNegInf ? 0.0f : fast_exp2(mi - M);
-        Ls = fmaf(ws_ml[sid * 2 + 1], w, Ls);
+        Ls = fmaf(load_dev(&ws_ml[sid * 2 + 1]), w, Ls);
         const float* pi = ws_o + sid * kHeadDim;
 #pragma unroll
         for (int db = 0; db < 4; ++db)
 #pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                const float4v v = *(const float4v*)(pi + db * 32 + 8 * q4 + 4 * g);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[db][q4 * 4 + e] = fmaf(v[e], w, acc[db][q4 * 4 + e]);
-            }
+            for (int e = 0; e < 16; ++e)
+                acc[db][e] = fmaf(load_dev(pi + db * 32 + 8 * (e >> 2) + 4 * g + (e & 3)), w, acc[db][e]);
     }
     if (row_ok) {
         const float inv = 1.0f / Ls;
@@ -260,7 +250,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attn_kernel(
                 *(half4v*)(orow + db * 32 + 8 * q4 + 4 * g) = h4;
             }
     }
-    if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) ticket_reset(ctr);
 }
 
 }  // namespace

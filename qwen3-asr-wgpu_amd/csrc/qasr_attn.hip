@@ -166,11 +166,12 @@ void free_prefill_ws(qasr_kv* kv) {
     kv->pws_items = 0;
 }
 
-// Decode workspace: every launch plans at most kMaxBatch entries with chunks of
-// >= 128 keys over <= cap keys.
+// Decode workspace: every launch plans at most kMaxBatch entries (a slot may
+// appear in several entries of qasr_decode_attn) with chunks of >= 128 keys
+// over <= cap keys.
 int alloc_decode_ws(qasr_kv* kv) {
     const int nkvh = kv->ctx->cfg.num_key_value_heads;
-    const int64_t items = (int64_t)std::min(kv->slots, qasr::kMaxBatch) * nkvh *
+    const int64_t items = (int64_t)qasr::kMaxBatch * nkvh *
                           ((kv->cap + qasr::kDecodeWgKeys - 1) / qasr::kDecodeWgKeys);
     HIP_TRY(hipMalloc(&kv->dws_acc, items * 2 * qasr::kHeadDim * sizeof(float)), "decode workspace");
     HIP_TRY(hipMalloc(&kv->dws_ml, items * 4 * sizeof(float)), "decode workspace");
