@@ -52,6 +52,45 @@ __device__ __forceinline__ float row_sum16(float x) {
     return x;
 }
 
+// Transposing reduction of 16 values over a 16-lane row: lane i of the row
+// ends with the row-wide sum of value index i.  Each step pairs the lane with
+// a partner in the other half of the current index bit (row_mirror: bit 3,
+// row_half_mirror: bit 2, quad_perm: bits 1 and 0), keeps the half of the
+// values whose index bit equals its own lane bit and adds the partner's copy
+// of them: 15 DPP adds and 30 selects instead of 64 DPP adds.
+__device__ __forceinline__ float row_reduce_transpose16(const float (&v)[16], int i) {
+    float w[8], x[4], y[2];
+    const bool b3 = i & 8, b2 = i & 4, b1 = i & 2, b0 = i & 1;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float keep = b3 ? v[k + 8] : v[k], send = b3 ? v[k] : v[k + 8];
+        w[k] = keep + dpp<kDppMirror>(send);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float keep = b2 ? w[k + 4] : w[k], send = b2 ? w[k] : w[k + 4];
+        x[k] = keep + dpp<kDppHalfMirror>(send);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const float keep = b1 ? x[k + 2] : x[k], send = b1 ? x[k] : x[k + 2];
+        y[k] = keep + dpp<kDppXor2>(send);
+    }
+    const float keep = b0 ? y[1] : y[0], send = b0 ? y[0] : y[1];
+    return keep + dpp<kDppXor1>(send);
+}
+
+// acc += p * f16 (low / high half of a packed dword), one v_fma_mix_f32 with a
+// single rounding (as fmaf(p, (float)h, acc)).  Written out so the packed
+// register feeds both halves through op_sel instead of being unpacked into
+// extra registers first.
+__device__ __forceinline__ void fma_mix_lo(float& acc, float p, uint32_t pk) {
+    asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[0,1,0]" : "+v"(acc) : "v"(p), "v"(pk));
+}
+__device__ __forceinline__ void fma_mix_hi(float& acc, float p, uint32_t pk) {
+    asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(acc) : "v"(p), "v"(pk));
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ---- publishing partial results to other workgroups ---------------------

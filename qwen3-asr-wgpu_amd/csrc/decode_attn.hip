@@ -7,21 +7,25 @@
 // query row, i.e. softmax(q.k_t * scale) . v over keys t < cur_len.
 //
 // Work decomposition (one launch for the whole batch):
-//   workgroup = (batch entry b, kv head, chunk of `chunk` keys), 4 waves.
+//   workgroup = (batch entry b, kv head, chunk of keys), W waves.  Chunk sizes
+//   are planned per entry on the host so every workgroup streams about the
+//   same number of keys whatever the ragged lengths.
 //   Both q heads of the kv head (GQA 2:1) are computed from one K/V read.
-//   A wave pass covers 32 keys: 8 dwordx4 loads of K and 8 of V per lane, each
-//   load instruction reading 1 KiB contiguous (4 keys x 256 B, lane l -> key
-//   l/16, dims (l%16)*8..+8), so every instruction is fully coalesced.  Keys
-//   past the chunk end load a clamped (valid) row and are masked to -inf.
-//   The next pass's K loads are issued right after this pass's scores, and its
-//   V loads right after this pass's P.V, so memory stays busy during compute.
-//   q.k: v_dot2_f32_f16 on the lane's 8 dims, then a 16-lane DPP all-reduce
-//   inside the row (no LDS).  Softmax is online per 16-lane row (exp2 domain),
-//   P.V accumulates in f32 registers (v_fma_mix).  Rows and waves merge through
-//   LDS.  When an entry needs more than one chunk, each workgroup publishes
-//   its partial (max, sum, unnormalised output) with device-scope stores and
-//   the last one to arrive (ticket) merges them: no second launch and no
-//   L2-wide cache maintenance.
+//   A wave pass covers 32 keys: 8 dwordx4 buffer loads of K and 8 of V per
+//   lane, each load instruction reading 1 KiB contiguous (4 keys x 256 B,
+//   lane l -> key l/16, dims (l%16)*8..+8), so every instruction is fully
+//   coalesced.  The buffer resources end at the chunk's last key, so the
+//   hardware range check returns zeros past it (those scores are masked).
+//   q.k: v_dot2_f32_f16 on the lane's 8 dims, then a transposing 16-lane DPP
+//   reduction that leaves each lane with one (key, head) score.  Softmax is
+//   online per (16-lane row, head) in the exp2 domain; the row's 16
+//   probabilities reach the V layout through LDS and P.V accumulates in f32
+//   (v_fma_mix on packed f16).  The 4W rows of the workgroup merge through
+//   one LDS pass.
+//   When an entry needs more than one chunk, each workgroup publishes its
+//   partial (max, sum, unnormalised output) with device-scope stores and the
+//   last one to arrive (ticket) merges them, issuing all its loads at once:
+//   no second launch and no L2-wide cache maintenance.
 //
 // Fused variant (stage (a) + (b)): the workgroup recomputes its two q heads
 // from the raw qkv row (bit-identical to the stage-(a) kernel); the workgroup
@@ -36,6 +40,10 @@ namespace qasr {
 
 namespace {
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kNegInf = -__builtin_inff();
+
 __device__ __forceinline__ float dot8(const H8& a, const H8& b) {
     float s = 0.0f;
     s = __builtin_amdgcn_fdot2(a.h2[0], b.h2[0], s, false);
@@ -45,35 +53,41 @@ __device__ __forceinline__ float dot8(const H8& a, const H8& b) {
     return s;
 }
 
-constexpr float kNegInf = -__builtin_inff();
+// Buffer resource over `bytes` bytes at `p` (raw buffer, gfx9 data format).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
 
-// One wave pass of 8 loads (32 keys) of K or V starting at key t0; keys at or
-// past `kend` are clamped to row kend-1 (valid, masked later).
-__device__ __forceinline__ void load_pass(const f16* __restrict__ base, int t0, int kend, int row,
-                                          int seg, H8 (&r)[8]) {
+// One wave pass (32 keys from t0) of K or V: 8 x 16 B per lane.
+__device__ __forceinline__ void load_pass(__amdgpu_buffer_rsrc_t r, int t0, int row, int seg,
+                                          H8 (&x)[8]) {
+    const int voff = (t0 + row) * (kHeadDim * 2) + seg * 16;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
-        const int key = min(t0 + kk * 4 + row, kend - 1);
-        r[kk].u = *(const uint4*)(base + (int64_t)key * kHeadDim + seg * 8);
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + kk * 1024, 0, 0);
+        x[kk].u = make_uint4(v.x, v.y, v.z, v.w);
     }
 }
 
-template <bool FUSED>
-__global__ __launch_bounds__(kDecodeWaves * 64) void decode_attn_kernel(
+template <bool FUSED, int W>
+__global__ __launch_bounds__(W * 64)
+__attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kernel(
     CacheGeom g, int layer, DecodePlan P, const f16* __restrict__ qin,
     const f16* __restrict__ q_gain, const f16* __restrict__ k_gain,
     const f16* __restrict__ cos_tab, const f16* __restrict__ sin_tab, f16* __restrict__ out,
     float* __restrict__ ws_acc, float* __restrict__ ws_ml, uint32_t* __restrict__ counters) {
-    constexpr int kRows = kDecodeWaves * 4;  // 16-lane rows per workgroup
+    constexpr int kWgKeys = W * kDecodeTileKeys;  // keys per round of all waves
     __shared__ H8 s_q[2][16];
     __shared__ H8 s_knew[16];
     __shared__ H8 s_vnew[16];
     __shared__ __attribute__((aligned(16))) f16 s_raw[4][kHeadDim];  // q0, q1, k, v raw heads
     __shared__ __attribute__((aligned(16))) f16 s_tab[4][kHeadDim];  // q gain, k gain, cos, sin
     __shared__ float s_inv[3];
-    __shared__ float s_m[kRows][2];
-    __shared__ float s_l[kRows][2];
-    __shared__ float s_acc[kRows][2][kHeadDim];
+    __shared__ float s_p[W][64];
+    __shared__ float s_wm[4 * W][2];
+    __shared__ float s_wl[4 * W][2];
+    __shared__ float s_wa[4 * W][2][kHeadDim];
+    __shared__ float s_ml[kDecodeMaxChunksPerEntry][4];
     __shared__ int s_last;
 
     const int wg = blockIdx.x;
@@ -93,16 +107,22 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_attn_kernel(
         b = lo;
     }
     const int L = P.len[b];
-    const int nch = (L + P.chunk - 1) / P.chunk;
+    const int chunk = P.chunk[b];
+    const int nch = (L + chunk - 1) / chunk;
     const int rel = wg - P.wg_base[b];
     const int kvh = rel / nch;
     const int c = rel - kvh * nch;
-    const int key0 = c * P.chunk;
-    const int key1 = min(key0 + P.chunk, L);
+    const int key0 = c * chunk;
+    const int key1 = min(key0 + chunk, L);
+    const int nkeys = key1 - key0;
     const int nqh = P.nqh;
     const int h0 = kvh * kRep;
     f16* Kc = g.base + P.slot[b] * g.slot_stride + layer * g.layer_stride + kvh * g.head_stride;
     f16* Vc = Kc + g.kv_stride;
+    // Resources start at the chunk's first key and end at its last.
+    const int rbytes = nkeys * (kHeadDim * 2);
+    const __amdgpu_buffer_rsrc_t kres = make_rsrc(Kc + (int64_t)key0 * kHeadDim, rbytes);
+    const __amdgpu_buffer_rsrc_t vres = make_rsrc(Vc + (int64_t)key0 * kHeadDim, rbytes);
 
     // Raw inputs of the fused prologue are requested before the first K/V pass
     // so that waiting for them does not wait for the pass.
@@ -125,27 +145,32 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_attn_kernel(
         }
     }
 
-    H8 kr[8], vr[8];
-    int t0 = key0 + wave * kDecodeTileKeys;
-    load_pass(Kc, t0, key1, row, seg, kr);
-    load_pass(Vc, t0, key1, row, seg, vr);
+    // Two pass buffers per wave: while one pass is computed the next one's
+    // loads are in flight.  Passes past the chunk fall outside the buffer
+    // range: their loads return zeros without touching memory.
+    H8 ka[8], va[8], kb[8], vb[8];
+    const int tw = wave * kDecodeTileKeys;  // this wave's first key, relative to key0
+    load_pass(kres, tw, row, seg, ka);
+    load_pass(vres, tw, row, seg, va);
 
     H8 q0, q1;
     if constexpr (FUSED) {
         __syncthreads();
         if (tid < 3 && (tid < 2 || owner)) s_inv[tid] = head_inv_rms_serial(s_raw[tid], P.eps);
         __syncthreads();
-        const int h = tid >> 7, j = tid & 127;
-        ((f16*)s_q[h])[j] = rope_elem(s_raw[h], s_tab[0], s_tab[2], s_tab[3], s_inv[h], j);
-        if (owner) {
-            if (h == 0) {
-                const f16 kv = rope_elem(s_raw[2], s_tab[1], s_tab[2], s_tab[3], s_inv[2], j);
-                ((f16*)s_knew)[j] = kv;
-                Kc[(int64_t)pos * kHeadDim + j] = kv;
-            } else {
-                const f16 vv = s_raw[3][j];
-                ((f16*)s_vnew)[j] = vv;
-                Vc[(int64_t)pos * kHeadDim + j] = vv;
+        if (tid < 256) {
+            const int h = tid >> 7, j = tid & 127;
+            ((f16*)s_q[h])[j] = rope_elem(s_raw[h], s_tab[0], s_tab[2], s_tab[3], s_inv[h], j);
+            if (owner) {
+                if (h == 0) {
+                    const f16 kv = rope_elem(s_raw[2], s_tab[1], s_tab[2], s_tab[3], s_inv[2], j);
+                    ((f16*)s_knew)[j] = kv;
+                    Kc[(int64_t)pos * kHeadDim + j] = kv;
+                } else {
+                    const f16 vv = s_raw[3][j];
+                    ((f16*)s_vnew)[j] = vv;
+                    Vc[(int64_t)pos * kHeadDim + j] = vv;
+                }
             }
         }
         __syncthreads();
@@ -157,101 +182,127 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_attn_kernel(
         q1.u = *(const uint4*)(qb + kHeadDim);
     }
 
-    float m0 = kNegInf, m1 = kNegInf, l0 = 0.0f, l1 = 0.0f;
+    load_pass(kres, tw + kWgKeys, row, seg, kb);
+    load_pass(vres, tw + kWgKeys, row, seg, vb);
+
+    // Per 16-lane row: running (max, sum) of the head given by the lane's
+    // parity (replicated over the 8 lanes of that parity), and the lane's 8
+    // output dims of both heads.
+    float m_run = kNegInf, l_run = 0.0f;
     float a0[8], a1[8];
 #pragma unroll
     for (int d = 0; d < 8; ++d) a0[d] = a1[d] = 0.0f;
-
+    const bool odd = seg & 1;
+    float* s_pw = &s_p[wave][0];
     const float sl2 = P.scale_log2;
-    for (; t0 < key1; t0 += kDecodeWgKeys) {
+    const int new_rel = pos - key0;  // the appended key, relative (owner only)
+
+    auto process = [&](H8 (&kr)[8], H8 (&vr)[8], int t0) {
         if constexpr (FUSED) {
             if (owner) {
 #pragma unroll
                 for (int kk = 0; kk < 8; ++kk) {
-                    if (t0 + kk * 4 + row == pos) {
+                    if (t0 + kk * 4 + row == new_rel) {
                         kr[kk] = s_knew[seg];
                         vr[kk] = s_vnew[seg];
                     }
                 }
             }
         }
-        float s0[8], s1[8];
+        // Partial dots of the lane's 8 dims, value index kk*2 + head; the
+        // transposing row reduction leaves lane seg of row `row` with the full
+        // score of key t0 + 4*(seg>>1) + row, head seg&1.
+        float v[16];
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
-            s0[kk] = row_sum16(dot8(q0, kr[kk])) * sl2;
-            s1[kk] = row_sum16(dot8(q1, kr[kk])) * sl2;
-            if (t0 + kk * 4 + row >= key1) s0[kk] = s1[kk] = kNegInf;
+            v[2 * kk] = dot8(q0, kr[kk]);
+            v[2 * kk + 1] = dot8(q1, kr[kk]);
         }
-        const int tn = t0 + kDecodeWgKeys;
-        if (tn < key1) load_pass(Kc, tn, key1, row, seg, kr);
-        float mt0 = s0[0], mt1 = s1[0];
-#pragma unroll
-        for (int kk = 1; kk < 8; ++kk) {
-            mt0 = fmaxf(mt0, s0[kk]);
-            mt1 = fmaxf(mt1, s1[kk]);
-        }
-        const float mn0 = fmaxf(m0, mt0), mn1 = fmaxf(m1, mt1);
-        const float mu0 = mn0 == kNegInf ? 0.0f : mn0;
-        const float mu1 = mn1 == kNegInf ? 0.0f : mn1;
-        const float al0 = fast_exp2(m0 - mu0), al1 = fast_exp2(m1 - mu1);
-        m0 = mn0;
-        m1 = mn1;
-        float ps0 = 0.0f, ps1 = 0.0f;
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-            s0[kk] = fast_exp2(s0[kk] - mu0);
-            s1[kk] = fast_exp2(s1[kk] - mu1);
-            ps0 += s0[kk];
-            ps1 += s1[kk];
-        }
-        l0 = l0 * al0 + ps0;
-        l1 = l1 * al1 + ps1;
+        const float sc = row_reduce_transpose16(v, seg);
+        const int my_key = t0 + 4 * (seg >> 1) + row;
+        const float sv = my_key < nkeys ? sc * sl2 : kNegInf;
+        // Online softmax per (row, head): max / sum over the 8 lanes of the
+        // lane's parity.
+        float mt = fmaxf(sv, dpp<kDppXor2>(sv));
+        mt = fmaxf(mt, dpp<kDppRor4>(mt));
+        mt = fmaxf(mt, dpp<kDppRor8>(mt));
+        const float mn = fmaxf(m_run, mt);
+        const float mu = mn == kNegInf ? 0.0f : mn;
+        const float alpha = fast_exp2(m_run - mu);
+        const float pv = fast_exp2(sv - mu);
+        m_run = mn;
+        float ps = pv + dpp<kDppXor2>(pv);
+        ps += dpp<kDppRor4>(ps);
+        ps += dpp<kDppRor8>(ps);
+        l_run = l_run * alpha + ps;
+        // Broadcast the row's 16 probabilities to the V layout through LDS.
+        s_pw[lane] = pv;
+        const float alpha_x = dpp<kDppXor1>(alpha);  // the other head's factor
+        const float al0 = odd ? alpha_x : alpha, al1 = odd ? alpha : alpha_x;
 #pragma unroll
         for (int d = 0; d < 8; ++d) {
             a0[d] *= al0;
             a1[d] *= al1;
         }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
+            const float2 p2 = *(const float2*)&s_pw[16 * row + 2 * kk];
+            const uint32_t w4[4] = {vr[kk].u.x, vr[kk].u.y, vr[kk].u.z, vr[kk].u.w};
 #pragma unroll
-            for (int d = 0; d < 8; ++d) {
-                const float v = h2f(vr[kk].e[d]);
-                a0[d] = fmaf(s0[kk], v, a0[d]);
-                a1[d] = fmaf(s1[kk], v, a1[d]);
+            for (int e = 0; e < 4; ++e) {
+                fma_mix_lo(a0[2 * e], p2.x, w4[e]);
+                fma_mix_lo(a1[2 * e], p2.y, w4[e]);
+                fma_mix_hi(a0[2 * e + 1], p2.x, w4[e]);
+                fma_mix_hi(a1[2 * e + 1], p2.y, w4[e]);
             }
         }
-        if (tn < key1) load_pass(Vc, tn, key1, row, seg, vr);
+        __builtin_amdgcn_wave_barrier();
+    };
+
+    for (int t0 = tw; t0 < nkeys; t0 += 2 * kWgKeys) {
+        process(ka, va, t0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_pass(kres, t0 + 2 * kWgKeys, row, seg, ka);
+        load_pass(vres, t0 + 2 * kWgKeys, row, seg, va);
+        if (t0 + kWgKeys < nkeys) process(kb, vb, t0 + kWgKeys);
+        __builtin_amdgcn_sched_barrier(0);
+        load_pass(kres, t0 + 3 * kWgKeys, row, seg, kb);
+        load_pass(vres, t0 + 3 * kWgKeys, row, seg, vb);
     }
 
-    // Merge the 16 rows of the workgroup (each row saw a disjoint key subset).
-    const int r16 = wave * 4 + row;
-    if (seg == 0) {
-        s_m[r16][0] = m0;
-        s_m[r16][1] = m1;
-        s_l[r16][0] = l0;
-        s_l[r16][1] = l1;
-    }
+    // Merge the 4W rows of the workgroup through LDS: every row holds the
+    // (max, sum) of the head of the lane's parity and 8 dims of both heads.
+    {
+        const int r = wave * 4 + row;
+        if (seg < 2) {  // lane 0 of the row holds head 0's (m, l), lane 1 head 1's
+            s_wm[r][seg] = m_run;
+            s_wl[r][seg] = l_run;
+        }
 #pragma unroll
-    for (int d = 0; d < 8; ++d) {
-        s_acc[r16][0][seg * 8 + d] = a0[d];
-        s_acc[r16][1][seg * 8 + d] = a1[d];
+        for (int d = 0; d < 8; ++d) {
+            s_wa[r][0][seg * 8 + d] = a0[d];
+            s_wa[r][1][seg * 8 + d] = a1[d];
+        }
     }
     __syncthreads();
+    if (tid >= 256) return;  // 256 threads: one per (head, dim)
     const int h = tid >> 7, j = tid & 127;
     float M = kNegInf;
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) M = fmaxf(M, s_m[r][h]);
+    for (int r = 0; r < 4 * W; ++r) M = fmaxf(M, s_wm[r][h]);
     float Ls = 0.0f, A = 0.0f;
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-        const float mr = s_m[r][h];
-        const float w = mr == kNegInf ? 0.0f : fast_exp2(mr - M);
-        Ls = fmaf(s_l[r][h], w, Ls);
-        A = fmaf(s_acc[r][h][j], w, A);
+    for (int r = 0; r < 4 * W; ++r) {
+        const float mr = s_wm[r][h];
+        const float f = mr == kNegInf ? 0.0f : fast_exp2(mr - M);
+        Ls = fmaf(s_wl[r][h], f, Ls);
+        A = fmaf(s_wa[r][h][j], f, A);
     }
-    f16* ob = out + (int64_t)b * nqh * kHeadDim + (h0 + h) * kHeadDim + j;
+    f16* ob = out + (int64_t)b * nqh * kHeadDim + h0 * kHeadDim;
     if (nch == 1) {
-        *ob = f2h(A / Ls);
+        ob[h * kHeadDim + j] = f2h(A / Ls);
         return;
     }
 
@@ -260,42 +311,88 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_attn_kernel(
         store_dev(&ws_ml[(int64_t)wg * 4 + h], M);
         store_dev(&ws_ml[(int64_t)wg * 4 + 2 + h], Ls);
     }
-    stores_done_barrier();
+    stores_done_barrier();  // waves past thread 256 have exited: s_barrier counts live waves
     uint32_t* ctr = &counters[b * g.nkvh + kvh];
     if (tid == 0) s_last = (ticket_add(ctr) == (uint32_t)(nch - 1));
     __syncthreads();
     if (!s_last) return;
+
+    // Last arrival: merge the nch partials of (b, kv head).  The (m, l) of
+    // every chunk (to LDS) and this thread's first 16 partial outputs are
+    // requested together, so up to 32 chunks merge in one memory round trip.
     const int64_t it0 = P.wg_base[b] + kvh * nch;
-    float M2 = kNegInf;
-    for (int i = 0; i < nch; ++i) M2 = fmaxf(M2, load_dev(&ws_ml[(it0 + i) * 4 + h]));
-    float L2 = 0.0f, A2 = 0.0f;
-    for (int i = 0; i < nch; ++i) {
-        const float mi = load_dev(&ws_ml[(it0 + i) * 4 + h]);
-        const float w = mi == kNegInf ? 0.0f : fast_exp2(mi - M2);
-        L2 = fmaf(load_dev(&ws_ml[(it0 + i) * 4 + 2 + h]), w, L2);
-        A2 = fmaf(load_dev(&ws_acc[(it0 + i) * (2 * kHeadDim) + h * kHeadDim + j]), w, A2);
+    if (tid < nch) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) s_ml[tid][k] = load_dev(&ws_ml[(it0 + tid) * 4 + k]);
     }
-    *ob = f2h(A2 / L2);
+    constexpr int kBatch = 32;
+    float x[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+        x[u] = u < nch ? load_dev(&ws_acc[(it0 + u) * (2 * kHeadDim) + h * kHeadDim + j]) : 0.0f;
+    __syncthreads();
+    float Mh = kNegInf;
+    for (int i = 0; i < nch; ++i) Mh = fmaxf(Mh, s_ml[i][h]);
+    float lsum = 0.0f, acc = 0.0f;
+    for (int i0 = 0; i0 < nch; i0 += kBatch) {
+        if (i0 > 0) {
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                x[u] = i0 + u < nch
+                           ? load_dev(&ws_acc[(it0 + i0 + u) * (2 * kHeadDim) + h * kHeadDim + j])
+                           : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            if (i0 + u < nch) {
+                const float mi = s_ml[i0 + u][h];
+                const float w = mi == kNegInf ? 0.0f : fast_exp2(mi - Mh);
+                lsum = fmaf(s_ml[i0 + u][2 + h], w, lsum);
+                acc = fmaf(x[u], w, acc);
+            }
+        }
+    }
+    ob[h * kHeadDim + j] = f2h(acc / lsum);
     if (tid == 0) ticket_reset(ctr);
+}
+
+template <bool FUSED>
+hipError_t launch_w(int waves, const dim3& grid, hipStream_t stream, const CacheGeom& g,
+                    int layer, const DecodePlan& P, const f16* qin, const f16* q_gain,
+                    const f16* k_gain, const f16* cos_tab, const f16* sin_tab, f16* out,
+                    const DecodeWs& ws) {
+    switch (waves) {
+        case 4:
+            hipLaunchKernelGGL((decode_attn_kernel<FUSED, 4>), grid, dim3(4 * 64), 0, stream, g,
+                               layer, P, qin, q_gain, k_gain, cos_tab, sin_tab, out, ws.acc,
+                               ws.ml, ws.counters);
+            break;
+        case 8:
+            hipLaunchKernelGGL((decode_attn_kernel<FUSED, 8>), grid, dim3(8 * 64), 0, stream, g,
+                               layer, P, qin, q_gain, k_gain, cos_tab, sin_tab, out, ws.acc,
+                               ws.ml, ws.counters);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_decode_attn(bool fused, const CacheGeom& g, int layer, const DecodePlan& P,
-                              int total_wgs, const f16* q_or_qkv, const f16* q_gain,
-                              const f16* k_gain, const f16* cos_tab, const f16* sin_tab,
-                              f16* out, const DecodeWs& ws, hipStream_t stream) {
+hipError_t launch_decode_attn(bool fused, int waves, const CacheGeom& g, int layer,
+                              const DecodePlan& P, int total_wgs, const f16* q_or_qkv,
+                              const f16* q_gain, const f16* k_gain, const f16* cos_tab,
+                              const f16* sin_tab, f16* out, const DecodeWs& ws,
+                              hipStream_t stream) {
     if (total_wgs <= 0) return hipSuccess;
     if (total_wgs > ws.items) return hipErrorInvalidValue;
-    const dim3 grid(total_wgs), block(kDecodeWaves * 64);
+    const dim3 grid(total_wgs);
     if (fused)
-        hipLaunchKernelGGL(decode_attn_kernel<true>, grid, block, 0, stream, g, layer, P, q_or_qkv,
-                           q_gain, k_gain, cos_tab, sin_tab, out, ws.acc, ws.ml, ws.counters);
-    else
-        hipLaunchKernelGGL(decode_attn_kernel<false>, grid, block, 0, stream, g, layer, P,
-                           q_or_qkv, q_gain, k_gain, cos_tab, sin_tab, out, ws.acc, ws.ml,
-                           ws.counters);
-    return hipGetLastError();
+        return launch_w<true>(waves, grid, stream, g, layer, P, q_or_qkv, q_gain, k_gain, cos_tab,
+                              sin_tab, out, ws);
+    return launch_w<false>(waves, grid, stream, g, layer, P, q_or_qkv, q_gain, k_gain, cos_tab,
+                           sin_tab, out, ws);
 }
 
 }  // namespace qasr

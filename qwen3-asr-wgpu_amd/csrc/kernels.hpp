@@ -33,18 +33,22 @@ struct SegPlan {
 // Workgroups of entry b are wg_base[b] .. wg_base[b+1]-1, kv-head major.
 struct DecodePlan {
     int32_t batch;
-    int32_t chunk;  // keys per workgroup, multiple of kDecodeWgKeys
     int32_t nqh;
     float scale_log2;  // softmax scale * log2(e): scores live in the exp2 domain
     float eps;
     int32_t slot[kMaxBatch];
-    int32_t len[kMaxBatch];  // keys attended; the fused step appends key len-1
+    int32_t len[kMaxBatch];    // keys attended; the fused step appends key len-1
+    int32_t chunk[kMaxBatch];  // keys per workgroup of this entry
     int32_t wg_base[kMaxBatch + 1];
 };
 
-constexpr int kDecodeWaves = 4;
-constexpr int kDecodeTileKeys = 32;                           // keys per wave pass
-constexpr int kDecodeWgKeys = kDecodeWaves * kDecodeTileKeys;  // 128
+constexpr int kDecodeWaves = 4;       // default workgroup size (waves)
+constexpr int kDecodeWavesPerEU = 2;  // occupancy target: <= 256 VGPRs (two pass buffers)
+constexpr int kDecodeTileKeys = 32;   // keys per wave pass
+constexpr int kDecodeMaxChunksPerEntry = 256;
+constexpr int kDecodeTargetWgs = 512;   // 2 resident 4-wave workgroups on each of 256 CUs
+constexpr int kDecodeMinChunk = 64;
+constexpr int kDecodeMaxItems = 8192;   // >= 4096 target + kMaxBatch * nkvh rounding slack
 
 // Split-K workspace of one launch: per workgroup the unnormalised partial
 // output of both q heads (2 x 128 f32) and (max, sum) per head, plus one
@@ -62,10 +66,12 @@ hipError_t launch_norm_rope_append(const CacheGeom& g, int layer, const SegPlan&
                                    const f16* cos_tab, const f16* sin_tab, f16* q_out,
                                    hipStream_t stream);
 
-hipError_t launch_decode_attn(bool fused, const CacheGeom& g, int layer, const DecodePlan& P,
-                              int total_wgs, const f16* q_or_qkv, const f16* q_gain,
-                              const f16* k_gain, const f16* cos_tab, const f16* sin_tab,
-                              f16* out, const DecodeWs& ws, hipStream_t stream);
+// waves: workgroup size in waves (4 or 8).
+hipError_t launch_decode_attn(bool fused, int waves, const CacheGeom& g, int layer,
+                              const DecodePlan& P, int total_wgs, const f16* q_or_qkv,
+                              const f16* q_gain, const f16* k_gain, const f16* cos_tab,
+                              const f16* sin_tab, f16* out, const DecodeWs& ws,
+                              hipStream_t stream);
 
 struct PrefillArgs {
     const f16* q;   // [s][nqh*128], roped

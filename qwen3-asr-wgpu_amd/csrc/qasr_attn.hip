@@ -166,13 +166,11 @@ void free_prefill_ws(qasr_kv* kv) {
     kv->pws_items = 0;
 }
 
-// Decode workspace: every launch plans at most kMaxBatch entries (a slot may
-// appear in several entries of qasr_decode_attn) with chunks of >= 128 keys
-// over <= cap keys.
+// Decode workspace: one partial per workgroup of a launch (the planner keeps a
+// launch under kDecodeMaxItems workgroups) and one ticket per (entry, kv head).
 int alloc_decode_ws(qasr_kv* kv) {
     const int nkvh = kv->ctx->cfg.num_key_value_heads;
-    const int64_t items = (int64_t)qasr::kMaxBatch * nkvh *
-                          ((kv->cap + qasr::kDecodeWgKeys - 1) / qasr::kDecodeWgKeys);
+    const int64_t items = qasr::kDecodeMaxItems;
     HIP_TRY(hipMalloc(&kv->dws_acc, items * 2 * qasr::kHeadDim * sizeof(float)), "decode workspace");
     HIP_TRY(hipMalloc(&kv->dws_ml, items * 4 * sizeof(float)), "decode workspace");
     const size_t cbytes = (size_t)qasr::kMaxBatch * nkvh * sizeof(uint32_t);
@@ -198,21 +196,28 @@ int ensure_prefill_ws(qasr_kv* kv, int64_t items) {
     return QASR_OK;
 }
 
-// Keys per decode workgroup: the largest power-of-two multiple of 128 that
-// still leaves >= kDecodeMinWgs workgroups, so that short batches spread over
-// all 256 CUs and long ones avoid merge traffic.
-int pick_decode_chunk(const int32_t* len, int n, int nkvh) {
-    const int forced = env_int("QASR_DECODE_CHUNK", 0);
-    if (forced >= qasr::kDecodeWgKeys && forced % qasr::kDecodeWgKeys == 0) return forced;
-    const int64_t min_wgs = env_int("QASR_DECODE_MIN_WGS", 2048);
-    auto wgs = [&](int chunk) {
-        int64_t t = 0;
-        for (int i = 0; i < n; ++i) t += (int64_t)nkvh * ((len[i] + chunk - 1) / chunk);
-        return t;
-    };
-    int chunk = qasr::kDecodeWgKeys;
-    while (chunk < 2048 && wgs(chunk * 2) >= min_wgs) chunk *= 2;
-    return chunk;
+// Decode launch plan: every workgroup should stream about the same number of
+// keys whatever the ragged lengths, and one launch should be about one round
+// of resident workgroups (4 per CU on 256 CUs).  Entry b is cut into
+// n_b = round(len_b / t) chunks with t = total keys / target workgroups, each
+// chunk rounded up to whole 32-key wave passes and at least kMinChunk keys.
+void plan_decode_chunks(qasr::DecodePlan& P, int nkvh) {
+    const int target = std::max(1, std::min(env_int("QASR_DECODE_WGS", qasr::kDecodeTargetWgs), 4096));
+    const int min_chunk = std::max(32, env_int("QASR_DECODE_MIN_CHUNK", qasr::kDecodeMinChunk));
+    int64_t total = 0;
+    for (int i = 0; i < P.batch; ++i) total += P.len[i];
+    const int64_t t = std::max<int64_t>(min_chunk, (total * nkvh + target - 1) / target);
+    P.wg_base[0] = 0;
+    for (int i = 0; i < P.batch; ++i) {
+        const int L = P.len[i];
+        int64_t n = std::max<int64_t>(1, (L + t / 2) / t);
+        n = std::min<int64_t>(n, qasr::kDecodeMaxChunksPerEntry);
+        int chunk = (int)((L + n - 1) / n);
+        chunk = std::max(min_chunk, (chunk + qasr::kDecodeTileKeys - 1) / qasr::kDecodeTileKeys *
+                                        qasr::kDecodeTileKeys);
+        P.chunk[i] = chunk;
+        P.wg_base[i + 1] = P.wg_base[i] + nkvh * ((L + chunk - 1) / chunk);
+    }
 }
 
 int check_common(qasr_ctx* ctx, qasr_kv* kv, int layer) {
@@ -244,13 +249,11 @@ int run_decode(bool fused, qasr_ctx* ctx, qasr_kv* kv, int layer, int batch, con
             P.slot[i] = slots ? slots[b0 + i] : b0 + i;
             P.len[i] = lens[b0 + i];
         }
-        P.chunk = pick_decode_chunk(P.len, nb, nkvh);
-        P.wg_base[0] = 0;
-        for (int i = 0; i < nb; ++i)
-            P.wg_base[i + 1] = P.wg_base[i] + nkvh * ((P.len[i] + P.chunk - 1) / P.chunk);
+        plan_decode_chunks(P, nkvh);
         const f16* qp = (const f16*)qin + b0 * in_row;
         f16* op = (f16*)out + b0 * out_row;
-        hipError_t e = qasr::launch_decode_attn(fused, g, layer, P, P.wg_base[nb], qp,
+        const int waves = env_int("QASR_DECODE_WAVES", qasr::kDecodeWaves);
+        hipError_t e = qasr::launch_decode_attn(fused, waves, g, layer, P, P.wg_base[nb], qp,
                                                 (const f16*)q_gain, (const f16*)k_gain, ctx->cos,
                                                 ctx->sin, op, ws, (hipStream_t)stream);
         if (e != hipSuccess) return hip_fail(e, "decode attention launch");
