@@ -12,49 +12,105 @@
 // Work item = (kv head, block of 64 query rows, split of the key range).
 // 4 waves: wave w takes q head 2*kvh + (w&1) and rows (w>>1)*32..+32 of the
 // block, so both q heads of a kv head share each K/V tile staged in LDS.
+// Items are laid out kv-head minor (blockIdx % nkvh = kv head): with 8 kv
+// heads and workgroups dealt round-robin to the 8 XCDs, every row block and
+// split of one kv head runs on the same XCD and reuses its K/V through that
+// XCD's L2.
 // Each wave computes S^T = K Q^T (keys on the MFMA M axis, queries on N), so a
 // lane owns one query column: row max / row sum need one cross-half shuffle,
 // and the probabilities are already in the B-operand layout of O^T += V^T P^T.
-// V is transposed into LDS ([dim][key]) while it is staged.
-// When the key range of a row block is split, each item writes its partial
-// (max, sum, unnormalised O) and the last to arrive merges (agent-scope
-// ticket), as in the decode kernel.
-
-#include "kernels.hpp"
+// K/V tiles of 64 keys are double-buffered in LDS (V transposed to [dim][key],
+// key columns XOR-swizzled per 8 dims, while it is stored): the next tile's global loads (buffer loads whose range
+// ends at the row block's last key, so the tail reads zeros) are in flight
+// while the current tile's MFMAs run, with one barrier per tile.  Only tiles
+// that straddle the diagonal are masked, and O is rescaled only when a row
+// max moved.
+// When the key range of a row block is split, each item publishes its partial
+// (max, sum, unnormalised O) with device-scope stores and the last to arrive
+// merges (ticket), as in the decode kernel.
 
 #include <algorithm>
+
+#include "kernels.hpp"
 
 namespace qasr {
 
 namespace {
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kWaves = 4;
-constexpr int kRowsPerBlock = 64;
+constexpr int kThreads = kWaves * 64;
+constexpr int kRowsPerBlock = kPrefillRows;
 constexpr int kTileKeys = 64;
-constexpr int kKPad = kHeadDim + 8;     // Ks row stride (halves)
-constexpr int kVPad = kTileKeys + 8;    // Vt row stride (halves)
+constexpr int kKPad = kHeadDim + 8;   // Ks row stride (halves)
+constexpr int kVPad = kTileKeys + 8;  // Vt row stride (halves)
+constexpr int kKsHalves = kTileKeys * kKPad;
+constexpr int kVtHalves = kHeadDim * kVPad;
 constexpr float kNegInf = -__builtin_inff();
 
 __device__ __forceinline__ float16v mfma32(const half8v& a, const half8v& b, const float16v& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-__global__ __launch_bounds__(kWaves * 64, 2) void prefill_attn_kernel(
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+}
+
+// One 64-key tile of K and V: 4 + 4 dwordx4 per thread (thread t, chunk c
+// covers key (c*256+t)/16, dims ((c*256+t)%16)*8..+8).
+struct TileRegs {
+    uint4 k[4];
+    uint4 v[4];
+};
+
+__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
+                                          int k0, int tid, TileRegs& t) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int off = (k0 * kHeadDim + (c * kThreads + tid) * 8) * 2;
+        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0);
+        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0);
+        t.k[c] = make_uint4(a.x, a.y, a.z, a.w);
+        t.v[c] = make_uint4(b.x, b.y, b.z, b.w);
+    }
+}
+
+// V^T column of (dim, key): the key XOR 4*((dim/8) % 16).  The 16 lanes that
+// store one key's dims 8j+e then hit 16 different banks (the plain layout
+// put them all in one bank), and 4-key groups stay contiguous for the 8-byte
+// operand reads.
+__device__ __forceinline__ int vt_col(int dim, int key) { return key ^ (4 * ((dim >> 3) & 15)); }
+
+__device__ __forceinline__ void store_tile(const TileRegs& t, f16* Ks, f16* Vt, int tid) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int idx = c * kThreads + tid;
+        const int key = idx >> 4, dseg = (idx & 15) * 8;
+        *(uint4*)&Ks[key * kKPad + dseg] = t.k[c];
+        H8 v;
+        v.u = t.v[c];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) Vt[(dseg + e) * kVPad + vt_col(dseg + e, key)] = v.e[e];
+    }
+}
+
+__global__ __launch_bounds__(kThreads, 2) void prefill_attn_kernel(
     PrefillArgs a, PrefillPlan P, float* __restrict__ ws_o, float* __restrict__ ws_ml,
     uint32_t* __restrict__ counters) {
-    __shared__ __attribute__((aligned(16))) f16 Ks[kTileKeys * kKPad];
-    __shared__ __attribute__((aligned(16))) f16 Vt[kHeadDim * kVPad];
+    __shared__ __attribute__((aligned(16))) f16 Ks[2][kKsHalves];
+    __shared__ __attribute__((aligned(16))) f16 Vt[2][kVtHalves];
     __shared__ int s_last;
 
-    const int item = blockIdx.x;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int n = lane & 31;  // query column within the wave's 32 rows
     const int g = lane >> 5;  // k-slot group of the MFMA operands
 
-    const int kvh = item / P.items_per_kvh;
-    const int rem = item - kvh * P.items_per_kvh;
+    const int kvh = blockIdx.x % a.nkvh;
+    const int rem = blockIdx.x / a.nkvh;
+    const int item = kvh * P.items_per_kvh + rem;  // canonical index (workspace)
     int rb = 0;
     {
         int lo = 0, hi = P.nrb - 1;
@@ -67,17 +123,24 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attn_kernel(
     const int sp = rem - P.sp_base[rb];
     const int nsp = P.sp_base[rb + 1] - P.sp_base[rb];
     const int row0 = rb * kRowsPerBlock;
-    const int kend = a.kv_start + min(row0 + kRowsPerBlock, a.s);
+    const int kend = a.kv_start + min(row0 + kRowsPerBlock, a.s);  // keys < kend
     const int ntiles = (kend + kTileKeys - 1) / kTileKeys;
     const int t_begin = sp * P.tps;
     const int t_end = min(t_begin + P.tps, ntiles);
 
     const int hh = wave & 1;
     const int head = kvh * kRep + hh;
-    const int r = row0 + (wave >> 1) * 32 + n;  // this lane's query row
+    const int wrow0 = row0 + (wave >> 1) * 32;  // first row of this wave
+    const int r = wrow0 + n;                      // this lane's query row
     const bool row_ok = r < a.s;
     const int qpos = a.kv_start + r;
     const int ldq = a.nqh * kHeadDim;
+
+    const __amdgpu_buffer_rsrc_t kres = make_rsrc(a.k + kvh * a.head_stride, kend * kHeadDim * 2);
+    const __amdgpu_buffer_rsrc_t vres = make_rsrc(a.v + kvh * a.head_stride, kend * kHeadDim * 2);
+
+    TileRegs pre;
+    load_tile(kres, vres, t_begin * kTileKeys, tid, pre);
 
     // Q^T as B operand: k-step ks covers dims ks*16 + g*8 .. +8.
     half8v qb[8];
@@ -91,34 +154,20 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attn_kernel(
         }
     }
 
-    const f16* Kg = a.k + kvh * a.head_stride;
-    const f16* Vg = a.v + kvh * a.head_stride;
     float m = kNegInf, lsum = 0.0f;
     float16v o[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[db] = (float16v){};
 
+    store_tile(pre, Ks[0], Vt[0], tid);
+    __syncthreads();
+
     for (int t = t_begin; t < t_end; ++t) {
+        const int buf = (t - t_begin) & 1;
         const int k0 = t * kTileKeys;
-        __syncthreads();
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int idx = c * (kWaves * 64) + tid;
-            const int key = idx >> 4, dseg = (idx & 15) * 8;
-            const int gk = k0 + key;
-            H8 kv, vv;
-            if (gk < kend) {
-                kv.u = *(const uint4*)(Kg + (int64_t)gk * kHeadDim + dseg);
-                vv.u = *(const uint4*)(Vg + (int64_t)gk * kHeadDim + dseg);
-            } else {
-                kv.u = make_uint4(0, 0, 0, 0);
-                vv.u = make_uint4(0, 0, 0, 0);
-            }
-            *(uint4*)&Ks[key * kKPad + dseg] = kv.u;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) Vt[(dseg + e) * kVPad + key] = vv.e[e];
-        }
-        __syncthreads();
+        if (t + 1 < t_end) load_tile(kres, vres, k0 + kTileKeys, tid, pre);
+        const f16* ks_ = Ks[buf];
+        const f16* vt_ = Vt[buf];
 
         // S^T: keys kb*32 + (8*(i/4) + 4*g + i%4) x query n, accumulated over dims.
         float16v st[2];
@@ -127,21 +176,29 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attn_kernel(
             st[kb] = (float16v){};
 #pragma unroll
             for (int ks = 0; ks < 8; ++ks) {
-                const half8v ka = *(const half8v*)&Ks[(kb * 32 + n) * kKPad + ks * 16 + g * 8];
+                const half8v ka = *(const half8v*)&ks_[(kb * 32 + n) * kKPad + ks * 16 + g * 8];
                 st[kb] = mfma32(ka, qb[ks], st[kb]);
             }
         }
         float mx = kNegInf;
+        if (k0 + kTileKeys - 1 <= a.kv_start + wrow0) {  // whole tile visible to the wave
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int key = k0 + kb * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-                float v = st[kb][i] * a.scale_log2;
-                if (key > qpos) v = kNegInf;
-                st[kb][i] = v;
-                mx = fmaxf(mx, v);
-            }
+                for (int i = 0; i < 16; ++i) {
+                    st[kb][i] *= a.scale_log2;
+                    mx = fmaxf(mx, st[kb][i]);
+                }
+        } else {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key = k0 + kb * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+                    const float v = key > qpos ? kNegInf : st[kb][i] * a.scale_log2;
+                    st[kb][i] = v;
+                    mx = fmaxf(mx, v);
+                }
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float mn = fmaxf(m, mx);
@@ -150,18 +207,19 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attn_kernel(
         m = mn;
         float ps = 0.0f;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const float p = fast_exp2(st[kb][i] - mu);
                 st[kb][i] = p;
                 ps += p;
             }
-        }
         ps += __shfl_xor(ps, 32);
         lsum = lsum * alpha + ps;
+        if (__ballot(alpha != 1.0f)) {
 #pragma unroll
-        for (int db = 0; db < 4; ++db) o[db] *= alpha;
+            for (int db = 0; db < 4; ++db) o[db] *= alpha;
+        }
 
         // O^T += V^T P^T; k-step w4 covers tile keys 16*w4 + 4*g + {0..3, 8..11}.
 #pragma unroll
@@ -171,13 +229,16 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attn_kernel(
             for (int j = 0; j < 8; ++j) pb[j] = (f16)st[w4 >> 1][8 * (w4 & 1) + j];
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                const f16* vrow = &Vt[(db * 32 + n) * kVPad + 16 * w4 + 4 * g];
-                const half4v lo = *(const half4v*)vrow;
-                const half4v hi = *(const half4v*)(vrow + 8);
+                const int dim = db * 32 + n;
+                const f16* vrow = &vt_[dim * kVPad];
+                const half4v lo = *(const half4v*)(vrow + vt_col(dim, 16 * w4 + 4 * g));
+                const half4v hi = *(const half4v*)(vrow + vt_col(dim, 16 * w4 + 4 * g + 8));
                 const half8v va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
                 o[db] = mfma32(va, pb, o[db]);
             }
         }
+        if (t + 1 < t_end) store_tile(pre, Ks[buf ^ 1], Vt[buf ^ 1], tid);
+        __syncthreads();
     }
 
     // o[db][i] holds dim db*32 + 8*(i/4) + 4*g + i%4 of query row r.
@@ -255,8 +316,6 @@ __global__ __launch_bounds__(kWaves * 64, 2) void prefill_attn_kernel(
 
 }  // namespace
 
-
-
 PrefillPlan plan_prefill(int s, int kv_start, int nkvh, int tiles_per_split) {
     PrefillPlan P{};
     P.nrb = (s + kRowsPerBlock - 1) / kRowsPerBlock;
@@ -277,7 +336,7 @@ hipError_t launch_prefill_attn(const PrefillArgs& a, const PrefillPlan& P, const
     const int items = P.items_per_kvh * a.nkvh;
     if (items <= 0) return hipSuccess;
     if (items > ws.items || P.nrb > kMaxRowBlocks) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(prefill_attn_kernel, dim3(items), dim3(kWaves * 64), 0, stream, a, P, ws.o,
+    hipLaunchKernelGGL(prefill_attn_kernel, dim3(items), dim3(kThreads), 0, stream, a, P, ws.o,
                        ws.ml, ws.counters);
     return hipGetLastError();
 }
