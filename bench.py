@@ -175,6 +175,26 @@ def bench_prefill(s: int, kv_start: int, steps: int, warmup: int, layers: int = 
             "stage_a_us_per_layer": ms_s * 1e3 / layers}
 
 
+def copy_calibration(steps: int):
+    """A plain device copy of 1 GiB (reads 1 GiB, writes 1 GiB): the reference
+    point for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes."""
+    import torch
+
+    x = torch.empty(512 * 1024 * 1024, dtype=torch.float16, device="cuda").normal_()
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(max(1, steps)):
+        y.copy_(x)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / max(1, steps)
+    return {"bytes_read": x.numel() * 2, "bytes_written": y.numel() * 2, "ms": ms,
+            "GBps_rw": 2 * x.numel() * 2 / (ms * 1e-3) / 1e9}
+
+
 def cpu_baseline(lengths, budget_s: float = 10.0):
     """Reference CPU path (C++ restatement of cpu_decoder.rs, oracle/) on config
     3: stage (a) + attention for each of the 16 slots, one layer at a time,
@@ -251,6 +271,7 @@ def main():
             "decode5": lambda: bench_decode(64, splitmix_lengths(SEED_BASE + 5, 64, 64, 4096), K, W),
             "prefill2": lambda: bench_prefill(420, 0, K, W),
             "prefill4": lambda: bench_prefill(512, 7680, K, W),
+            "copycal": lambda: copy_calibration(K),
         }
         log(json.dumps({only: runs[only]()}))
         return
