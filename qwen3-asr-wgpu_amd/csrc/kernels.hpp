@@ -98,16 +98,20 @@ struct PrefillPlan {
     int32_t sp_base[kMaxRowBlocks + 1];
 };
 
-// Split workspace: per item 4 waves x 32 rows of (unnormalised O[128], m, l);
-// one counter per (kv head, row block), zero at rest.
+// Split workspace: per item 4 waves x (64 accumulator elements x 64 lanes of
+// unnormalised O, element-major; then m and l per lane); one counter per
+// (kv head, row block), zero at rest.
 struct PrefillWs {
     float* o;
     float* ml;
     uint32_t* counters;  // [nkvh * kMaxRowBlocks]
     int64_t items;
 };
-constexpr int64_t kPrefillItemFloats = 4 * 32 * kHeadDim;
-constexpr int64_t kPrefillItemMl = 4 * 32 * 2;
+constexpr int kPrefillWaves = 4;
+constexpr int64_t kPrefillWaveFloats = 64 * 64;  // 64 accumulator elements x 64 lanes
+constexpr int64_t kPrefillWaveMl = 2 * 64;       // m and l of each lane
+constexpr int64_t kPrefillItemFloats = kPrefillWaves * kPrefillWaveFloats;
+constexpr int64_t kPrefillItemMl = kPrefillWaves * kPrefillWaveMl;
 
 PrefillPlan plan_prefill(int s, int kv_start, int nkvh, int tiles_per_split);
 hipError_t launch_prefill_attn(const PrefillArgs& a, const PrefillPlan& P, const PrefillWs& ws,

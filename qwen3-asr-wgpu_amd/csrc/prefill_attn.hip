@@ -39,8 +39,12 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4;
+constexpr int kWaves = kPrefillWaves;
 constexpr int kThreads = kWaves * 64;
+// The split workspace holds exactly what one wave publishes: its 4 x 16
+// accumulator registers for 64 lanes, and (m, l) for 64 lanes.
+static_assert(kPrefillWaveFloats == 4 * 16 * 64, "partial O record size");
+static_assert(kPrefillWaveMl == 2 * 64, "partial (m, l) record size");
 constexpr int kRowsPerBlock = kPrefillRows;
 constexpr int kTileKeys = 64;
 constexpr int kKPad = kHeadDim + 8;   // Ks row stride (halves)
@@ -260,44 +264,49 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_attn_kernel(
         return;
     }
 
-    // Partial: [item][wave][n][128] unnormalised O, [item][wave][n] (m, l),
-    // published with device-scope stores (see stores_done_barrier).
-    const int64_t slot_id = ((int64_t)item * kWaves + wave) * 32 + n;
-    float* po = ws_o + slot_id * kHeadDim;
+    // Partial of this wave: 64 accumulator elements x 64 lanes, element-major
+    // (element e of lane l at [e][l]) so every store and load instruction
+    // moves 256 contiguous bytes; then (m, l) per lane.  Published with
+    // device-scope stores (see stores_done_barrier).
+    float* po = ws_o + (int64_t)item * kPrefillItemFloats + wave * kPrefillWaveFloats;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) store_dev(po + db * 32 + 8 * (i >> 2) + 4 * g + (i & 3), o[db][i]);
-    if (g == 0) {
-        store_dev(&ws_ml[slot_id * 2], m);
-        store_dev(&ws_ml[slot_id * 2 + 1], lsum);
-    }
+        for (int i = 0; i < 16; ++i) store_dev(po + (db * 16 + i) * 64 + lane, o[db][i]);
+    float* pml = ws_ml + (int64_t)item * kPrefillItemMl + wave * kPrefillWaveMl;
+    store_dev(pml + lane, m);
+    store_dev(pml + 64 + lane, lsum);
     stores_done_barrier();
     uint32_t* ctr = &counters[kvh * P.nrb + rb];
     if (tid == 0) s_last = (ticket_add(ctr) == (uint32_t)(nsp - 1));
     __syncthreads();
     if (!s_last) return;
+
+    // Last arrival: merge the nsp partials of this (kv head, row block); each
+    // wave merges its own 32 rows.  (m, l) of all partials first, then the
+    // accumulators partial by partial, 64 independent loads in flight each.
     const int it0 = kvh * P.items_per_kvh + P.sp_base[rb];
     float M = kNegInf;
     for (int i = 0; i < nsp; ++i)
-        M = fmaxf(M, load_dev(&ws_ml[(((int64_t)(it0 + i) * kWaves + wave) * 32 + n) * 2]));
+        M = fmaxf(M, load_dev(ws_ml + (int64_t)(it0 + i) * kPrefillItemMl + wave * kPrefillWaveMl + lane));
     float Ls = 0.0f;
-    float acc[4][16];
+    float16v acc[4];
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[db][e] = 0.0f;
+    for (int db = 0; db < 4; ++db) acc[db] = (float16v){};
     for (int i = 0; i < nsp; ++i) {
-        const int64_t sid = ((int64_t)(it0 + i) * kWaves + wave) * 32 + n;
-        const float mi = load_dev(&ws_ml[sid * 2]);
+        const float* pm = ws_ml + (int64_t)(it0 + i) * kPrefillItemMl + wave * kPrefillWaveMl;
+        const float* pi = ws_o + (int64_t)(it0 + i) * kPrefillItemFloats + wave * kPrefillWaveFloats;
+        float x[64];
+#pragma unroll
+        for (int e = 0; e < 64; ++e) x[e] = load_dev(pi + e * 64 + lane);
+        const float mi = load_dev(pm + lane);
+        const float li = load_dev(pm + 64 + lane);
         const float w = mi == kNegInf ? 0.0f : fast_exp2(mi - M);
-        Ls = fmaf(load_dev(&ws_ml[sid * 2 + 1]), w, Ls);
-        const float* pi = ws_o + sid * kHeadDim;
+        Ls = fmaf(li, w, Ls);
 #pragma unroll
         for (int db = 0; db < 4; ++db)
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-                acc[db][e] = fmaf(load_dev(pi + db * 32 + 8 * (e >> 2) + 4 * g + (e & 3)), w, acc[db][e]);
+            for (int e = 0; e < 16; ++e) acc[db][e] = fmaf(x[db * 16 + e], w, acc[db][e]);
     }
     if (row_ok) {
         const float inv = 1.0f / Ls;
