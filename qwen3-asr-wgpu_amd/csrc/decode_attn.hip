@@ -11,11 +11,15 @@
 //   are planned per entry on the host so every workgroup streams about the
 //   same number of keys whatever the ragged lengths.
 //   Both q heads of the kv head (GQA 2:1) are computed from one K/V read.
-//   A wave pass covers 32 keys: 8 dwordx4 buffer loads of K and 8 of V per
-//   lane, each load instruction reading 1 KiB contiguous (4 keys x 256 B,
-//   lane l -> key l/16, dims (l%16)*8..+8), so every instruction is fully
-//   coalesced.  The buffer resources end at the chunk's last key, so the
-//   hardware range check returns zeros past it (those scores are masked).
+//   A wave pass covers 32 contiguous keys (wave w of a workgroup pass takes
+//   keys t0 + 32*w .. +32, so the workgroup's requests of one pass form one
+//   contiguous run): 8 dwordx4 buffer loads of K and 8 of V per lane, each
+//   instruction reading 1 KiB contiguous (4 keys x 256 B, lane l -> key l/16,
+//   dims (l%16)*8..+8), so every instruction is fully coalesced.  (Spreading
+//   a wave's loads over the workgroup pass in 4-key groups, or giving each
+//   wave one contiguous share of the chunk, both measured slower.)
+//   The buffer resources end at the chunk's last key, so the hardware range
+//   check returns zeros past it (those scores are masked).
 //   q.k: v_dot2_f32_f16 on the lane's 8 dims, then a transposing 16-lane DPP
 //   reduction that leaves each lane with one (key, head) score.  Softmax is
 //   online per (16-lane row, head) in the exp2 domain; the row's 16
@@ -58,7 +62,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int b
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
 }
 
-// One wave pass (32 keys from t0) of K or V: 8 x 16 B per lane.
+// One wave pass (32 keys from t0) of K or V: 8 x 16 B per lane; load kk
+// covers keys t0 + 4*kk .. +4 (this lane: key t0 + 4*kk + row).
 __device__ __forceinline__ void load_pass(__amdgpu_buffer_rsrc_t r, int t0, int row, int seg,
                                           H8 (&x)[8]) {
     const int voff = (t0 + row) * (kHeadDim * 2) + seg * 16;
@@ -76,12 +81,12 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     const f16* __restrict__ q_gain, const f16* __restrict__ k_gain,
     const f16* __restrict__ cos_tab, const f16* __restrict__ sin_tab, f16* __restrict__ out,
     float* __restrict__ ws_acc, float* __restrict__ ws_ml, uint32_t* __restrict__ counters) {
-    constexpr int kWgKeys = W * kDecodeTileKeys;  // keys per round of all waves
     __shared__ H8 s_q[2][16];
     __shared__ H8 s_knew[16];
     __shared__ H8 s_vnew[16];
     __shared__ __attribute__((aligned(16))) f16 s_raw[4][kHeadDim];  // q0, q1, k, v raw heads
     __shared__ __attribute__((aligned(16))) f16 s_tab[4][kHeadDim];  // q gain, k gain, cos, sin
+    __shared__ __attribute__((aligned(16))) float s_sq[3][kHeadDim];  // squares of q0, q1, k
     __shared__ float s_inv[3];
     __shared__ float s_p[W][64];
     __shared__ float s_wm[4 * W][2];
@@ -97,15 +102,10 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     const int row = lane >> 4;  // key within a 4-key load
     const int seg = lane & 15;  // 8-dim segment
 
-    int b = 0;
-    {
-        int lo = 0, hi = P.batch - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (P.wg_base[mid] <= wg) lo = mid; else hi = mid - 1;
-        }
-        b = lo;
-    }
+    // Entry of this workgroup = number of later entry starts at or before it:
+    // lane i tests wg_base[i + 1], one load per lane and a ballot, no search.
+    static_assert(kMaxBatch <= 64, "one lane per entry");
+    const int b = __popcll(__ballot(lane + 1 < P.batch && P.wg_base[lane + 1] <= wg));
     const int L = P.len[b];
     const int chunk = P.chunk[b];
     const int nch = (L + chunk - 1) / chunk;
@@ -123,18 +123,37 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     const int rbytes = nkeys * (kHeadDim * 2);
     const __amdgpu_buffer_rsrc_t kres = make_rsrc(Kc + (int64_t)key0 * kHeadDim, rbytes);
     const __amdgpu_buffer_rsrc_t vres = make_rsrc(Vc + (int64_t)key0 * kHeadDim, rbytes);
+    constexpr int kWgKeys = W * kDecodeTileKeys;  // keys per workgroup pass
+    const int tw = wave * kDecodeTileKeys;         // this wave's first key in a pass
 
-    // Raw inputs of the fused prologue are requested before the first K/V pass
-    // so that waiting for them does not wait for the pass.
+    // The query inputs (the raw qkv heads, or q itself) are requested first and
+    // the first K/V pass right after them, so the K/V stream starts without
+    // waiting for a round trip; the prologue runs while the pass is in flight.
     const int pos = L - 1;
     const bool owner = FUSED && (c == nch - 1);
+    H8 q0, q1;
     if constexpr (FUSED) {
         const int64_t tot = (int64_t)(nqh + 2 * g.nkvh) * kHeadDim;
         const f16* qkv_row = qin + b * tot;
         if (tid < 64) {
             const int which = tid >> 4;
             const int hoff = which < 2 ? (h0 + which) : which == 2 ? (nqh + kvh) : (nqh + g.nkvh + kvh);
-            *(uint4*)&s_raw[which][seg * 8] = *(const uint4*)(qkv_row + hoff * kHeadDim + seg * 8);
+            H8 x;
+            x.u = *(const uint4*)(qkv_row + hoff * kHeadDim + seg * 8);
+            *(uint4*)&s_raw[which][seg * 8] = x.u;
+            if (which < 3) {  // f16 squares are exact in f32
+                float4 lo, hi;
+                lo.x = h2f(x.e[0]) * h2f(x.e[0]);
+                lo.y = h2f(x.e[1]) * h2f(x.e[1]);
+                lo.z = h2f(x.e[2]) * h2f(x.e[2]);
+                lo.w = h2f(x.e[3]) * h2f(x.e[3]);
+                hi.x = h2f(x.e[4]) * h2f(x.e[4]);
+                hi.y = h2f(x.e[5]) * h2f(x.e[5]);
+                hi.z = h2f(x.e[6]) * h2f(x.e[6]);
+                hi.w = h2f(x.e[7]) * h2f(x.e[7]);
+                *(float4*)&s_sq[which][seg * 8] = lo;
+                *(float4*)&s_sq[which][seg * 8 + 4] = hi;
+            }
         } else if (tid < 128) {
             const int which = (tid >> 4) & 3;
             const f16* p = which == 0 ? q_gain
@@ -143,20 +162,22 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
                                       : sin_tab + (int64_t)pos * kHeadDim;
             *(uint4*)&s_tab[which][seg * 8] = *(const uint4*)(p + seg * 8);
         }
+    } else {
+        const f16* qb = qin + (int64_t)b * nqh * kHeadDim + h0 * kHeadDim + seg * 8;
+        q0.u = *(const uint4*)qb;
+        q1.u = *(const uint4*)(qb + kHeadDim);
     }
 
     // Two pass buffers per wave: while one pass is computed the next one's
     // loads are in flight.  Passes past the chunk fall outside the buffer
     // range: their loads return zeros without touching memory.
     H8 ka[8], va[8], kb[8], vb[8];
-    const int tw = wave * kDecodeTileKeys;  // this wave's first key, relative to key0
     load_pass(kres, tw, row, seg, ka);
     load_pass(vres, tw, row, seg, va);
 
-    H8 q0, q1;
     if constexpr (FUSED) {
         __syncthreads();
-        if (tid < 3 && (tid < 2 || owner)) s_inv[tid] = head_inv_rms_serial(s_raw[tid], P.eps);
+        if (tid < 3 && (tid < 2 || owner)) s_inv[tid] = head_inv_rms_squares(s_sq[tid], P.eps);
         __syncthreads();
         if (tid < 256) {
             const int h = tid >> 7, j = tid & 127;
@@ -176,10 +197,6 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
         __syncthreads();
         q0 = s_q[0][seg];
         q1 = s_q[1][seg];
-    } else {
-        const f16* qb = qin + (int64_t)b * nqh * kHeadDim + h0 * kHeadDim + seg * 8;
-        q0.u = *(const uint4*)qb;
-        q1.u = *(const uint4*)(qb + kHeadDim);
     }
 
     load_pass(kres, tw + kWgKeys, row, seg, kb);
@@ -195,14 +212,14 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     const bool odd = seg & 1;
     float* s_pw = &s_p[wave][0];
     const float sl2 = P.scale_log2;
-    const int new_rel = pos - key0;  // the appended key, relative (owner only)
+    const int new_rel = pos - key0;  // the appended key, relative to the chunk (owner only)
 
     auto process = [&](H8 (&kr)[8], H8 (&vr)[8], int t0) {
         if constexpr (FUSED) {
             if (owner) {
 #pragma unroll
                 for (int kk = 0; kk < 8; ++kk) {
-                    if (t0 + kk * 4 + row == new_rel) {
+                    if (t0 + 4 * kk + row == new_rel) {
                         kr[kk] = s_knew[seg];
                         vr[kk] = s_vnew[seg];
                     }
@@ -318,14 +335,15 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     if (!s_last) return;
 
     // Last arrival: merge the nch partials of (b, kv head).  The (m, l) of
-    // every chunk (to LDS) and this thread's first 16 partial outputs are
-    // requested together, so up to 32 chunks merge in one memory round trip.
+    // every chunk (to LDS) and this thread's first kBatch partial outputs are
+    // requested together, so up to kBatch chunks merge in one memory round
+    // trip.
     const int64_t it0 = P.wg_base[b] + kvh * nch;
     if (tid < nch) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) s_ml[tid][k] = load_dev(&ws_ml[(it0 + tid) * 4 + k]);
     }
-    constexpr int kBatch = 32;
+    constexpr int kBatch = 64;
     float x[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)

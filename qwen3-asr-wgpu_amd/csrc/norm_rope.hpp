@@ -28,6 +28,22 @@ __device__ __forceinline__ float head_inv_rms_serial(const f16* raw, float eps) 
     return 1.0f / sqrtf(sum2 / (float)kHeadDim + eps);
 }
 
+// The same chain over squares already in LDS (sq[j] = x_j*x_j in f32, exact):
+// only the 128 dependent adds remain on the serial path, read 4 at a time.
+__device__ __forceinline__ float head_inv_rms_squares(const float* sq, float eps) {
+#pragma clang fp contract(off)
+    float sum2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kHeadDim / 4; ++i) {
+        const float4 v = *(const float4*)(sq + 4 * i);
+        sum2 += v.x;
+        sum2 += v.y;
+        sum2 += v.z;
+        sum2 += v.w;
+    }
+    return 1.0f / sqrtf(sum2 / (float)kHeadDim + eps);
+}
+
 // One roped element j of a head whose raw values, gains and cos/sin rows are
 // given (all f16).  `inv` is the head's inverse RMS.
 __device__ __forceinline__ f16 rope_elem(const f16* raw, const f16* gain, const f16* cos_row,

@@ -50,11 +50,24 @@ constexpr int kTileKeys = 64;
 constexpr int kKPad = kHeadDim + 8;   // Ks row stride (halves)
 constexpr int kVPad = kTileKeys + 8;  // Vt row stride (halves)
 constexpr int kKsHalves = kTileKeys * kKPad;
-constexpr int kVtHalves = kHeadDim * kVPad;
+// One past the last V^T element (row 127 at skew 4*15, position 63; see
+// vt_index), rounded up to 16 bytes so both buffers stay 16-byte aligned.
+constexpr int kVtHalves = ((kHeadDim - 1) * kVPad + 4 * ((kHeadDim - 1) >> 3) + kTileKeys + 7) / 8 * 8;
 constexpr float kNegInf = -__builtin_inff();
 
 __device__ __forceinline__ float16v mfma32(const half8v& a, const half8v& b, const float16v& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Lanes l and l^32 hold the two key halves of one query column.  One
+// v_permlane32_swap gives every lane both values (no LDS round trip).
+__device__ __forceinline__ float halves_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int bytes) {
@@ -80,11 +93,21 @@ __device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t kr, __amdgpu_bu
     }
 }
 
-// V^T column of (dim, key): the key XOR 4*((dim/8) % 16).  The 16 lanes that
-// store one key's dims 8j+e then hit 16 different banks (the plain layout
-// put them all in one bank), and 4-key groups stay contiguous for the 8-byte
-// operand reads.
-__device__ __forceinline__ int vt_col(int dim, int key) { return key ^ (4 * ((dim >> 3) & 15)); }
+// V^T element (dim, key) of a 64-key tile, in halves.
+//  * Within each 16-key block, key bits 2 and 3 are swapped, so the keys one
+//    lane feeds to a k-step, 4g + {0..3} and 4g + {8..11}, are 8 contiguous
+//    halves (one ds_read2_b64 into the 4 registers of the operand).
+//  * Row dim starts at dim*kVPad + 4*(dim/8): the 16 lanes that store dims
+//    8j + e of one key then fall 2*j dwords apart, on 16 different banks.
+//    The skew never decreases with dim and kVPad - 64 >= 4, so rows never
+//    overlap.
+__device__ __forceinline__ int vt_pos(int key) {
+    return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+}
+__device__ __forceinline__ int vt_index(int dim, int key) {
+    return dim * kVPad + 4 * (dim >> 3) + vt_pos(key);
+}
+static_assert(kVPad - kTileKeys >= 4, "V^T rows would overlap");
 
 __device__ __forceinline__ void store_tile(const TileRegs& t, f16* Ks, f16* Vt, int tid) {
 #pragma unroll
@@ -95,7 +118,7 @@ __device__ __forceinline__ void store_tile(const TileRegs& t, f16* Ks, f16* Vt, 
         H8 v;
         v.u = t.v[c];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) Vt[(dseg + e) * kVPad + vt_col(dseg + e, key)] = v.e[e];
+        for (int e = 0; e < 8; ++e) Vt[vt_index(dseg + e, key)] = v.e[e];
     }
 }
 
@@ -163,6 +186,12 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_attn_kernel(
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[db] = (float16v){};
 
+    // V^T operand of k-step w4, dims db*32..+32: keys 16*w4 + 4*g + {0..3,
+    // 8..11} of dim db*32 + n sit at vt_index(dim, 16*w4 + 4*g) .. +8, which
+    // is the per-lane vlane plus a compile-time offset (dim>>3 = 4*db + n/8).
+    const int vlane = n * kVPad + 4 * (n >> 3) + 8 * g;
+    const half2v ones2 = {(f16)1.0f, (f16)1.0f};
+
     store_tile(pre, Ks[0], Vt[0], tid);
     __syncthreads();
 
@@ -174,71 +203,72 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_attn_kernel(
         const f16* vt_ = Vt[buf];
 
         // S^T: keys kb*32 + (8*(i/4) + 4*g + i%4) x query n, accumulated over dims.
-        float16v st[2];
+        float16v st[2] = {(float16v){}, (float16v){}};
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            st[kb] = (float16v){};
+        for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
+            for (int kb = 0; kb < 2; ++kb) {
                 const half8v ka = *(const half8v*)&ks_[(kb * 32 + n) * kKPad + ks * 16 + g * 8];
                 st[kb] = mfma32(ka, qb[ks], st[kb]);
             }
-        }
+        // Row max on the raw scores (the scale is positive), scaled once; the
+        // scale is then folded into the exponent: p = 2^(s*scale_log2 - m).
         float mx = kNegInf;
         if (k0 + kTileKeys - 1 <= a.kv_start + wrow0) {  // whole tile visible to the wave
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    st[kb][i] *= a.scale_log2;
-                    mx = fmaxf(mx, st[kb][i]);
-                }
+                for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[kb][i]);
         } else {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int key = k0 + kb * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-                    const float v = key > qpos ? kNegInf : st[kb][i] * a.scale_log2;
+                    const float v = key > qpos ? kNegInf : st[kb][i];
                     st[kb][i] = v;
                     mx = fmaxf(mx, v);
                 }
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = halves_max(mx) * a.scale_log2;
         const float mn = fmaxf(m, mx);
         const float mu = mn == kNegInf ? 0.0f : mn;
         const float alpha = fast_exp2(m - mu);
         m = mn;
+        // P^T in the B-operand layout, k-step w4 covering tile keys
+        // 16*w4 + 4*g + {0..3, 8..11}; its row sum is taken from the same f16
+        // values the MFMA consumes (v_dot2 against ones, f32 accumulate).
+        half8v pb[4];
+#pragma unroll
+        for (int w4 = 0; w4 < 4; ++w4)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                pb[w4][j] = (f16)fast_exp2(fmaf(st[w4 >> 1][8 * (w4 & 1) + j], a.scale_log2, -mu));
         float ps = 0.0f;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int w4 = 0; w4 < 4; ++w4)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const float p = fast_exp2(st[kb][i] - mu);
-                st[kb][i] = p;
-                ps += p;
+            for (int q2 = 0; q2 < 4; ++q2) {
+                const half2v pr = {pb[w4][2 * q2], pb[w4][2 * q2 + 1]};
+                ps = __builtin_amdgcn_fdot2(pr, ones2, ps, false);
             }
-        ps += __shfl_xor(ps, 32);
+        ps = halves_sum(ps);
         lsum = lsum * alpha + ps;
         if (__ballot(alpha != 1.0f)) {
 #pragma unroll
             for (int db = 0; db < 4; ++db) o[db] *= alpha;
         }
 
-        // O^T += V^T P^T; k-step w4 covers tile keys 16*w4 + 4*g + {0..3, 8..11}.
+        // O^T += V^T P^T.
 #pragma unroll
         for (int w4 = 0; w4 < 4; ++w4) {
-            half8v pb;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) pb[j] = (f16)st[w4 >> 1][8 * (w4 & 1) + j];
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                const int dim = db * 32 + n;
-                const f16* vrow = &vt_[dim * kVPad];
-                const half4v lo = *(const half4v*)(vrow + vt_col(dim, 16 * w4 + 4 * g));
-                const half4v hi = *(const half4v*)(vrow + vt_col(dim, 16 * w4 + 4 * g + 8));
+                const f16* vp = vt_ + vlane + db * (32 * kVPad + 16) + 16 * w4;
+                const half4v lo = *(const half4v*)vp;
+                const half4v hi = *(const half4v*)(vp + 4);
                 const half8v va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                o[db] = mfma32(va, pb, o[db]);
+                o[db] = mfma32(va, pb[w4], o[db]);
             }
         }
         if (t + 1 < t_end) store_tile(pre, Ks[buf ^ 1], Vt[buf ^ 1], tid);

@@ -91,8 +91,15 @@ def test_config3_batch16_ragged_decode(O, gpu):
     g.close()
 
 
-@pytest.mark.parametrize("chunk", ["128", "256", "512", "1024"])
-def test_decode_chunk_sizes_and_unfused_equal_fused(O, gpu, chunk, monkeypatch):
+# (minimum chunk keys, workgroup target): from the finest split the planner
+# allows (32-key chunks, up to 256 per entry) through the default plan to one
+# chunk per entry (no split-K, no merge), plus 8-wave workgroups.
+CHUNK_PLANS = [("32", "4096", "4"), ("64", "512", "4"), ("256", "512", "4"),
+               ("100000", "512", "4"), ("64", "512", "8")]
+
+
+@pytest.mark.parametrize("min_chunk,wgs,waves", CHUNK_PLANS)
+def test_decode_chunk_sizes_and_unfused_equal_fused(O, gpu, min_chunk, wgs, waves, monkeypatch):
     """Every split-K chunking matches the oracle; the unfused path
     (qasr_decode_attn on stage-(a) output) equals the fused step bitwise."""
     import qasr_attn
@@ -100,8 +107,11 @@ def test_decode_chunk_sizes_and_unfused_equal_fused(O, gpu, chunk, monkeypatch):
 
     from oracle import Rng
 
-    monkeypatch.setenv("QASR_DECODE_CHUNK", chunk)
-    rng = Rng(SEED_BASE + 200 + int(chunk))
+    monkeypatch.setenv("QASR_DECODE_MIN_CHUNK", min_chunk)
+    monkeypatch.setenv("QASR_DECODE_WGS", wgs)
+    monkeypatch.setenv("QASR_DECODE_WAVES", waves)
+    chunk = f"{min_chunk}/{wgs}/w{waves}"
+    rng = Rng(SEED_BASE + 200 + int(min_chunk) % 1000 + int(waves))
     lay = Layer(rng)
     lengths = [1, 2, 127, 128, 129, 255, 256, 1023, 1024, 1500, 2047, 2048, 4095]
     cap = cap_for(max(lengths) + 1)
