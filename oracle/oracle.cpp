@@ -3,7 +3,7 @@
 // TEST INFRASTRUCTURE, NOT PRODUCT CODE: the checker that tests/, smoke() and
 // bench.py's cpu_baseline leg use.  The shipped HIP library never links it.
 //
-// Build: g++ -O2 -ffp-contract=off -fno-fast-math (oracle/Makefile).  Without
+// Build: g++ -O3 -mf16c -ffp-contract=off -fno-fast-math (oracle/Makefile).  Without
 // contraction every a*b+c below rounds twice, as in the Rust source it follows.
 // std::exp(float) / std::sqrt(float) are glibc expf / IEEE sqrtf, the functions
 // Rust's f32::exp / f32::sqrt call on Linux.
@@ -16,6 +16,7 @@
 #include <condition_variable>
 #include <cstring>
 #include <functional>
+#include <immintrin.h>
 #include <mutex>
 #include <thread>
 #include <vector>
@@ -179,8 +180,25 @@ float qo_f32_from_f16(uint16_t h) {
     return f;
 }
 
+// Arrays go through a 65536-entry table filled from qo_f32_from_f16 (every
+// f16 value widens exactly, so the table is the function); large arrays are
+// split over the worker pool.
 void qo_f16_to_f32_array(const uint16_t* src, float* dst, int64_t n) {
-    for (int64_t i = 0; i < n; ++i) dst[i] = qo_f32_from_f16(src[i]);
+    static const std::vector<float> table = [] {
+        std::vector<float> t(65536);
+        for (int i = 0; i < 65536; ++i) t[i] = qo_f32_from_f16((uint16_t)i);
+        return t;
+    }();
+    const float* T = table.data();
+    const int64_t blk = 1 << 20;
+    if (n < 4 * blk) {
+        for (int64_t i = 0; i < n; ++i) dst[i] = T[src[i]];
+        return;
+    }
+    pool_for(0).run((n + blk - 1) / blk, [&](int64_t b) {
+        const int64_t e = std::min(n, (b + 1) * blk);
+        for (int64_t i = b * blk; i < e; ++i) dst[i] = T[src[i]];
+    });
 }
 
 void qo_f32_to_f16_array(const float* src, uint16_t* dst, int64_t n) {
@@ -445,5 +463,262 @@ int32_t qo_uniform_int(uint64_t* state, int32_t lo, int32_t hi) {
     uint64_t span = (uint64_t)((int64_t)hi - (int64_t)lo + 1);
     return (int32_t)((int64_t)lo + (int64_t)(qo_splitmix64(state) % span));
 }
+
+// ===========================================================================
+// The whole text decoder for one sequence: CpuTextDecoder (cpu_decoder.rs).
+// Test infrastructure for the end-to-end greedy check: the attention path
+// under test sits inside this layer sequence on the GPU side.
+// ===========================================================================
+}  // extern "C"
+
+namespace {
+
+// Mat (cpu_decoder.rs:11-27) holds f16 checkpoint weights widened to f32.
+// Here the f16 rows are read in place (borrowed from the caller) and widened
+// four at a time with vcvtph2ps, which is exact, so the products are the same
+// f32 products.  [rows][cols].
+struct Mat {
+    const uint16_t* w = nullptr;
+    int rows = 0, cols = 0;
+    void load(const uint16_t* p, int r, int c) {
+        w = p;
+        rows = r;
+        cols = c;
+    }
+    // dot_transposed (cpu_decoder.rs:64-100) for one row x (f32 values of f16):
+    // four strided partial sums a[k % 4] (one SSE lane each: a separate
+    // multiply and add per element, as in Rust), then (a0 + a1) + (a2 + a3),
+    // then the tail.  Output blocks of 64 rows run as pool tasks, as the
+    // reference's par_chunks.
+    void dot(const float* x, float* acc, Pool& pool) const {
+        const int OB = 64;
+        const int64_t nblk = (rows + OB - 1) / OB;
+        pool.run(nblk, [&](int64_t bi) {
+            const int o1 = std::min<int>(rows, (int)(bi + 1) * OB);
+            for (int o = (int)bi * OB; o < o1; ++o) {
+                const uint16_t* wr = w + (size_t)o * cols;
+                __m128 a = _mm_setzero_ps();
+                const int quads = cols / 4;
+                for (int q = 0; q < quads; ++q) {
+                    const __m128 wv = _mm_cvtph_ps(_mm_loadl_epi64((const __m128i*)(wr + 4 * q)));
+                    a = _mm_add_ps(a, _mm_mul_ps(wv, _mm_loadu_ps(x + 4 * q)));
+                }
+                float a4[4];
+                _mm_storeu_ps(a4, a);
+                float s = (a4[0] + a4[1]) + (a4[2] + a4[3]);
+                for (int k = quads * 4; k < cols; ++k) s += qo_f32_from_f16(wr[k]) * x[k];
+                acc[o] = s;
+            }
+        });
+    }
+};
+
+struct DecLayer {
+    std::vector<float> iln, pln, qn, kn;
+    std::vector<uint16_t> qn16, kn16;
+    Mat q, k, v, o, gate, up, down;
+};
+
+struct Decoder {
+    qo_dec_cfg cfg;
+    int cap = 0;
+    const uint16_t* embed = nullptr;  // f16, as the reference keeps it (borrowed)
+    std::vector<float> norm_w;
+    std::vector<DecLayer> layers;
+    std::vector<float> cos, sin;  // f32 values of the f16 tables
+    int tab_rows = 0;
+    std::vector<float> k_cache, v_cache;  // [layer][nkvh][cap][hd]
+    int pos = 0;
+    uint32_t last_token = 0;
+};
+
+std::vector<float> widen(const uint16_t* p, int64_t n) {
+    std::vector<float> v(n);
+    qo_f16_to_f32_array(p, v.data(), n);
+    return v;
+}
+
+// rms_norm_row (cpu_decoder.rs:261-272): sequential sum of squares,
+// inv = 1 / sqrt(sum2 / n + eps), out = f16(x * inv * w).
+void rms_norm_row(const uint16_t* x, const float* w, int n, float eps, uint16_t* out) {
+    float sum2 = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        const float f = qo_f32_from_f16(x[i]);
+        sum2 += f * f;
+    }
+    const float inv = 1.0f / std::sqrt(sum2 / (float)n + eps);
+    for (int i = 0; i < n; ++i) out[i] = qo_f16_from_f32(qo_f32_from_f16(x[i]) * inv * w[i]);
+}
+
+// forward (cpu_decoder.rs:367-456) for rows q0..q0+rows-1 of hidden state x
+// ([rows][hs] f16, updated in place).  Rows >= 2 use the reference's gemm crate
+// there (gemm 0.18.2, summation order not restated); here every row takes the
+// one-row order of dot_transposed.
+void forward(Decoder& D, std::vector<uint16_t>& x, int q0, int rows, Pool& pool) {
+    const qo_dec_cfg& c = D.cfg;
+    const int hs = c.hs, nqh = c.nqh, nkvh = c.nkvh, hd = c.hd, inter = c.inter;
+    const int q_dim = nqh * hd, kv_dim = nkvh * hd, tot = q_dim + 2 * kv_dim;
+    const int64_t layer_kv = (int64_t)nkvh * D.cap * hd;
+    std::vector<uint16_t> normed((size_t)rows * hs), qkv((size_t)rows * tot), qout((size_t)rows * q_dim),
+        attn((size_t)rows * q_dim), gate16((size_t)inter), up16((size_t)inter);
+    std::vector<float> xf(std::max(hs, std::max(q_dim, inter))), acc(std::max(tot, std::max(hs, inter)));
+    qo_shape sh{nqh, nkvh, hd, c.max_seq, c.eps};
+    for (int li = 0; li < c.layers; ++li) {
+        DecLayer& L = D.layers[li];
+        // input norm + q/k/v projections (383-394), f16 after each projection
+        for (int r = 0; r < rows; ++r) {
+            rms_norm_row(&x[(size_t)r * hs], L.iln.data(), hs, c.eps, &normed[(size_t)r * hs]);
+            qo_f16_to_f32_array(&normed[(size_t)r * hs], xf.data(), hs);
+            uint16_t* row = &qkv[(size_t)r * tot];
+            L.q.dot(xf.data(), acc.data(), pool);
+            for (int i = 0; i < q_dim; ++i) row[i] = qo_f16_from_f32(acc[i]);
+            L.k.dot(xf.data(), acc.data(), pool);
+            for (int i = 0; i < kv_dim; ++i) row[q_dim + i] = qo_f16_from_f32(acc[i]);
+            L.v.dot(xf.data(), acc.data(), pool);
+            for (int i = 0; i < kv_dim; ++i) row[q_dim + kv_dim + i] = qo_f16_from_f32(acc[i]);
+        }
+        // q/k norm + RoPE, KV append, attention (396-427)
+        if (qo_layer_attn(&sh, D.cap, qkv.data(), rows, q0, L.qn16.data(), L.kn16.data(), D.cos.data(),
+                          D.sin.data(), D.tab_rows, D.k_cache.data() + li * layer_kv,
+                          D.v_cache.data() + li * layer_kv, qout.data(), attn.data(), 0))
+            return;
+        for (int r = 0; r < rows; ++r) {
+            uint16_t* xr = &x[(size_t)r * hs];
+            // o_proj + residual (429): x = f16(x + acc)
+            qo_f16_to_f32_array(&attn[(size_t)r * q_dim], xf.data(), q_dim);
+            L.o.dot(xf.data(), acc.data(), pool);
+            for (int i = 0; i < hs; ++i) xr[i] = qo_f16_from_f32(qo_f32_from_f16(xr[i]) + acc[i]);
+            // post-attention norm, gate/up, SiLU * up, down + residual (433-447)
+            rms_norm_row(xr, L.pln.data(), hs, c.eps, &normed[(size_t)r * hs]);
+            qo_f16_to_f32_array(&normed[(size_t)r * hs], xf.data(), hs);
+            L.gate.dot(xf.data(), acc.data(), pool);
+            for (int i = 0; i < inter; ++i) gate16[i] = qo_f16_from_f32(acc[i]);
+            L.up.dot(xf.data(), acc.data(), pool);
+            for (int i = 0; i < inter; ++i) up16[i] = qo_f16_from_f32(acc[i]);
+            for (int i = 0; i < inter; ++i) {
+                const float g = qo_f32_from_f16(gate16[i]);
+                const float silu = g / (1.0f + std::exp(-g));
+                gate16[i] = qo_f16_from_f32(silu * qo_f32_from_f16(up16[i]));
+            }
+            qo_f16_to_f32_array(gate16.data(), xf.data(), inter);
+            L.down.dot(xf.data(), acc.data(), pool);
+            for (int i = 0; i < hs; ++i) xr[i] = qo_f16_from_f32(qo_f32_from_f16(xr[i]) + acc[i]);
+        }
+    }
+}
+
+// final_norm_logits + argmax (cpu_decoder.rs:458-482): logits against the
+// tied embedding, sequential f32 sums; the first maximum wins.
+int final_logits_argmax(Decoder& D, const uint16_t* x_last, float* logits_out, Pool& pool) {
+    const int hs = D.cfg.hs, vocab = D.cfg.vocab;
+    std::vector<uint16_t> normed(hs);
+    rms_norm_row(x_last, D.norm_w.data(), hs, D.cfg.eps, normed.data());
+    std::vector<float> nf(hs), logits(vocab);
+    qo_f16_to_f32_array(normed.data(), nf.data(), hs);
+    const int64_t blk = 256;
+    pool.run((vocab + blk - 1) / blk, [&](int64_t bi) {
+        const int t1 = std::min<int>(vocab, (int)(bi + 1) * blk);
+        for (int t = (int)bi * blk; t < t1; ++t) {
+            const uint16_t* row = D.embed + (size_t)t * hs;
+            float a = 0.0f;
+            int i = 0;
+            for (; i + 4 <= hs; i += 4) {  // widen 4 at a time, add in order
+                float w4[4];
+                _mm_storeu_ps(w4, _mm_cvtph_ps(_mm_loadl_epi64((const __m128i*)(row + i))));
+                a += w4[0] * nf[i];
+                a += w4[1] * nf[i + 1];
+                a += w4[2] * nf[i + 2];
+                a += w4[3] * nf[i + 3];
+            }
+            for (; i < hs; ++i) a += qo_f32_from_f16(row[i]) * nf[i];
+            logits[t] = a;
+        }
+    });
+    int best = 0;
+    for (int t = 0; t < vocab; ++t)
+        if (logits[t] > logits[best]) best = t;
+    if (logits_out) std::memcpy(logits_out, logits.data(), sizeof(float) * vocab);
+    return best;
+}
+
+}  // namespace
+
+extern "C" {
+
+void* qo_dec_create(const qo_dec_cfg* cfg, const uint16_t* embed, const uint16_t* final_norm,
+                    const uint16_t* const* layer_ptrs, int cap) {
+    if (!cfg || !embed || !final_norm || !layer_ptrs) return nullptr;
+    const qo_dec_cfg& c = *cfg;
+    if (c.hs <= 0 || c.nqh <= 0 || c.nkvh <= 0 || c.nqh % c.nkvh || c.hd <= 0 || c.hd % 4 ||
+        c.inter <= 0 || c.layers <= 0 || c.vocab <= 0 || cap <= 0 || cap > c.max_seq)
+        return nullptr;
+    Decoder* D = new Decoder();
+    D->cfg = c;
+    D->cap = cap;
+    D->embed = embed;
+    D->norm_w = widen(final_norm, c.hs);
+    D->layers.resize(c.layers);
+    const int q_dim = c.nqh * c.hd, kv_dim = c.nkvh * c.hd;
+    for (int l = 0; l < c.layers; ++l) {
+        const uint16_t* const* p = layer_ptrs + 11 * l;
+        DecLayer& L = D->layers[l];
+        L.iln = widen(p[0], c.hs);
+        L.pln = widen(p[1], c.hs);
+        L.qn16.assign(p[2], p[2] + c.hd);
+        L.kn16.assign(p[3], p[3] + c.hd);
+        L.q.load(p[4], q_dim, c.hs);
+        L.k.load(p[5], kv_dim, c.hs);
+        L.v.load(p[6], kv_dim, c.hs);
+        L.o.load(p[7], c.hs, q_dim);
+        L.gate.load(p[8], c.inter, c.hs);
+        L.up.load(p[9], c.inter, c.hs);
+        L.down.load(p[10], c.hs, c.inter);
+    }
+    const size_t kvn = (size_t)c.layers * c.nkvh * cap * c.hd;
+    D->k_cache.assign(kvn, 0.0f);
+    D->v_cache.assign(kvn, 0.0f);
+    return D;
+}
+
+void qo_dec_destroy(void* d) { delete (Decoder*)d; }
+
+int qo_dec_set_rope(void* d, const uint16_t* cos_f16, const uint16_t* sin_f16, int rows) {
+    Decoder* D = (Decoder*)d;
+    if (!D || !cos_f16 || !sin_f16 || rows <= 0) return -1;
+    D->cos = widen(cos_f16, (int64_t)rows * D->cfg.hd);
+    D->sin = widen(sin_f16, (int64_t)rows * D->cfg.hd);
+    D->tab_rows = rows;
+    return 0;
+}
+
+int qo_dec_prefill(void* d, const uint16_t* hidden, int s, int kv_start, float* logits) {
+    Decoder* D = (Decoder*)d;
+    if (!D || !hidden || s <= 0 || kv_start < 0 || kv_start + s > D->cap || kv_start + s > D->tab_rows)
+        return -1;
+    const int hs = D->cfg.hs;
+    std::vector<uint16_t> x(hidden, hidden + (size_t)s * hs);
+    Pool& pool = pool_for(0);
+    forward(*D, x, kv_start, s, pool);
+    D->pos = kv_start + s;
+    const int tok = final_logits_argmax(*D, &x[(size_t)(s - 1) * hs], logits, pool);
+    D->last_token = (uint32_t)tok;
+    return tok;
+}
+
+int qo_dec_step(void* d, float* logits) {
+    Decoder* D = (Decoder*)d;
+    if (!D || D->pos >= D->cap || D->pos >= D->tab_rows) return -1;
+    const int hs = D->cfg.hs;
+    std::vector<uint16_t> x(D->embed + (size_t)D->last_token * hs,
+                            D->embed + (size_t)(D->last_token + 1) * hs);
+    Pool& pool = pool_for(0);
+    forward(*D, x, D->pos, 1, pool);
+    D->pos += 1;
+    const int tok = final_logits_argmax(*D, x.data(), logits, pool);
+    D->last_token = (uint32_t)tok;
+    return tok;
+}
+
+int qo_dec_pos(void* d) { return d ? ((Decoder*)d)->pos : -1; }
 
 }  // extern "C"

@@ -99,6 +99,43 @@ int32_t qo_uniform_int(uint64_t* state, int32_t lo, int32_t hi); /* inclusive */
 
 int qo_hardware_threads(void);
 
+/* ---- the whole text decoder for one sequence (cpu_decoder.rs) -----------
+ * CpuTextDecoder restated for the end-to-end greedy check: rms_norm_row
+ * 261-272, forward 367-456 (q/k/v/o/gate/up/down with dot_transposed's
+ * 4-way partial sums 64-100, f16 after every projection and residual add,
+ * SiLU), final_norm_logits 458-472 (tied embedding), argmax 474-482 (first
+ * maximum), prefill 487-516, step 518-532.  Rows >= 2 of a prefill use the
+ * one-row summation order (the reference calls the gemm crate there).
+ * layer_ptrs: 11 f16 tensors per layer, checkpoint layout [out][in]:
+ *   input_layernorm[hs], post_attention_layernorm[hs], q_norm[hd], k_norm[hd],
+ *   q_proj[nqh*hd][hs], k_proj[nkvh*hd][hs], v_proj[nkvh*hd][hs],
+ *   o_proj[hs][nqh*hd], gate_proj[inter][hs], up_proj[inter][hs],
+ *   down_proj[hs][inter].
+ * The decoder reads the weight arrays in place: the caller keeps them alive
+ * until qo_dec_destroy.  The KV caches hold `cap` positions per layer (no
+ * growth). */
+typedef struct qo_dec_cfg {
+    int32_t hs;
+    int32_t nqh;
+    int32_t nkvh;
+    int32_t hd;
+    int32_t inter;
+    int32_t layers;
+    int32_t vocab;
+    int32_t max_seq;
+    float eps;
+} qo_dec_cfg;
+
+void* qo_dec_create(const qo_dec_cfg* cfg, const uint16_t* embed, const uint16_t* final_norm,
+                    const uint16_t* const* layer_ptrs, int cap);
+void qo_dec_destroy(void* d);
+int qo_dec_set_rope(void* d, const uint16_t* cos_f16, const uint16_t* sin_f16, int rows);
+/* Returns the argmax token of the last row (or -1); logits may be NULL. */
+int qo_dec_prefill(void* d, const uint16_t* hidden, int s, int kv_start, float* logits);
+/* Embeds the previous argmax token and runs one position. */
+int qo_dec_step(void* d, float* logits);
+int qo_dec_pos(void* d);
+
 #ifdef __cplusplus
 }
 #endif

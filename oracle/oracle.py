@@ -12,6 +12,7 @@ the eclipse005/qwen3-asr-wgpu checkout):
   layer_attn      src/cpu_decoder.rs:398-427 (q/k norm-RoPE, KV write, attention)
   mrope tables    src/mrope.rs:5-80, src/inference.rs:1038-1049
   kv_target_cap   src/cpu_decoder.rs:227-229, src/decoder.rs:1610
+  TextDecoder     src/cpu_decoder.rs:261-272, 367-532 (whole decoder, greedy)
 """
 from __future__ import annotations
 
@@ -39,6 +40,12 @@ class Shape(ctypes.Structure):
         ("max_seq", ctypes.c_int32),
         ("eps", ctypes.c_float),
     ]
+
+
+class DecCfg(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in
+                ("hs", "nqh", "nkvh", "hd", "inter", "layers", "vocab", "max_seq")] + [
+        ("eps", ctypes.c_float)]
 
 
 def build() -> str:
@@ -77,6 +84,15 @@ def lib():
         L.qo_attention.argtypes = [ctypes.POINTER(Shape), ctypes.c_int, _u16p, ctypes.c_int,
                                    ctypes.c_int, _f32p, _f32p, _u16p, ctypes.c_int]
         L.qo_kv_target_cap.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.qo_dec_create.restype = ctypes.c_void_p
+        L.qo_dec_create.argtypes = [ctypes.POINTER(DecCfg), _u16p, _u16p,
+                                    ctypes.POINTER(_u16p), ctypes.c_int]
+        L.qo_dec_destroy.argtypes = [ctypes.c_void_p]
+        L.qo_dec_destroy.restype = None
+        L.qo_dec_set_rope.argtypes = [ctypes.c_void_p, _u16p, _u16p, ctypes.c_int]
+        L.qo_dec_prefill.argtypes = [ctypes.c_void_p, _u16p, ctypes.c_int, ctypes.c_int, _f32p]
+        L.qo_dec_step.argtypes = [ctypes.c_void_p, _f32p]
+        L.qo_dec_pos.argtypes = [ctypes.c_void_p]
         L.qo_splitmix64.restype = ctypes.c_uint64
         L.qo_splitmix64.argtypes = [_u64p]
         L.qo_fill_normal_f16.argtypes = [_u64p, ctypes.c_int64, ctypes.c_double,
@@ -233,3 +249,66 @@ class Rng:
 
     def uniform_int(self, lo: int, hi: int) -> int:
         return int(lib().qo_uniform_int(ctypes.byref(self.state), lo, hi))
+
+
+# Per-layer tensor order of TextDecoder (checkpoint names under model.layers.N).
+LAYER_TENSORS = ("input_layernorm", "post_attention_layernorm", "q_norm", "k_norm", "q_proj",
+                 "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+class TextDecoder:
+    """CpuTextDecoder (src/cpu_decoder.rs) for one sequence: prefill then greedy
+    steps, returning argmax tokens and (optionally) the logits.  `weights` maps
+    "embed", "norm" and (layer, name) for name in LAYER_TENSORS to f16 arrays
+    (uint16 bits, checkpoint layout [out][in])."""
+
+    def __init__(self, cfg: dict, weights, cap: int, cos_f16, sin_f16):
+        L = lib()
+        self.cfg = cfg
+        c = DecCfg(cfg["hs"], cfg["nqh"], cfg["nkvh"], cfg["hd"], cfg["inter"], cfg["layers"],
+                   cfg["vocab"], cfg["max_seq"], cfg["eps"])
+        self._keep = [np.ascontiguousarray(weights["embed"], dtype=np.uint16),
+                      np.ascontiguousarray(weights["norm"], dtype=np.uint16)]
+        ptrs = (_u16p * (11 * cfg["layers"]))()
+        for l in range(cfg["layers"]):
+            for i, n in enumerate(LAYER_TENSORS):
+                a = np.ascontiguousarray(weights[(l, n)], dtype=np.uint16)
+                self._keep.append(a)
+                ptrs[11 * l + i] = _p(a, _u16p)
+        self._h = L.qo_dec_create(ctypes.byref(c), _p(self._keep[0], _u16p),
+                                  _p(self._keep[1], _u16p), ptrs, cap)
+        if not self._h:
+            raise ValueError("qo_dec_create rejected the configuration")
+        # the decoder reads the weights in place: self._keep stays alive with it
+        cs = np.ascontiguousarray(cos_f16, dtype=np.uint16)
+        sn = np.ascontiguousarray(sin_f16, dtype=np.uint16)
+        if L.qo_dec_set_rope(self._h, _p(cs, _u16p), _p(sn, _u16p), cs.shape[0]):
+            raise ValueError("qo_dec_set_rope failed")
+
+    def prefill(self, hidden_f16, kv_start: int, want_logits: bool = True):
+        h = np.ascontiguousarray(hidden_f16, dtype=np.uint16)
+        logits = np.empty(self.cfg["vocab"], np.float32) if want_logits else None
+        tok = lib().qo_dec_prefill(self._h, _p(h, _u16p), h.shape[0], kv_start,
+                                   _p(logits, _f32p) if want_logits else None)
+        if tok < 0:
+            raise ValueError("qo_dec_prefill failed")
+        return tok, logits
+
+    def step(self, want_logits: bool = True):
+        logits = np.empty(self.cfg["vocab"], np.float32) if want_logits else None
+        tok = lib().qo_dec_step(self._h, _p(logits, _f32p) if want_logits else None)
+        if tok < 0:
+            raise ValueError("qo_dec_step failed")
+        return tok, logits
+
+    @property
+    def pos(self) -> int:
+        return lib().qo_dec_pos(self._h)
+
+    def close(self):
+        if self._h:
+            lib().qo_dec_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
