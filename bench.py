@@ -297,13 +297,22 @@ def main():
     us = d3["us_per_layer"]
     per_launch_bytes = decode_bytes([L + 1 for L in lens3])
     achieved = per_launch_bytes / (us * 1e-6) / 1e9
-    traffic = None
+    traffic = traffic_pf = None
     tf = os.path.join(REPO, "profiles", "decode_attn_traffic.json")
     if os.path.exists(tf):
         try:
-            traffic = json.load(open(tf)).get("config3_hbm_bytes_per_launch")
+            tj = json.load(open(tf))
+            traffic = tj.get("config3_hbm_bytes_per_launch")
+            traffic_pf = tj.get("prefill4_hbm_bytes_per_launch")
         except Exception:
-            traffic = None
+            traffic = traffic_pf = None
+    if "config4_prefill_last_chunk" in extra:
+        p4 = extra["config4_prefill_last_chunk"]
+        extra["roofline_prefill_config4"] = {
+            "bound": "mfma", "kernel": "prefill_attn_kernel (512 rows at kv_start 7680)",
+            "achieved": round(p4["TFLOPs"], 1), "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
+            "frac": round(p4["TFLOPs"] / MFMA_F16_PEAK_TFS, 4), "traffic": traffic_pf,
+            "flops_per_launch": p4["flops_per_layer"], "avg_launch_us": round(p4["us_per_layer"], 3)}
     roofline = {"bound": "hbm", "kernel": "decode_attn_kernel<true> (fused stage a+b)",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
