@@ -122,6 +122,65 @@ __device__ __forceinline__ void store_tile(const TileRegs& t, f16* Ks, f16* Vt, 
     }
 }
 
+// Merge of the nsp split-K partials of one wave's 32 rows (lane = query row):
+// returns the merged row sum and leaves the merged, unnormalised output in o.
+// The partials are combined in index order whichever workgroup arrives last,
+// so the result is bitwise reproducible.  Pass 1: the row max M (16 m values
+// requested per memory round trip).  Pass 2: partials in groups of G, their
+// (m, l) and, per 8-element chunk, the G x 8 accumulator values requested
+// together.  Unused slots of a group read partial 0's record and drop it.
+template <int G>
+__device__ __forceinline__ float merge_partials(const float* mlw, const float* ow, int nsp,
+                                                float16v (&o)[4]) {
+    float M = kNegInf;
+    for (int i0 = 0; i0 < nsp; i0 += 16) {
+        float mm[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int i = i0 + u;
+            const float v = load_dev(mlw + (int64_t)(i < nsp ? i : 0) * kPrefillItemMl);
+            mm[u] = i < nsp ? v : kNegInf;
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) M = fmaxf(M, mm[u]);
+    }
+    float Ls = 0.0f;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db] = (float16v){};
+    for (int i0 = 0; i0 < nsp; i0 += G) {
+        float w[G];
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+            const int i = i0 + u;
+            const float* rec = mlw + (int64_t)(i < nsp ? i : 0) * kPrefillItemMl;
+            const float mi = load_dev(rec), li = load_dev(rec + 64);
+            w[u] = (i >= nsp || mi == kNegInf) ? 0.0f : fast_exp2(mi - M);
+            Ls = fmaf(i < nsp ? li : 0.0f, w[u], Ls);
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {  // element chunk c: o[c/2][8*(c%2) .. +8]
+            float x[G][8];
+#pragma unroll
+            for (int u = 0; u < G; ++u) {
+                const int i = i0 + u;
+                const float* src = ow + (int64_t)(i < nsp ? i : 0) * kPrefillItemFloats + c * 8 * 64;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float v = load_dev(src + e * 64);
+                    x[u][e] = i < nsp ? v : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < G; ++u)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    o[c >> 1][8 * (c & 1) + e] = fmaf(x[u][e], w[u], o[c >> 1][8 * (c & 1) + e]);
+            __builtin_amdgcn_sched_barrier(0);  // keep the next chunk's loads after this one
+        }
+    }
+    return Ls;
+}
+
 __global__ __launch_bounds__(kThreads, 2) void prefill_attn_kernel(
     PrefillArgs a, PrefillPlan P, float* __restrict__ ws_o, float* __restrict__ ws_ml,
     uint32_t* __restrict__ counters) {
@@ -313,31 +372,15 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_attn_kernel(
     if (!s_last) return;
 
     // Last arrival: merge the nsp partials of this (kv head, row block); each
-    // wave merges its own 32 rows.  (m, l) of all partials first, then the
-    // accumulators partial by partial, 64 independent loads in flight each.
+    // wave merges its own 32 rows.
     const int it0 = kvh * P.items_per_kvh + P.sp_base[rb];
-    float M = kNegInf;
-    for (int i = 0; i < nsp; ++i)
-        M = fmaxf(M, load_dev(ws_ml + (int64_t)(it0 + i) * kPrefillItemMl + wave * kPrefillWaveMl + lane));
-    float Ls = 0.0f;
-    float16v acc[4];
-#pragma unroll
-    for (int db = 0; db < 4; ++db) acc[db] = (float16v){};
-    for (int i = 0; i < nsp; ++i) {
-        const float* pm = ws_ml + (int64_t)(it0 + i) * kPrefillItemMl + wave * kPrefillWaveMl;
-        const float* pi = ws_o + (int64_t)(it0 + i) * kPrefillItemFloats + wave * kPrefillWaveFloats;
-        float x[64];
-#pragma unroll
-        for (int e = 0; e < 64; ++e) x[e] = load_dev(pi + e * 64 + lane);
-        const float mi = load_dev(pm + lane);
-        const float li = load_dev(pm + 64 + lane);
-        const float w = mi == kNegInf ? 0.0f : fast_exp2(mi - M);
-        Ls = fmaf(li, w, Ls);
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[db][e] = fmaf(x[db * 16 + e], w, acc[db][e]);
-    }
+    const float* mlw = ws_ml + (int64_t)it0 * kPrefillItemMl + wave * kPrefillWaveMl + lane;
+    const float* ow = ws_o + (int64_t)it0 * kPrefillItemFloats + wave * kPrefillWaveFloats + lane;
+    float Ls;
+    if (nsp <= 2)
+        Ls = merge_partials<2>(mlw, ow, nsp, o);
+    else
+        Ls = merge_partials<8>(mlw, ow, nsp, o);
     if (row_ok) {
         const float inv = 1.0f / Ls;
 #pragma unroll
@@ -346,7 +389,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_attn_kernel(
             for (int q4 = 0; q4 < 4; ++q4) {
                 half4v h4;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) h4[e] = (f16)(acc[db][q4 * 4 + e] * inv);
+                for (int e = 0; e < 4; ++e) h4[e] = (f16)(o[db][q4 * 4 + e] * inv);
                 *(half4v*)(orow + db * 32 + 8 * q4 + 4 * g) = h4;
             }
     }
