@@ -6,6 +6,9 @@ shared library next to this file.  Flags:
   -fhip-fp32-correctly-rounded-divide-sqrt           IEEE '/' and sqrtf (stage (a)
                                                      is bit-exact against the
                                                      reference CPU path)
+Per file: prefill_attn.hip adds -amdgpu-mfma-vgpr-form, which keeps the MFMA
+accumulators in VGPRs; otherwise its one-wave-per-SIMD kernel puts O in AGPRs
+and every rescale and loop-carried copy goes through v_accvgpr moves.
 """
 from __future__ import annotations
 
@@ -37,13 +40,18 @@ FLAGS = [
 ]
 
 
+PER_FILE = {
+    "prefill_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *PER_FILE.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")

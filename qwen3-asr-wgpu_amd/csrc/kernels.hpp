@@ -86,7 +86,7 @@ struct PrefillArgs {
     float scale_log2;
 };
 
-// Stage (c) plan: row blocks of 64 rows; row block rb's key tiles (64 keys)
+// Stage (c) plan: row blocks of 64 rows; row block rb's key tiles (128 keys)
 // are split into ceil(tiles / tps) pieces.  Items of a kv head are laid out
 // rb-major: item = kvh*items_per_kvh + sp_base[rb] + split.
 constexpr int kMaxRowBlocks = 64;  // 4096 rows per launch
@@ -107,7 +107,9 @@ struct PrefillWs {
     uint32_t* counters;  // [nkvh * kMaxRowBlocks]
     int64_t items;
 };
-constexpr int kPrefillWaves = 4;
+constexpr int kPrefillWaves = 4;      // waves that own rows (2 q heads x 2 x 32 rows)
+constexpr int kPrefillKeyGroups = 2;  // each row wave has a twin taking the other half of every tile
+constexpr int kPrefillTileKeys = 128;
 constexpr int64_t kPrefillWaveFloats = 64 * 64;  // 64 accumulator elements x 64 lanes
 constexpr int64_t kPrefillWaveMl = 2 * 64;       // m and l of each lane
 constexpr int64_t kPrefillItemFloats = kPrefillWaves * kPrefillWaveFloats;

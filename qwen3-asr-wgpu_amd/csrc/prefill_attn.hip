@@ -9,22 +9,27 @@
 // f16 score or probability matrix in memory.  Semantics: src/cpu_decoder.rs:
 // 292-365 with rows = s, q0 = kv_start.
 //
-// Work item = (kv head, block of 64 query rows, split of the key range).
-// 4 waves: wave w takes q head 2*kvh + (w&1) and rows (w>>1)*32..+32 of the
-// block, so both q heads of a kv head share each K/V tile staged in LDS.
-// Items are laid out kv-head minor (blockIdx % nkvh = kv head): with 8 kv
-// heads and workgroups dealt round-robin to the 8 XCDs, every row block and
-// split of one kv head runs on the same XCD and reuses its K/V through that
-// XCD's L2.
+// Work item = (kv head, block of 64 query rows, split of the key range), one
+// 8-wave workgroup per CU (two waves per SIMD).  Row wave rw = wave & 3 takes
+// q head 2*kvh + (rw&1) and rows (rw>>1)*32..+32 of the block, so both q
+// heads of a kv head share each K/V tile in LDS; key group kg = wave >> 2
+// takes keys 64*kg..+64 of every 128-key tile, and the two key groups of a
+// row wave are merged through LDS at the end.  Two waves per SIMD let one
+// wave's softmax (VALU) run while the other's MFMAs do.  Items are laid out
+// kv-head minor (blockIdx % nkvh = kv head): with 8 kv heads and workgroups
+// dealt round-robin to the 8 XCDs, every row block and split of one kv head
+// runs on the same XCD and reuses its K/V through that XCD's L2.
+//
 // Each wave computes S^T = K Q^T (keys on the MFMA M axis, queries on N), so a
-// lane owns one query column: row max / row sum need one cross-half shuffle,
+// lane owns one query column: row max / row sum need one cross-half swap,
 // and the probabilities are already in the B-operand layout of O^T += V^T P^T.
-// K/V tiles of 64 keys are double-buffered in LDS (V transposed to [dim][key],
-// key columns XOR-swizzled per 8 dims, while it is stored): the next tile's global loads (buffer loads whose range
-// ends at the row block's last key, so the tail reads zeros) are in flight
-// while the current tile's MFMAs run, with one barrier per tile.  Only tiles
-// that straddle the diagonal are masked, and O is rescaled only when a row
-// max moved.
+// The running max is moved (and O rescaled) only when a row max exceeds it by
+// more than 2^8, so p <= 256 and the rescale branch is rarely taken; the
+// result is the same softmax.  Only key halves that straddle the diagonal are
+// masked, and halves wholly past it are skipped.
+// K/V tiles are copied global -> LDS directly (buffer_load ... lds, rows past
+// the row block's last key clamped to it), double buffered: the copy of tile
+// t+1 is in flight while tile t is consumed.
 // When the key range of a row block is split, each item publishes its partial
 // (max, sum, unnormalised O) with device-scope stores and the last to arrive
 // merges (ticket), as in the decode kernel.
@@ -37,23 +42,24 @@ namespace qasr {
 
 namespace {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int kWaves = kPrefillWaves;
-constexpr int kThreads = kWaves * 64;
+constexpr int kWaves = kPrefillWaves;            // row waves
+constexpr int kAllWaves = kWaves * kPrefillKeyGroups;
+constexpr int kThreads = kAllWaves * 64;
 // The split workspace holds exactly what one wave publishes: its 4 x 16
 // accumulator registers for 64 lanes, and (m, l) for 64 lanes.
 static_assert(kPrefillWaveFloats == 4 * 16 * 64, "partial O record size");
 static_assert(kPrefillWaveMl == 2 * 64, "partial (m, l) record size");
 constexpr int kRowsPerBlock = kPrefillRows;
-constexpr int kTileKeys = 64;
-constexpr int kKPad = kHeadDim + 8;   // Ks row stride (halves)
-constexpr int kVPad = kTileKeys + 8;  // Vt row stride (halves)
-constexpr int kKsHalves = kTileKeys * kKPad;
-// One past the last V^T element (row 127 at skew 4*15, position 63; see
-// vt_index), rounded up to 16 bytes so both buffers stay 16-byte aligned.
-constexpr int kVtHalves = ((kHeadDim - 1) * kVPad + 4 * ((kHeadDim - 1) >> 3) + kTileKeys + 7) / 8 * 8;
+constexpr int kTileKeys = kPrefillTileKeys;         // keys per LDS tile
+constexpr int kGroupKeys = kTileKeys / kPrefillKeyGroups;  // keys per key group
+static_assert(kGroupKeys == 64, "a key group's half tile is one 64-key wave step");
+constexpr int kTileHalves = kTileKeys * kHeadDim;  // one 32 KB K or V tile
 constexpr float kNegInf = -__builtin_inff();
+constexpr float kRescaleSlack = 8.0f;  // log2 of the largest p before the max moves
+
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) short4v lds_short4v;
 
 __device__ __forceinline__ float16v mfma32(const half8v& a, const half8v& b, const float16v& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -70,56 +76,166 @@ __device__ __forceinline__ float halves_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, bytes, 0x00020000);
+// ---- LDS tile layouts ----------------------------------------------------
+// LDS serves 16 lanes of a 16-byte read (or 32 lanes of an 8-byte read) per
+// cycle from 64 banks, so each such lane group must cover 256 distinct bytes
+// modulo 256.
+//
+// K tile: row r (key) is 256 contiguous bytes; its 16-byte chunk c (dims
+// 8c..8c+7) sits at slot c ^ swz16(r).  swz16 permutes 0..15 over every 16
+// consecutive rows, so the K operand read (16 consecutive rows, one chunk)
+// hits 16 different slots.
+__device__ __forceinline__ int swz16(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+// V tile: four slabs of 32 dims, [dims/32][row][32 dims], 8 KB each.  The
+// transposing read of 4 consecutive rows x 32 dims is then 256 contiguous
+// bytes, and every operand address is a per-lane base plus a constant.
+//
+// Both tiles arrive by direct global -> LDS copies: instruction j of wave w
+// (of 8) writes LDS bytes [(8j + w) KB, +1 KB), lane l at +16 l.
+//   K: row 32j + 4w + l/16, slot l%16 = chunk (l%16) ^ swz16(4w + l/16);
+//   V: slab j, rows 16w + l/4, dims 32j + 8(l%4) .. +8.
+// Per thread the global source row is fixed within the tile (plus 32 j for K;
+// V instruction j reads the next 64 bytes of the same row).
+// The copies are issued as inline asm (M0 = LDS destination): the compiler
+// then does not wait for them before unrelated LDS reads of the other
+// buffers; the kernel waits for them itself (vmcnt(0)) before each barrier.
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4v make_rsrc_words(const void* p, int bytes) {
+    const uint64_t a = (uint64_t)p;
+    return (u32x4v){(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)bytes, 0x00020000u};
+}
+__device__ __forceinline__ uint32_t lds_addr(const f16* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void dma16(u32x4v rsrc, int voff, uint32_t lds) {
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
+}
+// Rows past the last key of the row block (only in its last tile) are read
+// from row kend-1 instead: masked keys get p = 0, and 0 * (finite V) = 0,
+// whereas an out-of-range copy would leave whatever the LDS held before.
+// t0: first key of the tile; krow/vrow, kchunk/vchunk: this thread's row
+// within the tile and byte offset within the row (see the layout above).
+__device__ __forceinline__ void dma_tile(u32x4v kr, u32x4v vr, int t0, int kend, int krow,
+                                         int kchunk, int vrow, int vchunk, const f16* kdst,
+                                         const f16* vdst, int wave) {
+    const int last = kend - 1;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int rk = min(t0 + krow + 32 * j, last);
+        dma16(kr, rk * 256 + kchunk, lds_addr(kdst + (8 * j + wave) * 512));
+    }
+    const int rv = min(t0 + vrow, last);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(vr, rv * 256 + vchunk + j * 64, lds_addr(vdst + (8 * j + wave) * 512));
+}
+static_assert(kAllWaves == 8 && kTileKeys == 128, "copy pattern: 32 one-KB blocks per tile over 8 waves");
+
+// 4 halves of V^T: ds_read_b64_tr_b16 transposes 16-bit elements within each
+// 16-lane group (result lane 4m+e, element k <- source lane 4k+m, element e).
+__device__ __forceinline__ half4v read_tr(const f16* p) {
+    return __builtin_bit_cast(half4v, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v*)p));
 }
 
-// One 64-key tile of K and V: 4 + 4 dwordx4 per thread (thread t, chunk c
-// covers key (c*256+t)/16, dims ((c*256+t)%16)*8..+8).
-struct TileRegs {
-    uint4 k[4];
-    uint4 v[4];
+// Per-wave state.
+struct Wave {
+    half8v qb[8];     // Q^T B operand, k-step ks: dims 16*ks + 8*g .. +8 of query n
+    float16v o[4];    // O^T: o[db][i] = dim db*32 + 8*(i/4) + 4*g + i%4 of query n
+    float m;          // running max the exponents are taken against
+    float l;          // running row sum
+    int kaddr[8];     // K operand of k-step ks, rows 0..31 of the half tile (halves)
+    int vbase;        // V^T operand source address, slab 0, key 0 (halves)
+    int g, qpos;
+    float scale_log2;
 };
 
-__device__ __forceinline__ void load_tile(__amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
-                                          int k0, int tid, TileRegs& t) {
+// First half of a 64-key step: S^T from K rows kt[0..63] (first key k0),
+// row max, the running-max update, P^T (f16, B-operand layout) and its row
+// sum.  MASK: some key is past some row's position.
+template <bool MASK>
+__device__ __forceinline__ void step_s(Wave& w, const f16* kt, int k0, half8v (&pb)[4]) {
+    // S^T: keys kb*32 + (8*(i/4) + 4*g + i%4) x query n, accumulated over dims.
+    float16v s[2] = {(float16v){}, (float16v){}};
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int off = (k0 * kHeadDim + (c * kThreads + tid) * 8) * 2;
-        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0);
-        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0);
-        t.k[c] = make_uint4(a.x, a.y, a.z, a.w);
-        t.v[c] = make_uint4(b.x, b.y, b.z, b.w);
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const half8v ka = *(const half8v*)&kt[kb * 32 * kHeadDim + w.kaddr[ks]];
+            s[kb] = mfma32(ka, w.qb[ks], s[kb]);
+        }
+    // Operand reads run at most two k-steps ahead of the MFMAs (bounded
+    // register lifetime; 16 reads + 16 MFMAs).
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    float mx = kNegInf;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            if (MASK) {
+                const int key = k0 + kb * 32 + 8 * (i >> 2) + 4 * w.g + (i & 3);
+                s[kb][i] = key > w.qpos ? kNegInf : s[kb][i];
+            }
+            mx = fmaxf(mx, s[kb][i]);
+        }
+    mx = halves_max(mx) * w.scale_log2;
+    // Move the running max when a row max passed it by more than the slack.
+    {
+        const bool up = mx > w.m + kRescaleSlack;
+        if (__ballot(up)) {
+            const float mn = up ? mx : w.m;
+            const float alpha = w.m == kNegInf ? 0.0f : fast_exp2(w.m - mn);
+#pragma unroll
+            for (int db = 0; db < 4; ++db) w.o[db] *= alpha;
+            w.l *= alpha;
+            w.m = mn;
+        }
+    }
+    const float mu = w.m == kNegInf ? 0.0f : w.m;
+    // P^T = 2^(s*scale_log2 - m), k-step w4 covering keys 16*w4 + 4*g +
+    // {0..3, 8..11}; the row sum from the same f16 values (v_dot2, f32 sum).
+#pragma unroll
+    for (int w4 = 0; w4 < 4; ++w4)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            pb[w4][j] = (f16)fast_exp2(fmaf(s[w4 >> 1][8 * (w4 & 1) + j], w.scale_log2, -mu));
+    const half2v ones2 = {(f16)1.0f, (f16)1.0f};
+    float ps = 0.0f;
+#pragma unroll
+    for (int w4 = 0; w4 < 4; ++w4)
+#pragma unroll
+        for (int q2 = 0; q2 < 4; ++q2) {
+            const half2v pr = {pb[w4][2 * q2], pb[w4][2 * q2 + 1]};
+            ps = __builtin_amdgcn_fdot2(pr, ones2, ps, false);
+        }
+    w.l += halves_sum(ps);
 }
 
-// V^T element (dim, key) of a 64-key tile, in halves.
-//  * Within each 16-key block, key bits 2 and 3 are swapped, so the keys one
-//    lane feeds to a k-step, 4g + {0..3} and 4g + {8..11}, are 8 contiguous
-//    halves (one ds_read2_b64 into the 4 registers of the operand).
-//  * Row dim starts at dim*kVPad + 4*(dim/8): the 16 lanes that store dims
-//    8j + e of one key then fall 2*j dwords apart, on 16 different banks.
-//    The skew never decreases with dim and kVPad - 64 >= 4, so rows never
-//    overlap.
-__device__ __forceinline__ int vt_pos(int key) {
-    return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
-}
-__device__ __forceinline__ int vt_index(int dim, int key) {
-    return dim * kVPad + 4 * (dim >> 3) + vt_pos(key);
-}
-static_assert(kVPad - kTileKeys >= 4, "V^T rows would overlap");
-
-__device__ __forceinline__ void store_tile(const TileRegs& t, f16* Ks, f16* Vt, int tid) {
+// Second half: O^T += V^T P^T with V rows vt[0..63] (slab stride
+// kTileKeys*32 halves).
+__device__ __forceinline__ void step_pv(Wave& w, const f16* vt, const half8v (&pb)[4]) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int idx = c * kThreads + tid;
-        const int key = idx >> 4, dseg = (idx & 15) * 8;
-        *(uint4*)&Ks[key * kKPad + dseg] = t.k[c];
-        H8 v;
-        v.u = t.v[c];
+    for (int w4 = 0; w4 < 4; ++w4)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) Vt[vt_index(dseg + e, key)] = v.e[e];
+        for (int db = 0; db < 4; ++db) {
+            const f16* vp = vt + w.vbase + db * (kTileKeys * 32) + w4 * 16 * 32;
+            const half4v lo = read_tr(vp);
+            const half4v hi = read_tr(vp + 8 * 32);
+            const half8v va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+            w.o[db] = mfma32(va, pb[w4], w.o[db]);
+        }
+    // Two transposing reads per MFMA, at most two MFMAs ahead.
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 14; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
 }
 
 // Merge of the nsp split-K partials of one wave's 32 rows (lane = query row):
@@ -181,16 +297,20 @@ __device__ __forceinline__ float merge_partials(const float* mlw, const float* o
     return Ls;
 }
 
-__global__ __launch_bounds__(kThreads, 2) void prefill_attn_kernel(
+__global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     PrefillArgs a, PrefillPlan P, float* __restrict__ ws_o, float* __restrict__ ws_ml,
     uint32_t* __restrict__ counters) {
-    __shared__ __attribute__((aligned(16))) f16 Ks[2][kKsHalves];
-    __shared__ __attribute__((aligned(16))) f16 Vt[2][kVtHalves];
-    __shared__ int s_last;
+    // 128 KB: K and V tiles, double buffered.
+    __shared__ __attribute__((aligned(16))) f16 K0[kTileHalves];
+    __shared__ __attribute__((aligned(16))) f16 K1[kTileHalves];
+    __shared__ __attribute__((aligned(16))) f16 V0[kTileHalves];
+    __shared__ __attribute__((aligned(16))) f16 V1[kTileHalves];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = tid >> 6;       // 0..7: copy slot
+    const int rw = wave & 3;         // row wave
+    const int kg = wave >> 2;        // key group
     const int n = lane & 31;  // query column within the wave's 32 rows
     const int g = lane >> 5;  // k-slot group of the MFMA operands
 
@@ -214,130 +334,121 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_attn_kernel(
     const int t_begin = sp * P.tps;
     const int t_end = min(t_begin + P.tps, ntiles);
 
-    const int hh = wave & 1;
-    const int head = kvh * kRep + hh;
-    const int wrow0 = row0 + (wave >> 1) * 32;  // first row of this wave
-    const int r = wrow0 + n;                      // this lane's query row
+    const int head = kvh * kRep + (rw & 1);
+    const int wrow0 = row0 + (rw >> 1) * 32;  // first row of this wave
+    const int r = wrow0 + n;                    // this lane's query row
     const bool row_ok = r < a.s;
-    const int qpos = a.kv_start + r;
     const int ldq = a.nqh * kHeadDim;
+    // Key range of the wave's rows: a half tile from key k0 on is masked when
+    // k0 + 63 > first_pos and skipped when k0 > last_pos.
+    const int first_pos = a.kv_start + wrow0;
+    const int last_pos = first_pos + 31;
 
-    const __amdgpu_buffer_rsrc_t kres = make_rsrc(a.k + kvh * a.head_stride, kend * kHeadDim * 2);
-    const __amdgpu_buffer_rsrc_t vres = make_rsrc(a.v + kvh * a.head_stride, kend * kHeadDim * 2);
+    const u32x4v kres = make_rsrc_words(a.k + kvh * a.head_stride, kend * kHeadDim * 2);
+    const u32x4v vres = make_rsrc_words(a.v + kvh * a.head_stride, kend * kHeadDim * 2);
+    // This thread's copy slots (see the layout notes above dma16).
+    const int krow = 4 * wave + (lane >> 4);
+    const int kchunk = ((lane & 15) ^ swz16(krow)) * 16;
+    const int vrow = 16 * wave + (lane >> 2);
+    const int vchunk = (lane & 3) * 16;
 
-    TileRegs pre;
-    load_tile(kres, vres, t_begin * kTileKeys, tid, pre);
+    dma_tile(kres, vres, t_begin * kTileKeys, kend, krow, kchunk, vrow, vchunk, K0, V0, wave);
 
-    // Q^T as B operand: k-step ks covers dims ks*16 + g*8 .. +8.
-    half8v qb[8];
+    Wave w;
+    w.g = g;
+    w.qpos = a.kv_start + r;
+    w.scale_log2 = a.scale_log2;
     {
         const f16* qrow = a.q + (int64_t)(row_ok ? r : 0) * ldq + head * kHeadDim + g * 8;
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             H8 t;
             t.u = row_ok ? *(const uint4*)(qrow + ks * 16) : make_uint4(0, 0, 0, 0);
-            qb[ks] = t.h;
+            w.qb[ks] = t.h;
         }
     }
+#pragma unroll
+    for (int db = 0; db < 4; ++db) w.o[db] = (float16v){};
+    w.m = kNegInf;
+    w.l = 0.0f;
+    // K operand of k-step ks: row n, chunk 2*ks + g; V^T operand: source lane
+    // 16*q4 + 4*k + m reads row 4*(q4>>1) + k, dims 16*(q4&1) + 4*m .. +3.
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) w.kaddr[ks] = n * kHeadDim + (((2 * ks + g) ^ swz16(n)) * 8);
+    {
+        const int q4 = lane >> 4;
+        w.vbase = (4 * (q4 >> 1) + ((lane >> 2) & 3)) * 32 + 16 * (q4 & 1) + 4 * (lane & 3);
+    }
 
-    float m = kNegInf, lsum = 0.0f;
-    float16v o[4];
-#pragma unroll
-    for (int db = 0; db < 4; ++db) o[db] = (float16v){};
-
-    // V^T operand of k-step w4, dims db*32..+32: keys 16*w4 + 4*g + {0..3,
-    // 8..11} of dim db*32 + n sit at vt_index(dim, 16*w4 + 4*g) .. +8, which
-    // is the per-lane vlane plus a compile-time offset (dim>>3 = 4*db + n/8).
-    const int vlane = n * kVPad + 4 * (n >> 3) + 8 * g;
-    const half2v ones2 = {(f16)1.0f, (f16)1.0f};
-
-    store_tile(pre, Ks[0], Vt[0], tid);
-    __syncthreads();
-
-    for (int t = t_begin; t < t_end; ++t) {
-        const int buf = (t - t_begin) & 1;
-        const int k0 = t * kTileKeys;
-        if (t + 1 < t_end) load_tile(kres, vres, k0 + kTileKeys, tid, pre);
-        const f16* ks_ = Ks[buf];
-        const f16* vt_ = Vt[buf];
-
-        // S^T: keys kb*32 + (8*(i/4) + 4*g + i%4) x query n, accumulated over dims.
-        float16v st[2] = {(float16v){}, (float16v){}};
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const half8v ka = *(const half8v*)&ks_[(kb * 32 + n) * kKPad + ks * 16 + g * 8];
-                st[kb] = mfma32(ka, qb[ks], st[kb]);
-            }
-        // Row max on the raw scores (the scale is positive), scaled once; the
-        // scale is then folded into the exponent: p = 2^(s*scale_log2 - m).
-        float mx = kNegInf;
-        if (k0 + kTileKeys - 1 <= a.kv_start + wrow0) {  // whole tile visible to the wave
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[kb][i]);
-        } else {
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int key = k0 + kb * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-                    const float v = key > qpos ? kNegInf : st[kb][i];
-                    st[kb][i] = v;
-                    mx = fmaxf(mx, v);
-                }
-        }
-        mx = halves_max(mx) * a.scale_log2;
-        const float mn = fmaxf(m, mx);
-        const float mu = mn == kNegInf ? 0.0f : mn;
-        const float alpha = fast_exp2(m - mu);
-        m = mn;
-        // P^T in the B-operand layout, k-step w4 covering tile keys
-        // 16*w4 + 4*g + {0..3, 8..11}; its row sum is taken from the same f16
-        // values the MFMA consumes (v_dot2 against ones, f32 accumulate).
-        half8v pb[4];
-#pragma unroll
-        for (int w4 = 0; w4 < 4; ++w4)
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                pb[w4][j] = (f16)fast_exp2(fmaf(st[w4 >> 1][8 * (w4 & 1) + j], a.scale_log2, -mu));
-        float ps = 0.0f;
-#pragma unroll
-        for (int w4 = 0; w4 < 4; ++w4)
-#pragma unroll
-            for (int q2 = 0; q2 < 4; ++q2) {
-                const half2v pr = {pb[w4][2 * q2], pb[w4][2 * q2 + 1]};
-                ps = __builtin_amdgcn_fdot2(pr, ones2, ps, false);
-            }
-        ps = halves_sum(ps);
-        lsum = lsum * alpha + ps;
-        if (__ballot(alpha != 1.0f)) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db) o[db] *= alpha;
-        }
-
-        // O^T += V^T P^T.
-#pragma unroll
-        for (int w4 = 0; w4 < 4; ++w4) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const f16* vp = vt_ + vlane + db * (32 * kVPad + 16) + 16 * w4;
-                const half4v lo = *(const half4v*)vp;
-                const half4v hi = *(const half4v*)(vp + 4);
-                const half8v va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                o[db] = mfma32(va, pb[w4], o[db]);
-            }
-        }
-        if (t + 1 < t_end) store_tile(pre, Ks[buf ^ 1], Vt[buf ^ 1], tid);
+    // This thread's tile copies have landed, then every wave's have.
+    auto tile_sync = [&]() {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
+    };
+    // Tile t: start the copy of tile t+1 into the other buffers, then this
+    // wave's half of tile t.  Two tiles per iteration, so every LDS address
+    // is a per-lane base plus a constant.
+    auto run = [&](const f16* kt, const f16* vt, const f16* kn, const f16* vn, int t) {
+        if (t + 1 < t_end)
+            dma_tile(kres, vres, (t + 1) * kTileKeys, kend, krow, kchunk, vrow, vchunk, kn, vn, wave);
+        const int k0 = t * kTileKeys + kg * kGroupKeys;
+        if (k0 <= last_pos) {  // some key visible to some row
+            const f16* kh = kt + kg * kGroupKeys * kHeadDim;
+            const f16* vh = vt + kg * kGroupKeys * 32;
+            half8v pb[4];
+            if (k0 + kGroupKeys - 1 <= first_pos)  // no key masked
+                step_s<false>(w, kh, k0, pb);
+            else
+                step_s<true>(w, kh, k0, pb);
+            step_pv(w, vh, pb);
+        }
+        tile_sync();
+    };
+    tile_sync();  // tile t_begin and Q
+    for (int t = t_begin;;) {
+        run(K0, V0, K1, V1, t);
+        if (++t >= t_end) break;
+        run(K1, V1, K0, V0, t);
+        if (++t >= t_end) break;
     }
+
+    // Key group 1 hands its (m, l, O) to key group 0 through LDS (the tile
+    // buffers are free now), element-major so every access is 256 contiguous
+    // bytes.
+    float* xo = reinterpret_cast<float*>(rw < 2 ? K0 : K1) + (rw & 1) * (64 * 64);
+    float* xml = reinterpret_cast<float*>(V1) + rw * 128;
+    int& s_last = *reinterpret_cast<int*>(V0);
+    static_assert(2 * 64 * 64 * 4 <= kTileHalves * 2, "two row waves' O per K buffer");
+    if (kg == 1) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) xo[(db * 16 + i) * 64 + lane] = w.o[db][i];
+        xml[lane] = w.m;
+        xml[64 + lane] = w.l;
+    }
+    __syncthreads();
+    if (kg == 0) {
+        const float m1 = xml[lane], l1 = xml[64 + lane];
+        const float M = fmaxf(w.m, m1);
+        const float a0 = w.m == kNegInf ? 0.0f : fast_exp2(w.m - M);
+        const float a1 = m1 == kNegInf ? 0.0f : fast_exp2(m1 - M);
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                w.o[db][i] = w.o[db][i] * a0 + xo[(db * 16 + i) * 64 + lane] * a1;
+        w.l = w.l * a0 + l1 * a1;
+        w.m = M;
+    }
+    float16v (&o)[4] = w.o;
+    const float m = w.m, lsum = w.l;
 
     // o[db][i] holds dim db*32 + 8*(i/4) + 4*g + i%4 of query row r.
     f16* orow = a.out + (int64_t)r * ldq + head * kHeadDim;
+    const bool owner = kg == 0;  // key group 0 holds the merged result
     if (nsp == 1) {
-        if (row_ok) {
+        if (owner && row_ok) {
             const float inv = 1.0f / lsum;
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
@@ -357,25 +468,27 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_attn_kernel(
     // (element e of lane l at [e][l]) so every store and load instruction
     // moves 256 contiguous bytes; then (m, l) per lane.  Published with
     // device-scope stores (see stores_done_barrier).
-    float* po = ws_o + (int64_t)item * kPrefillItemFloats + wave * kPrefillWaveFloats;
+    if (owner) {
+        float* po = ws_o + (int64_t)item * kPrefillItemFloats + rw * kPrefillWaveFloats;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+        for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) store_dev(po + (db * 16 + i) * 64 + lane, o[db][i]);
-    float* pml = ws_ml + (int64_t)item * kPrefillItemMl + wave * kPrefillWaveMl;
-    store_dev(pml + lane, m);
-    store_dev(pml + 64 + lane, lsum);
+            for (int i = 0; i < 16; ++i) store_dev(po + (db * 16 + i) * 64 + lane, o[db][i]);
+        float* pml = ws_ml + (int64_t)item * kPrefillItemMl + rw * kPrefillWaveMl;
+        store_dev(pml + lane, m);
+        store_dev(pml + 64 + lane, lsum);
+    }
     stores_done_barrier();
     uint32_t* ctr = &counters[kvh * P.nrb + rb];
     if (tid == 0) s_last = (ticket_add(ctr) == (uint32_t)(nsp - 1));
     __syncthreads();
-    if (!s_last) return;
+    if (!s_last || !owner) return;
 
     // Last arrival: merge the nsp partials of this (kv head, row block); each
-    // wave merges its own 32 rows.
+    // row wave merges its own 32 rows.
     const int it0 = kvh * P.items_per_kvh + P.sp_base[rb];
-    const float* mlw = ws_ml + (int64_t)it0 * kPrefillItemMl + wave * kPrefillWaveMl + lane;
-    const float* ow = ws_o + (int64_t)it0 * kPrefillItemFloats + wave * kPrefillWaveFloats + lane;
+    const float* mlw = ws_ml + (int64_t)it0 * kPrefillItemMl + rw * kPrefillWaveMl + lane;
+    const float* ow = ws_o + (int64_t)it0 * kPrefillItemFloats + rw * kPrefillWaveFloats + lane;
     float Ls;
     if (nsp <= 2)
         Ls = merge_partials<2>(mlw, ow, nsp, o);
@@ -393,7 +506,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_attn_kernel(
                 *(half4v*)(orow + db * 32 + 8 * q4 + 4 * g) = h4;
             }
     }
-    if (tid == 0) ticket_reset(ctr);
+    if (tid == 0) ticket_reset(ctr);  // tid 0 is in key group 0
 }
 
 }  // namespace

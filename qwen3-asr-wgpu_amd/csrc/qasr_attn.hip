@@ -635,14 +635,15 @@ int qasr_prefill_attn(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_st
     for (int r0 = 0; r0 < s; r0 += rows_per_launch) {
         const int rows = std::min(rows_per_launch, s - r0);
         const int ks = kv_start + r0;
-        // Tiles per split: enough items to give every CU work, without
+        // Tiles per split: about one workgroup per CU (256), without
         // splitting row blocks whose key range is short.
         int tps = tps_forced;
         if (tps <= 0) {
             const int nrb = (rows + qasr::kPrefillRows - 1) / qasr::kPrefillRows;
-            const int64_t tiles_all = (int64_t)nrb * ((ks + rows + 63) / 64);
-            const int64_t want = std::max<int64_t>(1, 512 / nkvh);
-            tps = (int)std::max<int64_t>(4, (tiles_all + want - 1) / want);
+            const int64_t tiles_all =
+                (int64_t)nrb * ((ks + rows + qasr::kPrefillTileKeys - 1) / qasr::kPrefillTileKeys);
+            const int64_t want = std::max<int64_t>(1, 256 / nkvh);
+            tps = (int)std::max<int64_t>(2, (tiles_all + want - 1) / want);
         }
         qasr::PrefillPlan P = qasr::plan_prefill(rows, ks, nkvh, tps);
         rc = ensure_prefill_ws(kv, (int64_t)P.items_per_kvh * nkvh);
