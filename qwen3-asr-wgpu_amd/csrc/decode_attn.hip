@@ -47,6 +47,7 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kNegInf = -__builtin_inff();
+constexpr int kSc1 = 16;  // buffer cache policy: sc1 (device-coherent, as agent-scope atomics)
 
 __device__ __forceinline__ float dot8(const H8& a, const H8& b) {
     float s = 0.0f;
@@ -92,7 +93,7 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     __shared__ float s_wm[4 * W][2];
     __shared__ float s_wl[4 * W][2];
     __shared__ float s_wa[4 * W][2][kHeadDim];
-    __shared__ float s_ml[kDecodeMaxChunksPerEntry][4];
+    __shared__ __attribute__((aligned(16))) float s_ml[16][4];  // one merge batch
     __shared__ int s_last;
 
     const int wg = blockIdx.x;
@@ -334,39 +335,43 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     __syncthreads();
     if (!s_last) return;
 
-    // Last arrival: merge the nch partials of (b, kv head).  The (m, l) of
-    // every chunk (to LDS) and this thread's first kBatch partial outputs are
-    // requested together, so up to kBatch chunks merge in one memory round
-    // trip.
+    // Last arrival: merge the nch partials of (b, kv head), online (running
+    // max, rescaled sums) in chunk order.  Per batch of 16 chunks the (m, l)
+    // of each (one 16-byte load per chunk, to LDS) and this thread's element
+    // of each are requested together as plain device-coherent (sc1) loads, so
+    // a batch costs one memory round trip.
     const int64_t it0 = P.wg_base[b] + kvh * nch;
-    if (tid < nch) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) s_ml[tid][k] = load_dev(&ws_ml[(it0 + tid) * 4 + k]);
-    }
-    constexpr int kBatch = 64;
-    float x[kBatch];
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u)
-        x[u] = u < nch ? load_dev(&ws_acc[(it0 + u) * (2 * kHeadDim) + h * kHeadDim + j]) : 0.0f;
-    __syncthreads();
-    float Mh = kNegInf;
-    for (int i = 0; i < nch; ++i) Mh = fmaxf(Mh, s_ml[i][h]);
-    float lsum = 0.0f, acc = 0.0f;
+    const __amdgpu_buffer_rsrc_t acc_res = make_rsrc(ws_acc + it0 * (2 * kHeadDim), nch * (2 * kHeadDim) * 4);
+    const __amdgpu_buffer_rsrc_t ml_res = make_rsrc(ws_ml + it0 * 4, nch * 16);
+    constexpr int kBatch = 16;
+    float Mh = kNegInf, lsum = 0.0f, acc = 0.0f;
     for (int i0 = 0; i0 < nch; i0 += kBatch) {
-        if (i0 > 0) {
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u)
-                x[u] = i0 + u < nch
-                           ? load_dev(&ws_acc[(it0 + i0 + u) * (2 * kHeadDim) + h * kHeadDim + j])
-                           : 0.0f;
+        const int nb = min(kBatch, nch - i0);
+        if (i0 > 0) __syncthreads();  // s_ml of the previous batch is consumed
+        if (tid < nb) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(ml_res, (i0 + tid) * 16, 0, kSc1);
+            *(u32x4*)&s_ml[tid][0] = v;
         }
+        float x[kBatch];
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
-            if (i0 + u < nch) {
-                const float mi = s_ml[i0 + u][h];
-                const float w = mi == kNegInf ? 0.0f : fast_exp2(mi - Mh);
-                lsum = fmaf(s_ml[i0 + u][2 + h], w, lsum);
-                acc = fmaf(x[u], w, acc);
+            const int i = i0 + (u < nb ? u : 0);
+            x[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                  acc_res, (i * (2 * kHeadDim) + h * kHeadDim + j) * 4, 0, kSc1));
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            if (u < nb) {
+                const float mi = s_ml[u][h];
+                if (mi != kNegInf) {
+                    const float mn = fmaxf(Mh, mi);
+                    const float fo = Mh == kNegInf ? 0.0f : fast_exp2(Mh - mn);
+                    const float fi = fast_exp2(mi - mn);
+                    lsum = fmaf(s_ml[u][2 + h], fi, lsum * fo);
+                    acc = fmaf(x[u], fi, acc * fo);
+                    Mh = mn;
+                }
             }
         }
     }
