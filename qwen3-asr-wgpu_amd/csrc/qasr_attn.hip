@@ -106,6 +106,7 @@ struct qasr_ctx {
     f16* sin = nullptr;
     int rope_rows = 0;
     float scale_log2;
+    int cus = 256;  // compute units of the device (decode plans two workgroups per CU)
 };
 
 struct qasr_kv {
@@ -205,20 +206,54 @@ int ensure_prefill_ws(qasr_kv* kv, int64_t items) {
 // partial to publish and merge, more than streaming a few hundred extra keys
 // in one workgroup.  (Measured on MI355X against a plan that minimises the
 // largest chunk: no better on the ragged 16-slot batch, worse for one slot.)
-void plan_decode_chunks(qasr::DecodePlan& P, int nkvh) {
-    const int target = std::max(1, std::min(env_int("QASR_DECODE_WGS", qasr::kDecodeTargetWgs), 4096));
+// Decode launch plan: a fixed number of workgroups (QASR_DECODE_WGS, default
+// two per CU: every CU then carries the same number of workgroups), whose
+// chunks are as even as possible.  Entry b is cut into n_b equal chunks of
+// whole 32-key passes; starting from one chunk per entry, the entry with the
+// largest chunk gets one more until the workgroup budget is used (and the
+// largest chunk is within 1.5x of the average) or every chunk is down to
+// QASR_DECODE_MIN_CHUNK keys or every entry has QASR_DECODE_MAX_SPLIT chunks
+// (the merge reads one partial per chunk).
+int chunk_of(int L, int n) {
+    const int c = (L + n - 1) / n;
+    return (c + qasr::kDecodeTileKeys - 1) / qasr::kDecodeTileKeys * qasr::kDecodeTileKeys;
+}
+
+void plan_decode_chunks(qasr::DecodePlan& P, int nkvh, int cus) {
+    const int target = std::max(1, std::min(env_int("QASR_DECODE_WGS", 2 * cus), 4096));
     const int min_chunk = std::max(32, env_int("QASR_DECODE_MIN_CHUNK", qasr::kDecodeMinChunk));
-    int64_t total = 0;
-    for (int i = 0; i < P.batch; ++i) total += P.len[i];
-    const int64_t t = std::max<int64_t>(min_chunk, (total * nkvh + target - 1) / target);
+    const int max_split = std::max(1, std::min(env_int("QASR_DECODE_MAX_SPLIT", qasr::kDecodeMaxSplit),
+                                               qasr::kDecodeMaxChunksPerEntry));
+    int n[qasr::kMaxBatch];
+    int wgs = 0;
+    for (int i = 0; i < P.batch; ++i) {
+        n[i] = 1;
+        wgs += nkvh;
+    }
+    int64_t keys = 0;
+    for (int i = 0; i < P.batch; ++i) keys += (int64_t)nkvh * P.len[i];
+    // Past the budget (batches with more entries x kv heads than it), chunks
+    // more than 1.5x the average keys per workgroup are still split: the
+    // extra workgroups run as the first ones finish.
+    while (wgs + nkvh <= qasr::kDecodeMaxItems / 2) {
+        int best = -1, best_chunk = 0;
+        for (int i = 0; i < P.batch; ++i) {
+            const int c = chunk_of(P.len[i], n[i]);
+            if (n[i] < max_split && chunk_of(P.len[i], n[i] + 1) >= min_chunk &&
+                c > best_chunk) {
+                best = i;
+                best_chunk = c;
+            }
+        }
+        if (best < 0) break;
+        if (wgs + nkvh > target && 2 * (int64_t)best_chunk * wgs <= 3 * keys) break;
+        ++n[best];
+        wgs += nkvh;
+    }
     P.wg_base[0] = 0;
     for (int i = 0; i < P.batch; ++i) {
         const int L = P.len[i];
-        int64_t n = std::max<int64_t>(1, (L + t / 2) / t);
-        n = std::min<int64_t>(n, qasr::kDecodeMaxChunksPerEntry);
-        int chunk = (int)((L + n - 1) / n);
-        chunk = std::max(min_chunk, (chunk + qasr::kDecodeTileKeys - 1) / qasr::kDecodeTileKeys *
-                                        qasr::kDecodeTileKeys);
+        const int chunk = chunk_of(L, n[i]);
         P.chunk[i] = chunk;
         P.wg_base[i + 1] = P.wg_base[i] + nkvh * ((L + chunk - 1) / chunk);
     }
@@ -253,7 +288,7 @@ int run_decode(bool fused, qasr_ctx* ctx, qasr_kv* kv, int layer, int batch, con
             P.slot[i] = slots ? slots[b0 + i] : b0 + i;
             P.len[i] = lens[b0 + i];
         }
-        plan_decode_chunks(P, nkvh);
+        plan_decode_chunks(P, nkvh, ctx->cus);
         const f16* qp = (const f16*)qin + b0 * in_row;
         f16* op = (f16*)out + b0 * out_row;
         const int waves = env_int("QASR_DECODE_WAVES", qasr::kDecodeWaves);
@@ -294,9 +329,13 @@ int qasr_ctx_create(const qasr_attn_cfg* cfg, int device, qasr_ctx** out) {
     HIP_TRY(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
     if (device < 0 || device >= ndev)
         return fail(QASR_EINVAL, "device %d outside [0, %d)", device, ndev);
+    int cus = 0;
+    HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
+            "hipDeviceGetAttribute");
     qasr_ctx* ctx = new qasr_ctx();
     ctx->cfg = c;
     ctx->device = device;
+    ctx->cus = std::max(1, cus);
     // scale = 1/sqrt(hd) in f32 (decoder.rs:204-206), folded with log2(e) so the
     // kernels exponentiate with exp2.
     const float scale = 1.0f / std::sqrt((float)c.head_dim);
