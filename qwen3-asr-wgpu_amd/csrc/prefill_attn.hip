@@ -238,14 +238,16 @@ __device__ __forceinline__ void step_pv(Wave& w, const f16* vt, const half8v (&p
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
 }
 
-// Merge of the nsp split-K partials of one wave's 32 rows (lane = query row):
-// returns the merged row sum and leaves the merged, unnormalised output in o.
-// The partials are combined in index order whichever workgroup arrives last,
-// so the result is bitwise reproducible.  Pass 1: the row max M (16 m values
-// requested per memory round trip).  Pass 2: partials in groups of G, their
-// (m, l) and, per 8-element chunk, the G x 8 accumulator values requested
-// together.  Unused slots of a group read partial 0's record and drop it.
-template <int G>
+// Merge of the nsp split-K partials of one wave's 32 rows (lane = query row),
+// for the accumulator elements of dim blocks 2*HALF and 2*HALF+1 (element
+// chunks 4*HALF .. 4*HALF+3 of 8): returns the merged row sum and leaves the
+// merged, unnormalised output in those two blocks of o.  The partials are
+// combined in index order whichever workgroup arrives last, so the result is
+// bitwise reproducible.  Pass 1: the row max M (16 m values requested per
+// memory round trip).  Pass 2: partials in groups of G, their (m, l) and, per
+// 8-element chunk, the G x 8 accumulator values requested together.  Unused
+// slots of a group read partial 0's record and drop it.
+template <int G, int HALF>
 __device__ __forceinline__ float merge_partials(const float* mlw, const float* ow, int nsp,
                                                 float16v (&o)[4]) {
     float M = kNegInf;
@@ -261,8 +263,11 @@ __device__ __forceinline__ float merge_partials(const float* mlw, const float* o
         for (int u = 0; u < 16; ++u) M = fmaxf(M, mm[u]);
     }
     float Ls = 0.0f;
+    float acc[4][8];
 #pragma unroll
-    for (int db = 0; db < 4; ++db) o[db] = (float16v){};
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[c][e] = 0.0f;
     for (int i0 = 0; i0 < nsp; i0 += G) {
         float w[G];
 #pragma unroll
@@ -274,12 +279,13 @@ __device__ __forceinline__ float merge_partials(const float* mlw, const float* o
             Ls = fmaf(i < nsp ? li : 0.0f, w[u], Ls);
         }
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {  // element chunk c: o[c/2][8*(c%2) .. +8]
+        for (int c = 0; c < 4; ++c) {  // element chunk 4*half + c
             float x[G][8];
 #pragma unroll
             for (int u = 0; u < G; ++u) {
                 const int i = i0 + u;
-                const float* src = ow + (int64_t)(i < nsp ? i : 0) * kPrefillItemFloats + c * 8 * 64;
+                const float* src =
+                    ow + (int64_t)(i < nsp ? i : 0) * kPrefillItemFloats + (4 * HALF + c) * 8 * 64;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const float v = load_dev(src + e * 64);
@@ -289,12 +295,122 @@ __device__ __forceinline__ float merge_partials(const float* mlw, const float* o
 #pragma unroll
             for (int u = 0; u < G; ++u)
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    o[c >> 1][8 * (c & 1) + e] = fmaf(x[u][e], w[u], o[c >> 1][8 * (c & 1) + e]);
+                for (int e = 0; e < 8; ++e) acc[c][e] = fmaf(x[u][e], w[u], acc[c][e]);
             __builtin_amdgcn_sched_barrier(0);  // keep the next chunk's loads after this one
         }
     }
+    // Element chunk 4*HALF + c is o[2*HALF + c/2][8*(c%2) .. +8].
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[2 * HALF + (c >> 1)][8 * (c & 1) + e] = acc[c][e];
     return Ls;
+}
+
+// Kernel state the epilogue needs.
+struct EpiArgs {
+    const PrefillArgs& a;
+    const PrefillPlan& P;
+    float* ws_o;
+    float* ws_ml;
+    uint32_t* counters;
+    f16* K0;
+    f16* K1;
+    f16* V0;
+    f16* V1;
+    int item, kvh, rb, nsp, rw, r, head;
+    bool row_ok;
+    int g, lane, tid;
+};
+
+// Epilogue of the wave of key group KG: wave (rw, KG) keeps dim blocks 2*KG
+// and 2*KG+1 of the output and hands the other two blocks, with its (m, l),
+// to its twin through LDS (element-major records: every access is 256
+// contiguous bytes).  Then it writes, publishes and merges only its blocks.
+template <int KG>
+__device__ __forceinline__ void epilogue(Wave& w, const EpiArgs& e) {
+    constexpr int kMine = 2 * KG, kTheirs = 2 * (KG ^ 1);
+    const int lane = e.lane, rw = e.rw;
+    float* xbase = reinterpret_cast<float*>(rw < 2 ? e.K0 : e.K1) + (rw & 1) * 2 * (32 * 64);
+    float* xo_out = xbase + KG * (32 * 64);
+    float* xo_in = xbase + (KG ^ 1) * (32 * 64);
+    float* xml_out = reinterpret_cast<float*>(e.V1) + (rw * 2 + KG) * 128;
+    float* xml_in = reinterpret_cast<float*>(e.V1) + (rw * 2 + (KG ^ 1)) * 128;
+    int& s_last = *reinterpret_cast<int*>(e.V0);
+    static_assert(2 * 2 * 32 * 64 * 4 <= kTileHalves * 2, "two row waves' halves per K buffer");
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xo_out[(d * 16 + i) * 64 + lane] = w.o[kTheirs + d][i];
+    xml_out[lane] = w.m;
+    xml_out[64 + lane] = w.l;
+    __syncthreads();
+    {
+        const float m1 = xml_in[lane], l1 = xml_in[64 + lane];
+        const float M = fmaxf(w.m, m1);
+        const float a0 = w.m == kNegInf ? 0.0f : fast_exp2(w.m - M);
+        const float a1 = m1 == kNegInf ? 0.0f : fast_exp2(m1 - M);
+#pragma unroll
+        for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                w.o[kMine + d][i] = w.o[kMine + d][i] * a0 + xo_in[(d * 16 + i) * 64 + lane] * a1;
+        w.l = w.l * a0 + l1 * a1;
+        w.m = M;
+    }
+    float16v (&o)[4] = w.o;
+
+    // o[db][i] holds dim db*32 + 8*(i/4) + 4*g + i%4 of query row r.
+    f16* orow = e.a.out + (int64_t)e.r * (e.a.nqh * kHeadDim) + e.head * kHeadDim;
+    auto write_out = [&](float l) {
+        if (!e.row_ok) return;
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                half4v h4;
+#pragma unroll
+                for (int x = 0; x < 4; ++x) h4[x] = (f16)(o[kMine + d][q4 * 4 + x] * inv);
+                *(half4v*)(orow + (kMine + d) * 32 + 8 * q4 + 4 * e.g) = h4;
+            }
+    };
+    if (e.nsp == 1) {
+        write_out(w.l);
+        return;
+    }
+
+    // Partial of this row wave: 64 accumulator elements x 64 lanes,
+    // element-major (element x of lane l at [x][l]), each wave of the pair
+    // storing its 32; then (m, l) per lane.  Published with device-scope
+    // stores (see stores_done_barrier).
+    {
+        float* po = e.ws_o + (int64_t)e.item * kPrefillItemFloats + rw * kPrefillWaveFloats;
+#pragma unroll
+        for (int d = 0; d < 2; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) store_dev(po + ((kMine + d) * 16 + i) * 64 + lane, o[kMine + d][i]);
+        if (KG == 0) {
+            float* pml = e.ws_ml + (int64_t)e.item * kPrefillItemMl + rw * kPrefillWaveMl;
+            store_dev(pml + lane, w.m);
+            store_dev(pml + 64 + lane, w.l);
+        }
+    }
+    stores_done_barrier();
+    uint32_t* ctr = &e.counters[e.kvh * e.P.nrb + e.rb];
+    if (e.tid == 0) s_last = (ticket_add(ctr) == (uint32_t)(e.nsp - 1));
+    __syncthreads();
+    if (!s_last) return;
+
+    // Last arrival: merge the nsp partials of this (kv head, row block); each
+    // wave merges its half of its row wave's 32 rows.
+    const int it0 = e.kvh * e.P.items_per_kvh + e.P.sp_base[e.rb];
+    const float* mlw = e.ws_ml + (int64_t)it0 * kPrefillItemMl + rw * kPrefillWaveMl + lane;
+    const float* ow = e.ws_o + (int64_t)it0 * kPrefillItemFloats + rw * kPrefillWaveFloats + lane;
+    const float Ls = e.nsp <= 2 ? merge_partials<2, KG>(mlw, ow, e.nsp, o)
+                                : merge_partials<8, KG>(mlw, ow, e.nsp, o);
+    write_out(Ls);
+    if (e.tid == 0) ticket_reset(ctr);
 }
 
 __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
@@ -412,101 +528,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
         if (++t >= t_end) break;
     }
 
-    // Key group 1 hands its (m, l, O) to key group 0 through LDS (the tile
-    // buffers are free now), element-major so every access is 256 contiguous
-    // bytes.
-    float* xo = reinterpret_cast<float*>(rw < 2 ? K0 : K1) + (rw & 1) * (64 * 64);
-    float* xml = reinterpret_cast<float*>(V1) + rw * 128;
-    int& s_last = *reinterpret_cast<int*>(V0);
-    static_assert(2 * 64 * 64 * 4 <= kTileHalves * 2, "two row waves' O per K buffer");
-    if (kg == 1) {
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) xo[(db * 16 + i) * 64 + lane] = w.o[db][i];
-        xml[lane] = w.m;
-        xml[64 + lane] = w.l;
-    }
-    __syncthreads();
-    if (kg == 0) {
-        const float m1 = xml[lane], l1 = xml[64 + lane];
-        const float M = fmaxf(w.m, m1);
-        const float a0 = w.m == kNegInf ? 0.0f : fast_exp2(w.m - M);
-        const float a1 = m1 == kNegInf ? 0.0f : fast_exp2(m1 - M);
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-                w.o[db][i] = w.o[db][i] * a0 + xo[(db * 16 + i) * 64 + lane] * a1;
-        w.l = w.l * a0 + l1 * a1;
-        w.m = M;
-    }
-    float16v (&o)[4] = w.o;
-    const float m = w.m, lsum = w.l;
-
-    // o[db][i] holds dim db*32 + 8*(i/4) + 4*g + i%4 of query row r.
-    f16* orow = a.out + (int64_t)r * ldq + head * kHeadDim;
-    const bool owner = kg == 0;  // key group 0 holds the merged result
-    if (nsp == 1) {
-        if (owner && row_ok) {
-            const float inv = 1.0f / lsum;
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-#pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4) {
-                    half4v h4;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) h4[e] = (f16)(o[db][q4 * 4 + e] * inv);
-                    *(half4v*)(orow + db * 32 + 8 * q4 + 4 * g) = h4;
-                }
-            }
-        }
-        return;
-    }
-
-    // Partial of this wave: 64 accumulator elements x 64 lanes, element-major
-    // (element e of lane l at [e][l]) so every store and load instruction
-    // moves 256 contiguous bytes; then (m, l) per lane.  Published with
-    // device-scope stores (see stores_done_barrier).
-    if (owner) {
-        float* po = ws_o + (int64_t)item * kPrefillItemFloats + rw * kPrefillWaveFloats;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) store_dev(po + (db * 16 + i) * 64 + lane, o[db][i]);
-        float* pml = ws_ml + (int64_t)item * kPrefillItemMl + rw * kPrefillWaveMl;
-        store_dev(pml + lane, m);
-        store_dev(pml + 64 + lane, lsum);
-    }
-    stores_done_barrier();
-    uint32_t* ctr = &counters[kvh * P.nrb + rb];
-    if (tid == 0) s_last = (ticket_add(ctr) == (uint32_t)(nsp - 1));
-    __syncthreads();
-    if (!s_last || !owner) return;
-
-    // Last arrival: merge the nsp partials of this (kv head, row block); each
-    // row wave merges its own 32 rows.
-    const int it0 = kvh * P.items_per_kvh + P.sp_base[rb];
-    const float* mlw = ws_ml + (int64_t)it0 * kPrefillItemMl + rw * kPrefillWaveMl + lane;
-    const float* ow = ws_o + (int64_t)it0 * kPrefillItemFloats + rw * kPrefillWaveFloats + lane;
-    float Ls;
-    if (nsp <= 2)
-        Ls = merge_partials<2>(mlw, ow, nsp, o);
+    // The two key groups of a row wave combine through LDS (the tile buffers
+    // are free now); from here on both waves of a pair share the epilogue
+    // work half and half.
+    EpiArgs e{a, P, ws_o, ws_ml, counters, K0, K1, V0, V1, item, kvh, rb, nsp, rw, r, head, row_ok, g, lane, tid};
+    if (kg == 0)
+        epilogue<0>(w, e);
     else
-        Ls = merge_partials<8>(mlw, ow, nsp, o);
-    if (row_ok) {
-        const float inv = 1.0f / Ls;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                half4v h4;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) h4[e] = (f16)(o[db][q4 * 4 + e] * inv);
-                *(half4v*)(orow + db * 32 + 8 * q4 + 4 * g) = h4;
-            }
-    }
-    if (tid == 0) ticket_reset(ctr);  // tid 0 is in key group 0
+        epilogue<1>(w, e);
 }
 
 }  // namespace
