@@ -46,7 +46,6 @@ constexpr int kDecodeWaves = 4;       // default workgroup size (waves)
 constexpr int kDecodeWavesPerEU = 2;  // occupancy target: <= 256 VGPRs (two pass buffers)
 constexpr int kDecodeTileKeys = 32;   // keys per wave pass
 constexpr int kDecodeMaxChunksPerEntry = 256;
-constexpr int kDecodeTargetWgs = 512;   // 2 resident 4-wave workgroups on each of 256 CUs
 constexpr int kDecodeMinChunk = 256;   // keys
 constexpr int kDecodeMaxSplit = 16;    // chunks per entry by default (one merge batch)
 constexpr int kDecodeMaxItems = 8192;   // >= 4096 target + kMaxBatch * nkvh rounding slack
