@@ -1,0 +1,49 @@
+"""Writes reference_known_answers.json: the known answers the reference's own
+unit tests hold for this path, transcribed as data (no reference code runs).
+
+Sources (paths relative to the reference checkout):
+  src/mrope.rs:86-107   build_dim_map / compute_mrope_cos_sin tests
+  src/config.rs:102-110 text-decoder defaults (vocab, heads, head_dim, eps, theta)
+  src/config.rs:177-195 mrope_section default [24, 20, 20], interleaved default true
+  src/config.rs:261-290 HF-native config layout test (text_config values)
+
+The reference ships no numeric vectors for attention itself (its numeric gate
+is transcript identity on audio fixtures kept outside the repository), so
+these are the only reference-held answers on this path.
+
+Usage: python tests/golden/make_reference_known_answers.py
+"""
+import json
+import os
+
+KNOWN = {
+    "build_dim_map": [
+        {"source": "src/mrope.rs:87-94", "section": [24, 20, 20], "half": 64, "interleaved": True,
+         "len": 64, "counts": {"0": 24, "1": 20, "2": 20}, "prefix": [0, 1, 2, 0, 1, 2]},
+        {"source": "src/mrope.rs:96-100", "section": [2, 1], "half": 4, "interleaved": False,
+         "map": [0, 0, 1, 1]},
+    ],
+    "compute_mrope_cos_sin": [
+        {"source": "src/mrope.rs:102-106", "text_positions": 3, "head_dim": 8, "theta": 1e6,
+         "section": [2, 1, 1], "interleaved": True, "cos_len": 24, "halves_equal": [[0, 4], [4, 8]]},
+    ],
+    "text_decoder_defaults": {
+        "source": "src/config.rs:102-110, 177-195",
+        "vocab_size": 151936, "hidden_size": 1024, "intermediate_size": 3072,
+        "num_hidden_layers": 28, "num_attention_heads": 16, "num_key_value_heads": 8,
+        "head_dim": 128, "rms_norm_eps": 1e-6, "rope_theta": 1e6,
+        "mrope_section": [24, 20, 20], "mrope_interleaved": True,
+    },
+    "hf_native_text_config": {
+        "source": "src/config.rs:261-290",
+        "num_attention_heads": 16, "num_key_value_heads": 8, "head_dim": 128,
+        "rms_norm_eps": 1e-6, "rope_theta": 1000000, "num_hidden_layers": 28, "hidden_size": 1024,
+    },
+}
+
+if __name__ == "__main__":
+    out = os.path.join(os.path.dirname(os.path.abspath(__file__)), "reference_known_answers.json")
+    with open(out, "w") as f:
+        json.dump(KNOWN, f, indent=1)
+        f.write("\n")
+    print(f"wrote {out}")
