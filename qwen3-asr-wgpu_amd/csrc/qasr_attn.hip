@@ -197,15 +197,6 @@ int ensure_prefill_ws(qasr_kv* kv, int64_t items) {
     return QASR_OK;
 }
 
-// Decode launch plan: every workgroup should stream about the same number of
-// keys whatever the ragged lengths, and one launch should be about one round
-// of resident workgroups (two 4-wave workgroups on each of 256 CUs).  Entry b
-// is cut into n_b = round(len_b / t) chunks with t = max(min_chunk, total keys
-// / target workgroups), each chunk rounded up to whole 32-key wave passes.
-// min_chunk (384 keys) keeps short entries whole: a split costs one more
-// partial to publish and merge, more than streaming a few hundred extra keys
-// in one workgroup.  (Measured on MI355X against a plan that minimises the
-// largest chunk: no better on the ragged 16-slot batch, worse for one slot.)
 // Decode launch plan: a fixed number of workgroups (QASR_DECODE_WGS, default
 // two per CU: every CU then carries the same number of workgroups), whose
 // chunks are as even as possible.  Entry b is cut into n_b equal chunks of
