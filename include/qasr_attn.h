@@ -170,6 +170,68 @@ int qasr_prefill_layer(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_s
                        const void* qkv_dev, const void* q_gain_dev, const void* k_gain_dev,
                        void* q_work_dev, void* out_dev, void* stream);
 
+/* ---- Whole text decoder around the attention path ------------------------
+ * The layer sequence of src/cpu_decoder.rs:367-532 (CpuTextDecoder::forward,
+ * final_norm_logits, argmax, prefill, step), i.e. what WgpuTextDecoder::step
+ * and ::prefill run on the GPU (decoder.rs:1768-1925, 4489-5244): input
+ * RMSNorm, fused q/k/v projection, stages (a)+(b) or (a)+(c) of this library,
+ * o_proj + residual, post-attention RMSNorm, gate/up projection, SiLU(gate)*up,
+ * down_proj + residual; final RMSNorm, logits against the tied embedding and
+ * the greedy argmax.  Rounding follows the reference: f32 math, one f16
+ * rounding per op output (a residual add rounds x + dot once), f32 logits,
+ * the first maximal index on ties.  The projections are rocBLAS f16 GEMMs
+ * with f32 accumulation; their summation order differs from the reference's,
+ * so logits agree to rounding, not bitwise.
+ *
+ * Weights are device pointers owned by the caller and must outlive the
+ * decoder; f16 bits, row-major [out][in] as in the checkpoint. */
+typedef struct qasr_layer_weights {
+    const void* input_norm;   /* [hs] (input_layernorm) */
+    const void* qkv_proj;     /* [(nqh + 2*nkvh)*hd][hs]: q_proj rows, then k_proj, then v_proj */
+    const void* q_norm;       /* [hd] */
+    const void* k_norm;       /* [hd] */
+    const void* o_proj;       /* [hs][nqh*hd] */
+    const void* post_norm;    /* [hs] (post_attention_layernorm) */
+    const void* gate_up_proj; /* [2*inter][hs]: gate_proj rows, then up_proj */
+    const void* down_proj;    /* [hs][inter] */
+} qasr_layer_weights;
+
+typedef struct qasr_decoder_cfg {
+    int32_t hidden_size;       /* 1024 (0.6B) or 2048 (1.7B) */
+    int32_t intermediate_size; /* 3072 or 6144 */
+    int32_t vocab_size;        /* 151936 */
+    int32_t max_rows;          /* largest decode batch or prefill chunk one call runs */
+} qasr_decoder_cfg;
+
+typedef struct qasr_decoder qasr_decoder;
+
+/* embed_dev: [vocab][hs] (embed_tokens, also the tied lm_head);
+ * final_norm_dev: [hs]; layers: num_hidden_layers entries (a host array, read
+ * during the call).  Allocates the activation workspace for max_rows rows. */
+int qasr_decoder_create(qasr_ctx* ctx, const qasr_decoder_cfg* cfg, const void* embed_dev,
+                        const void* final_norm_dev, const qasr_layer_weights* layers,
+                        qasr_decoder** out);
+void qasr_decoder_destroy(qasr_decoder* dec);
+
+/* One greedy step for `batch` slots (the reference's step(), and --batch N
+ * through BatchProjections::step, decoder.rs:3348-3451): embeds
+ * tokens_dev[b] (int32, device; ids outside [0, vocab) read row 0), runs every
+ * layer at position pos[b] of slots[b] (host arrays; slots NULL = 0..batch-1)
+ * and writes the argmax token of each entry to next_dev[b] (int32, device).
+ * logits_dev, if not NULL, receives the f32 logits [batch][vocab]. */
+int qasr_decoder_step(qasr_decoder* dec, qasr_kv* kv, int batch, const int32_t* slots,
+                      const int32_t* pos, const int32_t* tokens_dev, int32_t* next_dev,
+                      float* logits_dev, void* stream);
+
+/* Prefill of s hidden rows ([s][hs] f16, device; the reference's
+ * prefill(hidden_words, s, kv_start)) into `slot` at positions kv_start ..
+ * kv_start+s-1 through every layer; next_dev[0] receives the argmax token of
+ * the last row, logits_dev (optional) its f32 logits [vocab].  s <= max_rows;
+ * longer prompts are prefilled in chunks (kv_start > 0). */
+int qasr_decoder_prefill(qasr_decoder* dec, qasr_kv* kv, int slot, int kv_start, int s,
+                         const void* hidden_dev, int32_t* next_dev, float* logits_dev,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

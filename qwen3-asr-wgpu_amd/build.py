@@ -26,6 +26,7 @@ OUT = os.path.join(HERE, "libqasr_attn.so")
 OBJ = os.path.join(HERE, "_build")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+ROCM_LIB = "/opt/rocm/lib"
 ARCH = "gfx950"
 FLAGS = [
     f"--offload-arch={ARCH}",
@@ -64,7 +65,9 @@ def build(verbose: bool = False) -> str:
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = OUT + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    # rocBLAS serves the text decoder's projection GEMMs (decoder.hip).
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
+           f"-L{ROCM_LIB}", "-lrocblas", f"-Wl,-rpath,{ROCM_LIB}"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")

@@ -1,0 +1,459 @@
+// decoder.hip -- the whole Qwen3 text decoder around the attention path: the
+// C ABI's qasr_decoder_* (include/qasr_attn.h).
+//
+// Layer sequence and rounding points of the reference's CpuTextDecoder
+// (src/cpu_decoder.rs:367-532), which WgpuTextDecoder::step / ::prefill run
+// on the GPU (src/decoder.rs:1768-1925, 4489-5244):
+//   n  = f16(rms_norm(x) * input_norm)                    cpu_decoder.rs:261-271, 386-389
+//   qkv = f16(n . W_qkv^T)                                 398-400
+//   stage (a) + (b) [decode] or (a) + (c) [prefill]       this library
+//   x  = f16(x + attn . W_o^T)                             431 (batch_dot_acc, 45-62)
+//   n2 = f16(rms_norm(x) * post_norm)                      435-438
+//   g|u = f16(n2 . W_gate_up^T)                            440-441
+//   h  = f16(g / (1 + exp(-g)) * u)                        442-448
+//   x  = f16(x + h . W_down^T)                             449
+// then logits = f32(rms_norm(x_last) * norm . E^T) against the tied embedding
+// and the first maximal index (458-485).
+//
+// The projections are plain GEMMs and go to rocBLAS (f16 operands, f32
+// accumulation, one f16 rounding of the f32 result; a residual add is the
+// GEMM's beta = 1 term, so x + dot is rounded once as in batch_dot_acc).  The
+// elementwise steps are small HIP kernels below.  Nothing here allocates per
+// call: the activation workspace is sized for max_rows at creation, and
+// rocBLAS gets a fixed workspace so that a step can be captured in a graph.
+
+#include <rocblas/rocblas.h>
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "abi_internal.hpp"
+#include "common.hpp"
+
+using qasr::f16;
+using qasr::H8;
+using qasr_abi::DeviceScope;
+using qasr_abi::fail;
+using qasr_abi::hip_fail;
+
+namespace {
+
+constexpr int kNormThreads = 256;
+constexpr int kArgmaxThreads = 256;
+constexpr int kArgmaxChunks = 32;  // workgroups per logits row in the first argmax pass
+constexpr int kHeadRows = 128;     // rows per logits GEMM + argmax (bounds the logits scratch)
+constexpr size_t kBlasWorkspace = size_t(64) << 20;
+
+// ---- block reductions (wave64 shuffles, then one LDS pass) ---------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// (value, index) pair order for the argmax: larger value, then smaller index
+// (the reference keeps the first maximal index: `if v > logits[best]`).
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = __shfl_xor(v, m);
+        const int oi = __shfl_xor(i, m);
+        if (better(ov, oi, v, i)) {
+            v = ov;
+            i = oi;
+        }
+    }
+}
+
+// ---- kernels -------------------------------------------------------------
+
+// Embedding rows of the batch's tokens (embed_row, cpu_decoder.rs:255-258).
+// An id outside [0, vocab) reads row 0 (the caller's contract says in range).
+__global__ __launch_bounds__(256) void embed_rows_kernel(const f16* __restrict__ embed,
+                                                         const int32_t* __restrict__ tokens,
+                                                         int vocab, int hs, f16* __restrict__ x) {
+    const int r = blockIdx.x;
+    int t = tokens[r];
+    if (t < 0 || t >= vocab) t = 0;
+    const uint4* src = (const uint4*)(embed + (int64_t)t * hs);
+    uint4* dst = (uint4*)(x + (int64_t)r * hs);
+    for (int c = threadIdx.x; c < hs / 8; c += blockDim.x) dst[c] = src[c];
+}
+
+// out[r] = f16((x * inv) * w) with inv = 1 / sqrt(sum(x^2) / n + eps), f32
+// (rms_norm_row, cpu_decoder.rs:261-271).  One workgroup per row; the sum of
+// squares is a tree sum (the reference sums in index order, so inv can
+// differ from it in the last bit).
+__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const f16* __restrict__ x,
+                                                                int64_t x_stride,
+                                                                const f16* __restrict__ w,
+                                                                f16* __restrict__ out, int n,
+                                                                float eps) {
+    __shared__ float s_part[kNormThreads / 64];
+    const f16* xr = x + (int64_t)blockIdx.x * x_stride;
+    f16* orow = out + (int64_t)blockIdx.x * n;
+    float s = 0.0f;
+    for (int c = threadIdx.x; c < n / 8; c += kNormThreads) {
+        H8 v;
+        v.u = ((const uint4*)xr)[c];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float f = (float)v.e[e];
+            s = fmaf(f, f, s);
+        }
+    }
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormThreads / 64; ++i) tot += s_part[i];
+    const float inv = 1.0f / sqrtf(tot / (float)n + eps);
+    for (int c = threadIdx.x; c < n / 8; c += kNormThreads) {
+        H8 v, g, o;
+        v.u = ((const uint4*)xr)[c];
+        g.u = ((const uint4*)w)[c];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o.e[e] = (f16)(((float)v.e[e] * inv) * (float)g.e[e]);
+        ((uint4*)orow)[c] = o.u;
+    }
+}
+
+// h[r][i] = f16(g / (1 + exp(-g)) * u), g|u = gu[r][i], gu[r][inter + i]
+// (cpu_decoder.rs:442-448).  8 elements per thread.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const f16* __restrict__ gu, int inter,
+                                                       int rows, f16* __restrict__ h) {
+    const int per_row = inter / 8;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)rows * per_row) return;
+    const int r = (int)(idx / per_row), c = (int)(idx - (int64_t)r * per_row);
+    const f16* grow = gu + (int64_t)r * 2 * inter;
+    H8 g, u, o;
+    g.u = ((const uint4*)grow)[c];
+    u.u = ((const uint4*)(grow + inter))[c];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float gf = (float)g.e[e];
+        const float silu = gf / (1.0f + expf(-gf));
+        o.e[e] = (f16)(silu * (float)u.e[e]);
+    }
+    ((uint4*)(h + (int64_t)r * inter))[c] = o.u;
+}
+
+// First argmax pass: workgroup (chunk, row) finds the best (value, index) of
+// its contiguous chunk of the row.
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(
+    const float* __restrict__ logits, int vocab, float* __restrict__ pv, int* __restrict__ pi) {
+    __shared__ float s_v[kArgmaxThreads / 64];
+    __shared__ int s_i[kArgmaxThreads / 64];
+    const int row = blockIdx.y, chunk = blockIdx.x;
+    const int per = (vocab + kArgmaxChunks - 1) / kArgmaxChunks;
+    const int lo = chunk * per, hi = min(vocab, lo + per);
+    const float* lr = logits + (int64_t)row * vocab;
+    float bv = -__builtin_inff();
+    int bi = vocab;  // no candidate yet
+    for (int i = lo + threadIdx.x; i < hi; i += kArgmaxThreads) {
+        const float v = lr[i];
+        if (better(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+    wave_argmax(bv, bi);
+    if ((threadIdx.x & 63) == 0) {
+        s_v[threadIdx.x >> 6] = bv;
+        s_i[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kArgmaxThreads / 64; ++w)
+            if (better(s_v[w], s_i[w], bv, bi)) {
+                bv = s_v[w];
+                bi = s_i[w];
+            }
+        pv[row * kArgmaxChunks + chunk] = bv;
+        pi[row * kArgmaxChunks + chunk] = bi;
+    }
+}
+
+// Second pass: one wave per row over the chunks' candidates.  A row whose
+// values are all NaN (no candidate) yields 0, as the reference's loop does.
+__global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restrict__ pv,
+                                                          const int* __restrict__ pi, int vocab,
+                                                          int32_t* __restrict__ out) {
+    const int row = blockIdx.x, lane = threadIdx.x;
+    float bv = -__builtin_inff();
+    int bi = vocab;
+    if (lane < kArgmaxChunks) {
+        bv = pv[row * kArgmaxChunks + lane];
+        bi = pi[row * kArgmaxChunks + lane];
+    }
+    wave_argmax(bv, bi);
+    if (lane == 0) out[row] = bi < vocab ? bi : 0;
+}
+
+const char* blas_msg(rocblas_status st) { return rocblas_status_to_string(st); }
+
+}  // namespace
+
+struct qasr_decoder {
+    qasr_ctx* ctx = nullptr;
+    qasr_decoder_cfg cfg{};
+    const f16* embed = nullptr;
+    const f16* final_norm = nullptr;
+    std::vector<qasr_layer_weights> layers;
+    rocblas_handle blas = nullptr;
+    void* blas_ws = nullptr;
+    // activations, max_rows rows each
+    f16* x = nullptr;     // residual stream [rows][hs]
+    f16* n = nullptr;     // normed rows [rows][hs]
+    f16* qkv = nullptr;   // [rows][(nqh + 2 nkvh) hd]
+    f16* qw = nullptr;    // roped q of a prefill [rows][nqh hd]
+    f16* attn = nullptr;  // [rows][nqh hd]
+    f16* gu = nullptr;    // [rows][2 inter]
+    f16* h = nullptr;     // [rows][inter]
+    float* logits = nullptr;  // [kHeadRows][vocab]
+    float* am_v = nullptr;    // argmax candidates [kHeadRows][kArgmaxChunks]
+    int* am_i = nullptr;
+};
+
+namespace {
+
+void free_decoder(qasr_decoder* d) {
+    if (d->blas) (void)rocblas_destroy_handle(d->blas);
+    for (void* p : {(void*)d->blas_ws, (void*)d->x, (void*)d->n, (void*)d->qkv, (void*)d->qw,
+                    (void*)d->attn, (void*)d->gu, (void*)d->h, (void*)d->logits, (void*)d->am_v,
+                    (void*)d->am_i})
+        if (p) (void)hipFree(p);
+    delete d;
+}
+
+// y[rows][n_out] = f16(x[rows][k] . W[n_out][k]^T (+ y)), f32 accumulation.
+// Row-major [rows][k] is column-major k x rows, so y^T = W . x^T is
+// op(A) = W^T of the column-major k x n_out array W.
+int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f16* x, f16* y,
+             bool accumulate) {
+    const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
+    const rocblas_status st = rocblas_gemm_ex(
+        d->blas, rocblas_operation_transpose, rocblas_operation_none, n_out, rows, k, &alpha, W,
+        rocblas_datatype_f16_r, k, x, rocblas_datatype_f16_r, k, &beta, y, rocblas_datatype_f16_r,
+        n_out, y, rocblas_datatype_f16_r, n_out, rocblas_datatype_f32_r,
+        rocblas_gemm_algo_standard, 0, 0);
+    if (st != rocblas_status_success) return fail(QASR_EDEVICE, "rocblas_gemm_ex: %s", blas_msg(st));
+    return QASR_OK;
+}
+
+// logits[rows][vocab] (f32) = n[rows][hs] . E[vocab][hs]^T.
+int gemm_logits(qasr_decoder* d, int rows, const f16* nrows, float* out) {
+    const int hs = d->cfg.hidden_size, vocab = d->cfg.vocab_size;
+    const float alpha = 1.0f, beta = 0.0f;
+    const rocblas_status st = rocblas_gemm_ex(
+        d->blas, rocblas_operation_transpose, rocblas_operation_none, vocab, rows, hs, &alpha,
+        d->embed, rocblas_datatype_f16_r, hs, nrows, rocblas_datatype_f16_r, hs, &beta, out,
+        rocblas_datatype_f32_r, vocab, out, rocblas_datatype_f32_r, vocab, rocblas_datatype_f32_r,
+        rocblas_gemm_algo_standard, 0, 0);
+    if (st != rocblas_status_success) return fail(QASR_EDEVICE, "rocblas_gemm_ex: %s", blas_msg(st));
+    return QASR_OK;
+}
+
+int launch_rms_norm(const f16* x, int64_t x_stride, const void* w, f16* out, int rows, int hs,
+                    float eps, hipStream_t st) {
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(rows), dim3(kNormThreads), 0, st, x, x_stride,
+                       (const f16*)w, out, hs, eps);
+    HIP_TRY(hipGetLastError(), "rms_norm launch");
+    return QASR_OK;
+}
+
+// Everything after attention in one layer, then on to the next layer's input
+// norm: o_proj + residual, post norm, gate|up, SiLU * up, down + residual.
+int layer_tail(qasr_decoder* d, const qasr_layer_weights& L, int rows, hipStream_t st) {
+    const qasr_attn_cfg& a = d->ctx->cfg;
+    const int hs = d->cfg.hidden_size, inter = d->cfg.intermediate_size;
+    const int qdim = a.num_attention_heads * a.head_dim;
+    int rc = gemm_f16(d, rows, hs, qdim, L.o_proj, d->attn, d->x, true);
+    if (rc) return rc;
+    rc = launch_rms_norm(d->x, hs, L.post_norm, d->n, rows, hs, a.rms_norm_eps, st);
+    if (rc) return rc;
+    rc = gemm_f16(d, rows, 2 * inter, hs, L.gate_up_proj, d->n, d->gu, false);
+    if (rc) return rc;
+    const int64_t threads = (int64_t)rows * (inter / 8);
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                       d->gu, inter, rows, d->h);
+    HIP_TRY(hipGetLastError(), "silu_mul launch");
+    return gemm_f16(d, rows, hs, inter, L.down_proj, d->h, d->x, true);
+}
+
+// Final norm of `rows` rows starting at x_rows, logits, argmax to next_dev;
+// kHeadRows rows at a time.
+int head(qasr_decoder* d, const f16* x_rows, int rows, int32_t* next_dev, float* logits_dev,
+         hipStream_t st) {
+    const int hs = d->cfg.hidden_size, vocab = d->cfg.vocab_size;
+    for (int r0 = 0; r0 < rows; r0 += kHeadRows) {
+        const int nr = std::min(kHeadRows, rows - r0);
+        int rc = launch_rms_norm(x_rows + (int64_t)r0 * hs, hs, d->final_norm, d->n, nr, hs,
+                                 d->ctx->cfg.rms_norm_eps, st);
+        if (rc) return rc;
+        float* lg = logits_dev ? logits_dev + (int64_t)r0 * vocab : d->logits;
+        rc = gemm_logits(d, nr, d->n, lg);
+        if (rc) return rc;
+        hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxChunks, nr), dim3(kArgmaxThreads), 0,
+                           st, lg, vocab, d->am_v, d->am_i);
+        HIP_TRY(hipGetLastError(), "argmax launch");
+        hipLaunchKernelGGL(argmax_final_kernel, dim3(nr), dim3(64), 0, st, d->am_v, d->am_i, vocab,
+                           next_dev + r0);
+        HIP_TRY(hipGetLastError(), "argmax launch");
+    }
+    return QASR_OK;
+}
+
+int bind_stream(qasr_decoder* d, void* stream) {
+    const rocblas_status st = rocblas_set_stream(d->blas, (hipStream_t)stream);
+    if (st != rocblas_status_success) return fail(QASR_EDEVICE, "rocblas_set_stream: %s", blas_msg(st));
+    return QASR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qasr_decoder_create(qasr_ctx* ctx, const qasr_decoder_cfg* cfg, const void* embed_dev,
+                        const void* final_norm_dev, const qasr_layer_weights* layers,
+                        qasr_decoder** out) {
+    if (!out) return fail(QASR_EINVAL, "null output handle");
+    *out = nullptr;
+    if (!ctx || !cfg || !embed_dev || !final_norm_dev || !layers)
+        return fail(QASR_EINVAL, "null argument");
+    const qasr_attn_cfg& a = ctx->cfg;
+    const int hs = cfg->hidden_size, inter = cfg->intermediate_size, vocab = cfg->vocab_size;
+    if (hs <= 0 || hs % 8 || inter <= 0 || inter % 8 || vocab <= 0 || cfg->max_rows <= 0)
+        return fail(QASR_EINVAL, "hidden %d / intermediate %d must be positive multiples of 8, "
+                    "vocab %d and max_rows %d positive", hs, inter, vocab, cfg->max_rows);
+    if (cfg->max_rows > 4096)
+        return fail(QASR_EINVAL, "max_rows %d above the prefill limit of 4096 rows per call",
+                    cfg->max_rows);
+    for (int l = 0; l < a.num_hidden_layers; ++l) {
+        const qasr_layer_weights& L = layers[l];
+        if (!L.input_norm || !L.qkv_proj || !L.q_norm || !L.k_norm || !L.o_proj || !L.post_norm ||
+            !L.gate_up_proj || !L.down_proj)
+            return fail(QASR_EINVAL, "layer %d: null weight pointer", l);
+    }
+    DeviceScope ds(ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    qasr_decoder* d = new qasr_decoder;
+    d->ctx = ctx;
+    d->cfg = *cfg;
+    d->embed = (const f16*)embed_dev;
+    d->final_norm = (const f16*)final_norm_dev;
+    d->layers.assign(layers, layers + a.num_hidden_layers);
+    const size_t R = (size_t)cfg->max_rows;
+    const size_t qdim = (size_t)a.num_attention_heads * a.head_dim;
+    const size_t qkvdim = qdim + 2 * (size_t)a.num_key_value_heads * a.head_dim;
+    struct Alloc {
+        void** p;
+        size_t bytes;
+    } allocs[] = {
+        {(void**)&d->x, R * hs * 2},          {(void**)&d->n, R * hs * 2},
+        {(void**)&d->qkv, R * qkvdim * 2},    {(void**)&d->qw, R * qdim * 2},
+        {(void**)&d->attn, R * qdim * 2},     {(void**)&d->gu, R * 2 * (size_t)inter * 2},
+        {(void**)&d->h, R * (size_t)inter * 2},
+        {(void**)&d->logits, (size_t)kHeadRows * vocab * 4},
+        {(void**)&d->am_v, (size_t)kHeadRows * kArgmaxChunks * 4},
+        {(void**)&d->am_i, (size_t)kHeadRows * kArgmaxChunks * 4},
+        {&d->blas_ws, kBlasWorkspace},
+    };
+    for (const Alloc& al : allocs) {
+        const hipError_t e = hipMalloc(al.p, al.bytes);
+        if (e != hipSuccess) {
+            free_decoder(d);
+            return hip_fail(e, "decoder workspace");
+        }
+    }
+    rocblas_status st = rocblas_create_handle(&d->blas);
+    if (st == rocblas_status_success) st = rocblas_set_workspace(d->blas, d->blas_ws, kBlasWorkspace);
+    if (st != rocblas_status_success) {
+        free_decoder(d);
+        return fail(QASR_EDEVICE, "rocBLAS handle: %s", blas_msg(st));
+    }
+    *out = d;
+    return QASR_OK;
+}
+
+void qasr_decoder_destroy(qasr_decoder* dec) {
+    if (!dec) return;
+    DeviceScope ds(dec->ctx->device);
+    (void)hipDeviceSynchronize();
+    free_decoder(dec);
+}
+
+int qasr_decoder_step(qasr_decoder* dec, qasr_kv* kv, int batch, const int32_t* slots,
+                      const int32_t* pos, const int32_t* tokens_dev, int32_t* next_dev,
+                      float* logits_dev, void* stream) {
+    if (!dec || !kv) return fail(QASR_EINVAL, "null decoder or KV pool");
+    if (batch < 0 || batch > dec->cfg.max_rows)
+        return fail(QASR_EINVAL, "batch %d outside [0, max_rows %d]", batch, dec->cfg.max_rows);
+    if (batch == 0) return QASR_OK;
+    if (!pos || !tokens_dev || !next_dev) return fail(QASR_EINVAL, "null argument");
+    DeviceScope ds(dec->ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    const hipStream_t st = (hipStream_t)stream;
+    int rc = bind_stream(dec, stream);
+    if (rc) return rc;
+    const qasr_attn_cfg& a = dec->ctx->cfg;
+    const int hs = dec->cfg.hidden_size;
+    const int qkvdim = (a.num_attention_heads + 2 * a.num_key_value_heads) * a.head_dim;
+    hipLaunchKernelGGL(embed_rows_kernel, dim3(batch), dim3(256), 0, st, dec->embed, tokens_dev,
+                       dec->cfg.vocab_size, hs, dec->x);
+    HIP_TRY(hipGetLastError(), "embedding launch");
+    for (int l = 0; l < a.num_hidden_layers; ++l) {
+        const qasr_layer_weights& L = dec->layers[l];
+        rc = launch_rms_norm(dec->x, hs, L.input_norm, dec->n, batch, hs, a.rms_norm_eps, st);
+        if (rc) return rc;
+        rc = gemm_f16(dec, batch, qkvdim, hs, L.qkv_proj, dec->n, dec->qkv, false);
+        if (rc) return rc;
+        rc = qasr_decode_step(dec->ctx, kv, l, batch, slots, pos, dec->qkv, L.q_norm, L.k_norm,
+                              dec->attn, stream);
+        if (rc) return rc;
+        rc = layer_tail(dec, L, batch, st);
+        if (rc) return rc;
+    }
+    return head(dec, dec->x, batch, next_dev, logits_dev, st);
+}
+
+int qasr_decoder_prefill(qasr_decoder* dec, qasr_kv* kv, int slot, int kv_start, int s,
+                         const void* hidden_dev, int32_t* next_dev, float* logits_dev,
+                         void* stream) {
+    if (!dec || !kv) return fail(QASR_EINVAL, "null decoder or KV pool");
+    if (s <= 0 || s > dec->cfg.max_rows)
+        return fail(QASR_EINVAL, "prefill rows %d outside [1, max_rows %d]", s, dec->cfg.max_rows);
+    if (!hidden_dev || !next_dev) return fail(QASR_EINVAL, "null argument");
+    DeviceScope ds(dec->ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    const hipStream_t st = (hipStream_t)stream;
+    int rc = bind_stream(dec, stream);
+    if (rc) return rc;
+    const qasr_attn_cfg& a = dec->ctx->cfg;
+    const int hs = dec->cfg.hidden_size;
+    const int qkvdim = (a.num_attention_heads + 2 * a.num_key_value_heads) * a.head_dim;
+    HIP_TRY(hipMemcpyAsync(dec->x, hidden_dev, (size_t)s * hs * 2, hipMemcpyDeviceToDevice, st),
+            "prefill input copy");
+    for (int l = 0; l < a.num_hidden_layers; ++l) {
+        const qasr_layer_weights& L = dec->layers[l];
+        rc = launch_rms_norm(dec->x, hs, L.input_norm, dec->n, s, hs, a.rms_norm_eps, st);
+        if (rc) return rc;
+        rc = gemm_f16(dec, s, qkvdim, hs, L.qkv_proj, dec->n, dec->qkv, false);
+        if (rc) return rc;
+        rc = qasr_prefill_layer(dec->ctx, kv, l, slot, kv_start, s, dec->qkv, L.q_norm, L.k_norm,
+                                dec->qw, dec->attn, stream);
+        if (rc) return rc;
+        rc = layer_tail(dec, L, s, st);
+        if (rc) return rc;
+    }
+    return head(dec, dec->x + (int64_t)(s - 1) * hs, 1, next_dev, logits_dev, st);
+}
+
+}  // extern "C"

@@ -21,48 +21,16 @@
 #include <string>
 #include <vector>
 
+#include "abi_internal.hpp"
 #include "kernels.hpp"
 
 using qasr::f16;
+using qasr_abi::DeviceScope;
+using qasr_abi::fail;
+using qasr_abi::g_err;
+using qasr_abi::hip_fail;
 
 namespace {
-
-thread_local std::string g_err;
-
-int fail(int code, const char* fmt, ...) {
-    char buf[512];
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(buf, sizeof buf, fmt, ap);
-    va_end(ap);
-    g_err = buf;
-    return code;
-}
-
-int hip_fail(hipError_t e, const char* what) {
-    return fail(e == hipErrorOutOfMemory ? QASR_ENOMEM : QASR_EDEVICE, "%s: %s", what,
-                hipGetErrorString(e));
-}
-
-#define HIP_TRY(expr, what)                     \
-    do {                                        \
-        hipError_t e_ = (expr);                 \
-        if (e_ != hipSuccess) return hip_fail(e_, what); \
-    } while (0)
-
-// Makes `dev` current for the scope of an ABI call and restores the caller's.
-struct DeviceScope {
-    int prev = -1;
-    hipError_t err = hipSuccess;
-    explicit DeviceScope(int dev) {
-        err = hipGetDevice(&prev);
-        if (err == hipSuccess && prev != dev) err = hipSetDevice(dev);
-    }
-    ~DeviceScope() {
-        int cur = -1;
-        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-    }
-};
 
 // f32 -> IEEE binary16 bits, round to nearest even, subnormals kept: the
 // conversion of half::f16::from_f32 (inference.rs:1046-1047).  Written out on
@@ -98,34 +66,6 @@ int env_int(const char* name, int dflt) {
 }
 
 }  // namespace
-
-struct qasr_ctx {
-    qasr_attn_cfg cfg;
-    int device;
-    f16* cos = nullptr;
-    f16* sin = nullptr;
-    int rope_rows = 0;
-    float scale_log2;
-    int cus = 256;  // compute units of the device (decode plans two workgroups per CU)
-};
-
-struct qasr_kv {
-    qasr_ctx* ctx;
-    int slots;
-    int cap;
-    f16* base = nullptr;
-    size_t bytes = 0;
-    // decode split-K workspace
-    float* dws_acc = nullptr;
-    float* dws_ml = nullptr;
-    uint32_t* dws_ctr = nullptr;
-    int64_t dws_items = 0;
-    // prefill split workspace (grown on demand)
-    float* pws_o = nullptr;
-    float* pws_ml = nullptr;
-    uint32_t* pws_ctr = nullptr;
-    int64_t pws_items = 0;
-};
 
 namespace {
 

@@ -35,6 +35,7 @@ ABI_SYMBOLS = (
     "qasr_mrope_text_tables", "qasr_set_rope_tables", "qasr_kv_create", "qasr_kv_destroy",
     "qasr_kv_get_info", "qasr_kv_ensure_capacity", "qasr_qk_norm_rope_append",
     "qasr_decode_attn", "qasr_decode_step", "qasr_prefill_attn", "qasr_prefill_layer",
+    "qasr_decoder_create", "qasr_decoder_destroy", "qasr_decoder_step", "qasr_decoder_prefill",
 )
 
 
@@ -72,6 +73,21 @@ class KvInfo(ctypes.Structure):
         ("kv_stride", ctypes.c_int64),
         ("head_stride", ctypes.c_int64),
         ("bytes", ctypes.c_size_t),
+    ]
+
+
+class LayerWeights(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in (
+        "input_norm", "qkv_proj", "q_norm", "k_norm", "o_proj", "post_norm", "gate_up_proj",
+        "down_proj")]
+
+
+class DecoderCfg(ctypes.Structure):
+    _fields_ = [
+        ("hidden_size", ctypes.c_int32),
+        ("intermediate_size", ctypes.c_int32),
+        ("vocab_size", ctypes.c_int32),
+        ("max_rows", ctypes.c_int32),
     ]
 
 
@@ -114,6 +130,13 @@ def load(path: str = LIB_PATH):
                                     ctypes.c_int, _vp, _vp, _vp]
     L.qasr_prefill_layer.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                      ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp]
+    L.qasr_decoder_create.argtypes = [_vp, ctypes.POINTER(DecoderCfg), _vp, _vp,
+                                      ctypes.POINTER(LayerWeights), ctypes.POINTER(_vp)]
+    L.qasr_decoder_destroy.argtypes = [_vp]
+    L.qasr_decoder_destroy.restype = None
+    L.qasr_decoder_step.argtypes = [_vp, _vp, ctypes.c_int, _i32p, _i32p, _vp, _vp, _vp, _vp]
+    L.qasr_decoder_prefill.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp,
+                                       _vp, _vp, _vp]
     _lib = L
     return L
 
@@ -364,3 +387,131 @@ class AttnBackend:
             for s in slots:
                 self.pos[s] += 1
         return out
+
+
+LAYER_WEIGHT_NAMES = ("input_layernorm", "q_proj", "k_proj", "v_proj", "q_norm", "k_norm",
+                      "o_proj", "post_attention_layernorm", "gate_proj", "up_proj", "down_proj")
+
+
+class TextDecoder:
+    """The whole text decoder on one GPU (qasr_decoder_*), with the reference
+    backend's contract (TextBackend, src/inference.rs:213-269; CpuTextDecoder
+    ::prefill / ::step, src/cpu_decoder.rs:486-530): `prefill(hidden, kv_start)`
+    returns the greedy token after a prompt, `step()` embeds each slot's last
+    token, runs one position and returns the next tokens; `max_seq`,
+    `ensure_capacity`, `set_rope_tables` as in the reference.  Slots are the
+    pooled sequences of `--batch N`.
+
+    `weights`: f16 CUDA tensors keyed like a checkpoint's tensors --
+    "embed" [vocab][hs] (tied lm_head), "norm" [hs], and (layer, name) for the
+    names in LAYER_WEIGHT_NAMES, row-major [out][in].  q/k/v and gate/up are
+    concatenated here into the fused layouts the library takes; the caller's
+    tensors are not modified.
+    """
+
+    def __init__(self, weights, nqh=16, nkvh=8, head_dim=128, layers=28, eps=1e-6,
+                 max_seq=DECODER_MAX_SEQ, slots=1, max_rows=512, cap=KV_INITIAL_CAP, device=0):
+        import torch
+
+        self.t = torch
+        self.ctx = Context(nqh, nkvh, head_dim, layers, eps, max_seq, device)
+        cs, sn = mrope_text_tables(max_seq, head_dim)
+        self.ctx.set_rope_tables(cs, sn)
+        self.kv = KVPool(self.ctx, slots, min(cap, max_seq))
+        self.max_seq = max_seq
+        embed = weights["embed"]
+        self.vocab, self.hs = int(embed.shape[0]), int(embed.shape[1])
+        self.inter = int(weights[(0, "gate_proj")].shape[0])
+        self.max_rows = max_rows
+        self._keep = [embed, weights["norm"]]
+        table = (LayerWeights * layers)()
+        for l in range(layers):
+            w = {n: weights[(l, n)] for n in LAYER_WEIGHT_NAMES}
+            qkv = torch.cat([w["q_proj"], w["k_proj"], w["v_proj"]]).contiguous()
+            gate_up = torch.cat([w["gate_proj"], w["up_proj"]]).contiguous()
+            parts = dict(input_norm=w["input_layernorm"], qkv_proj=qkv, q_norm=w["q_norm"],
+                         k_norm=w["k_norm"], o_proj=w["o_proj"],
+                         post_norm=w["post_attention_layernorm"], gate_up_proj=gate_up,
+                         down_proj=w["down_proj"])
+            for name, t in parts.items():
+                setattr(table[l], name, _dev(t, f"layer {l} {name}"))
+                self._keep.append(t)
+        cfg = DecoderCfg(self.hs, self.inter, self.vocab, max_rows)
+        h = _vp()
+        _check(load().qasr_decoder_create(self.ctx.handle, ctypes.byref(cfg),
+                                          _dev(embed, "embed"), _dev(weights["norm"], "norm"),
+                                          table, ctypes.byref(h)))
+        self.handle = h
+        self.pos = [0] * slots
+        self.last = [0] * slots
+        self._tok = torch.zeros(max(slots, 1), dtype=torch.int32, device="cuda")
+        self._next = torch.zeros(max(slots, 1), dtype=torch.int32, device="cuda")
+
+    def set_rope_tables(self, cos_u16, sin_u16):
+        self.ctx.set_rope_tables(cos_u16, sin_u16)
+
+    def ensure_capacity(self, need: int) -> int:
+        """Grow-only, KV_STEP granular; keeps every row already written."""
+        return self.kv.ensure_capacity(need, max(self.pos))
+
+    def prefill(self, hidden, kv_start: int = 0, slot: int = 0, logits=None) -> int:
+        """hidden: [s][hs] f16 CUDA tensor; prefilled in chunks of max_rows
+        rows.  Returns the argmax token after the last row (and fills
+        `logits`, a [vocab] f32 CUDA tensor, if given)."""
+        s = int(hidden.shape[0])
+        if kv_start + s > self.max_seq:
+            raise QasrError(QASR_ERANGE, f"prefill needs {kv_start + s} positions, "
+                                         f"max_seq is {self.max_seq}")
+        self.ensure_capacity(kv_start + s)
+        hidden = hidden.contiguous()
+        for r0 in range(0, s, self.max_rows):
+            n = min(self.max_rows, s - r0)
+            lg = _dev(logits, "logits", self.t.float32) if logits is not None else None
+            _check(load().qasr_decoder_prefill(self.handle, self.kv.handle, slot, kv_start + r0,
+                                               n, _dev(hidden[r0:r0 + n], "hidden"),
+                                               _dev(self._next, "next", self.t.int32), lg,
+                                               _stream(None)))
+        tok = int(self._next[0].item())
+        self.pos[slot] = kv_start + s
+        self.last[slot] = tok
+        return tok
+
+    def step_tokens(self, slots: Sequence[int], pos: Sequence[int], tokens_dev, next_dev,
+                    logits=None, stream=None):
+        """Asynchronous step: tokens_dev / next_dev are int32 CUDA tensors of
+        len(slots) entries (they may be the same tensor)."""
+        lg = _dev(logits, "logits", self.t.float32) if logits is not None else None
+        _check(load().qasr_decoder_step(self.handle, self.kv.handle, len(slots), _i32(slots),
+                                        _i32(pos), _dev(tokens_dev, "tokens", self.t.int32),
+                                        _dev(next_dev, "next", self.t.int32), lg,
+                                        _stream(stream)))
+
+    def step(self, slots: Optional[Sequence[int]] = None, logits=None):
+        """One greedy step of the given slots (default: all); returns their
+        next tokens."""
+        slots = list(range(len(self.pos))) if slots is None else list(slots)
+        if any(self.pos[s] >= self.max_seq for s in slots):
+            raise QasrError(QASR_ERANGE, f"decode past max_seq {self.max_seq}")
+        self.ensure_capacity(max(self.pos[s] for s in slots) + 1)
+        b = len(slots)
+        self._tok[:b].copy_(self.t.tensor([self.last[s] for s in slots], dtype=self.t.int32))
+        self.step_tokens(slots, [self.pos[s] for s in slots], self._tok[:b], self._next[:b],
+                         logits)
+        toks = self._next[:b].tolist()
+        for s, t in zip(slots, toks):
+            self.pos[s] += 1
+            self.last[s] = t
+        return toks
+
+    def close(self):
+        if getattr(self, "handle", None):
+            load().qasr_decoder_destroy(self.handle)
+            self.handle = None
+        self.kv.close()
+        self.ctx.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
