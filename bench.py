@@ -195,6 +195,65 @@ def copy_calibration(steps: int):
             "GBps_rw": 2 * x.numel() * 2 / (ms * 1e-3) / 1e9}
 
 
+DECODERS = {"0.6B": dict(hs=1024, inter=3072), "1.7B": dict(hs=2048, inter=6144)}
+VOCAB = 151936
+
+
+def decoder_weights(hs: int, inter: int, layers: int = LAYERS, seed: int = 7):
+    """Random f16 weights of the Qwen3 text decoder shapes (values do not
+    change the timing; no checkpoint exists offline)."""
+    import torch
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    qd, kd = NQH * HD, NKVH * HD
+
+    def mat(rows, cols):
+        return (torch.randn((rows, cols), device="cuda", generator=g) * cols ** -0.5).half()
+
+    def gain(n):
+        return (torch.randn(n, device="cuda", generator=g) * 0.1 + 1.0).half()
+
+    W = {"embed": (torch.randn((VOCAB, hs), device="cuda", generator=g) * 0.1).half(),
+         "norm": gain(hs)}
+    for l in range(layers):
+        W[(l, "input_layernorm")], W[(l, "post_attention_layernorm")] = gain(hs), gain(hs)
+        W[(l, "q_norm")], W[(l, "k_norm")] = gain(HD), gain(HD)
+        W[(l, "q_proj")], W[(l, "k_proj")], W[(l, "v_proj")] = mat(qd, hs), mat(kd, hs), mat(kd, hs)
+        W[(l, "o_proj")] = mat(hs, qd)
+        W[(l, "gate_proj")], W[(l, "up_proj")] = mat(inter, hs), mat(inter, hs)
+        W[(l, "down_proj")] = mat(hs, inter)
+    return W
+
+
+def bench_text_decoder(model: str, lengths, steps: int, warmup: int):
+    """One greedy token step of the whole text decoder (qasr_decoder_step:
+    28 layers of norms, projections, this library's attention, MLP; logits and
+    argmax) for len(lengths) slots at those cached lengths, HIP-graph replay.
+    The weights are streamed once per step: their bytes over the step time is
+    the step's weight bandwidth."""
+    import torch
+
+    import qasr_attn
+
+    dims = DECODERS[model]
+    W = decoder_weights(dims["hs"], dims["inter"])
+    wbytes = sum(t.numel() * 2 for t in W.values())
+    b = len(lengths)
+    dec = qasr_attn.TextDecoder(W, NQH, NKVH, HD, LAYERS, 1e-6, 16384, slots=b, max_rows=max(b, 16),
+                                cap=cap_for(max(lengths) + 1))
+    del W
+    slots, pos = list(range(b)), list(lengths)
+    tok = torch.randint(0, VOCAB, (b,), dtype=torch.int32, device="cuda")
+    nxt = torch.empty(b, dtype=torch.int32, device="cuda")
+    ms, graph = graph_time(torch, lambda: dec.step_tokens(slots, pos, tok, nxt), steps, warmup)
+    del graph
+    dec.close()
+    torch.cuda.empty_cache()
+    return {"model": model, "slots": b, "us_per_step": ms * 1e3, "weight_bytes": wbytes,
+            "weight_GBps": wbytes / (ms * 1e-3) / 1e9}
+
+
 def cpu_baseline(lengths, budget_s: float = 10.0):
     """Reference CPU path (C++ restatement of cpu_decoder.rs, oracle/) on config
     3: stage (a) + attention for each of the 16 slots, one layer at a time,
@@ -272,6 +331,8 @@ def main():
             "prefill2": lambda: bench_prefill(420, 0, K, W),
             "prefill4": lambda: bench_prefill(512, 7680, K, W),
             "copycal": lambda: copy_calibration(K),
+            "decoder16": lambda: bench_text_decoder("1.7B", lens3, K, W),
+            "decoder1": lambda: bench_text_decoder("0.6B", [511], K, W),
         }
         log(json.dumps({only: runs[only]()}))
         return
@@ -291,6 +352,9 @@ def main():
         log("[bench] config 5")
         lens5 = splitmix_lengths(SEED_BASE + 5, 64, 64, 4096)
         extra["config5_decode"] = bench_decode(64, lens5, max(5, K // 5), W)
+        log("[bench] text decoder steps (whole decoder around the attention path)")
+        extra["text_decoder_1p7b_16slots"] = bench_text_decoder("1.7B", lens3, max(5, K // 5), W)
+        extra["text_decoder_0p6b_1slot"] = bench_text_decoder("0.6B", [511], max(5, K // 5), W)
         for k, v in extra.items():
             log(f"[bench] {k}: {json.dumps(v)}")
 

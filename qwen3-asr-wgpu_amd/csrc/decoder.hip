@@ -26,6 +26,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <vector>
 
 #include "abi_internal.hpp"
@@ -197,6 +198,104 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
     if (lane == 0) out[row] = bi < vocab ? bi : 0;
 }
 
+// ---- skinny GEMM: the projections of a decode step ----------------------
+// Y[m][n] = X[m][k] . W[n][k]^T over at most 16 activation rows: a weight
+// stream, HBM-bound, so each weight byte is read once and fed to
+// v_mfma_f32_16x16x32_f16 straight from the load (no LDS staging).  The 16
+// activation rows are the MFMA's A operand (lane l: row l%16, k 8*(l/16)..+8;
+// rows >= M read zeros through the buffer range), 16 weight rows its B
+// operand (lane l: W row n0 + l%16, the same k), and lane l holds
+// D[4*(l/16) + i][l%16].  Workgroup = 16 output columns; its 4 waves take
+// one quarter of K each, two stages of 4 k-steps (16 x 1 KiB loads) in
+// flight, and are summed in wave order (deterministic), then rounded once -- with the
+// residual y added in f32 first when ACC, or kept f32 when OUT_F32 (logits).
+constexpr int kSkinnyRows = 16;
+constexpr int kSkinnyWaves = 4;
+constexpr int kSkinnyUnroll = 4;  // k-steps per stage
+constexpr int kSkinnyKAlign = 2 * 32 * kSkinnyUnroll * kSkinnyWaves;  // K: an even stage count per wave
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
+                                             (int)std::min<int64_t>(bytes, 0x7fffffff), 0x00020000);
+}
+
+__device__ __forceinline__ qasr::half8v load8(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(qasr::half8v, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+template <bool ACC, bool OUT_F32>
+__global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(
+    const f16* __restrict__ W, const f16* __restrict__ X, void* __restrict__ Y, int M, int N,
+    int K) {
+    __shared__ qasr::float4v s_red[kSkinnyWaves][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int kw = K / kSkinnyWaves;
+    const int kbeg = wave * kw;
+    const __amdgpu_buffer_rsrc_t wres = rsrc(W + (int64_t)n0 * K, (int64_t)16 * K * 2);
+    const __amdgpu_buffer_rsrc_t xres = rsrc(X, (int64_t)M * K * 2);
+    const int off = r * K * 2 + g * 16;  // bytes: row r, k 8g (W and X rows are both K long)
+    // Stages of kSkinnyUnroll k-steps, double buffered: stage st+1's loads
+    // are issued before stage st's MFMAs.
+    const int nst = kw / (32 * kSkinnyUnroll);
+    auto load_stage = [&](int st, qasr::half8v (&a)[kSkinnyUnroll], qasr::half8v (&b)[kSkinnyUnroll]) {
+        const int k0 = kbeg + st * 32 * kSkinnyUnroll;
+#pragma unroll
+        for (int u = 0; u < kSkinnyUnroll; ++u) {
+            b[u] = load8(wres, off + (k0 + 32 * u) * 2);
+            a[u] = load8(xres, off + (k0 + 32 * u) * 2);
+        }
+    };
+    qasr::float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto mma_stage = [&](const qasr::half8v (&a)[kSkinnyUnroll], const qasr::half8v (&b)[kSkinnyUnroll]) {
+#pragma unroll
+        for (int u = 0; u < kSkinnyUnroll; ++u)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], b[u], acc, 0, 0, 0);
+    };
+    // nst is even (K is a multiple of kSkinnyKAlign): no conditional load,
+    // so every wait leaves the other buffer's loads in flight.
+    qasr::half8v a0[kSkinnyUnroll], b0[kSkinnyUnroll], a1[kSkinnyUnroll], b1[kSkinnyUnroll];
+    load_stage(0, a0, b0);
+    int st = 0;
+    for (; st + 2 < nst; st += 2) {
+        load_stage(st + 1, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_stage(a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_stage(st + 2, a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_stage(a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    load_stage(st + 1, a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_stage(a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_stage(a1, b1);
+    s_red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    qasr::float4v sum = s_red[0][lane];
+#pragma unroll
+    for (int w = 1; w < kSkinnyWaves; ++w) sum += s_red[w][lane];
+    const int n = n0 + r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * g + i;
+        if (m >= M) continue;
+        const int64_t idx = (int64_t)m * N + n;
+        if constexpr (OUT_F32) {
+            ((float*)Y)[idx] = sum[i];
+        } else {
+            f16* y = (f16*)Y;
+            y[idx] = (f16)(ACC ? (float)y[idx] + sum[i] : sum[i]);
+        }
+    }
+}
+
 const char* blas_msg(rocblas_status st) { return rocblas_status_to_string(st); }
 
 }  // namespace
@@ -209,6 +308,8 @@ struct qasr_decoder {
     std::vector<qasr_layer_weights> layers;
     rocblas_handle blas = nullptr;
     void* blas_ws = nullptr;
+    hipStream_t stream = nullptr;  // of the call in progress
+    bool force_blas = false;       // QASR_DECODER_BLAS=1: every projection through rocBLAS
     // activations, max_rows rows each
     f16* x = nullptr;     // residual stream [rows][hs]
     f16* n = nullptr;     // normed rows [rows][hs]
@@ -236,8 +337,23 @@ void free_decoder(qasr_decoder* d) {
 // y[rows][n_out] = f16(x[rows][k] . W[n_out][k]^T (+ y)), f32 accumulation.
 // Row-major [rows][k] is column-major k x rows, so y^T = W . x^T is
 // op(A) = W^T of the column-major k x n_out array W.
+bool skinny_ok(qasr_decoder* d, int rows, int n_out, int k) {
+    return !d->force_blas && rows <= kSkinnyRows && n_out % 16 == 0 && k % kSkinnyKAlign == 0;
+}
+
 int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f16* x, f16* y,
              bool accumulate) {
+    if (skinny_ok(d, rows, n_out, k)) {
+        const dim3 grid(n_out / 16), block(kSkinnyWaves * 64);
+        if (accumulate)
+            hipLaunchKernelGGL((skinny_gemm_kernel<true, false>), grid, block, 0, d->stream,
+                               (const f16*)W, x, (void*)y, rows, n_out, k);
+        else
+            hipLaunchKernelGGL((skinny_gemm_kernel<false, false>), grid, block, 0, d->stream,
+                               (const f16*)W, x, (void*)y, rows, n_out, k);
+        HIP_TRY(hipGetLastError(), "projection launch");
+        return QASR_OK;
+    }
     const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
     const rocblas_status st = rocblas_gemm_ex(
         d->blas, rocblas_operation_transpose, rocblas_operation_none, n_out, rows, k, &alpha, W,
@@ -251,6 +367,13 @@ int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f
 // logits[rows][vocab] (f32) = n[rows][hs] . E[vocab][hs]^T.
 int gemm_logits(qasr_decoder* d, int rows, const f16* nrows, float* out) {
     const int hs = d->cfg.hidden_size, vocab = d->cfg.vocab_size;
+    if (skinny_ok(d, rows, vocab, hs)) {
+        hipLaunchKernelGGL((skinny_gemm_kernel<false, true>), dim3(vocab / 16),
+                           dim3(kSkinnyWaves * 64), 0, d->stream, d->embed, nrows, (void*)out, rows,
+                           vocab, hs);
+        HIP_TRY(hipGetLastError(), "logits launch");
+        return QASR_OK;
+    }
     const float alpha = 1.0f, beta = 0.0f;
     const rocblas_status st = rocblas_gemm_ex(
         d->blas, rocblas_operation_transpose, rocblas_operation_none, vocab, rows, hs, &alpha,
@@ -312,6 +435,9 @@ int head(qasr_decoder* d, const f16* x_rows, int rows, int32_t* next_dev, float*
 }
 
 int bind_stream(qasr_decoder* d, void* stream) {
+    d->stream = (hipStream_t)stream;
+    const char* e = std::getenv("QASR_DECODER_BLAS");
+    d->force_blas = e && *e == '1';
     const rocblas_status st = rocblas_set_stream(d->blas, (hipStream_t)stream);
     if (st != rocblas_status_success) return fail(QASR_EDEVICE, "rocblas_set_stream: %s", blas_msg(st));
     return QASR_OK;
