@@ -205,14 +205,15 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
 // activation rows are the MFMA's A operand (lane l: row l%16, k 8*(l/16)..+8;
 // rows >= M read zeros through the buffer range), 16 weight rows its B
 // operand (lane l: W row n0 + l%16, the same k), and lane l holds
-// D[4*(l/16) + i][l%16].  Workgroup = 16 output columns; its 4 waves take
-// one quarter of K each, two stages of 4 k-steps (16 x 1 KiB loads) in
-// flight, and are summed in wave order (deterministic), then rounded once -- with the
-// residual y added in f32 first when ACC, or kept f32 when OUT_F32 (logits).
+// D[4*(l/16) + i][l%16].  Workgroup = 16 output columns; its KS waves take
+// one K slice each (KS = 4 when there are enough column tiles to fill the
+// GPU, up to 12 for the narrow o_proj / down_proj), two stages of 4 k-steps
+// (16 x 1 KiB loads) in flight, and are summed in wave order
+// (deterministic), then rounded once -- with the residual y added in f32
+// first when ACC, or kept f32 when OUT_F32 (logits).
 constexpr int kSkinnyRows = 16;
-constexpr int kSkinnyWaves = 4;
-constexpr int kSkinnyUnroll = 4;  // k-steps per stage
-constexpr int kSkinnyKAlign = 2 * 32 * kSkinnyUnroll * kSkinnyWaves;  // K: an even stage count per wave
+constexpr int kSkinnyUnroll = 4;               // k-steps per stage
+constexpr int kSkinnyPair = 2 * 32 * kSkinnyUnroll;  // K per wave: a multiple (even stage count)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -225,15 +226,15 @@ __device__ __forceinline__ qasr::half8v load8(__amdgpu_buffer_rsrc_t r, int off)
     return __builtin_bit_cast(qasr::half8v, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
-template <bool ACC, bool OUT_F32>
-__global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(
+template <int KS, bool ACC, bool OUT_F32>
+__global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(
     const f16* __restrict__ W, const f16* __restrict__ X, void* __restrict__ Y, int M, int N,
     int K) {
-    __shared__ qasr::float4v s_red[kSkinnyWaves][64];
+    __shared__ qasr::float4v s_red[KS][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int n0 = blockIdx.x * 16;
-    const int kw = K / kSkinnyWaves;
+    const int kw = K / KS;
     const int kbeg = wave * kw;
     const __amdgpu_buffer_rsrc_t wres = rsrc(W + (int64_t)n0 * K, (int64_t)16 * K * 2);
     const __amdgpu_buffer_rsrc_t xres = rsrc(X, (int64_t)M * K * 2);
@@ -255,7 +256,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(
         for (int u = 0; u < kSkinnyUnroll; ++u)
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], b[u], acc, 0, 0, 0);
     };
-    // nst is even (K is a multiple of kSkinnyKAlign): no conditional load,
+    // nst is even (K / KS is a multiple of kSkinnyPair): no conditional load,
     // so every wait leaves the other buffer's loads in flight.
     qasr::half8v a0[kSkinnyUnroll], b0[kSkinnyUnroll], a1[kSkinnyUnroll], b1[kSkinnyUnroll];
     load_stage(0, a0, b0);
@@ -280,7 +281,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_gemm_kernel(
     if (wave != 0) return;
     qasr::float4v sum = s_red[0][lane];
 #pragma unroll
-    for (int w = 1; w < kSkinnyWaves; ++w) sum += s_red[w][lane];
+    for (int w = 1; w < KS; ++w) sum += s_red[w][lane];
     const int n = n0 + r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -337,23 +338,46 @@ void free_decoder(qasr_decoder* d) {
 // y[rows][n_out] = f16(x[rows][k] . W[n_out][k]^T (+ y)), f32 accumulation.
 // Row-major [rows][k] is column-major k x rows, so y^T = W . x^T is
 // op(A) = W^T of the column-major k x n_out array W.
-bool skinny_ok(qasr_decoder* d, int rows, int n_out, int k) {
-    return !d->force_blas && rows <= kSkinnyRows && n_out % 16 == 0 && k % kSkinnyKAlign == 0;
+// Waves per workgroup for an n_out x k projection: 4 when the column tiles
+// alone fill the GPU, else the most of {12, 8} that splits K into whole
+// stage pairs; 0 when no split fits (rocBLAS then).
+int skinny_waves(qasr_decoder* d, int rows, int n_out, int k) {
+    if (d->force_blas || rows > kSkinnyRows || n_out % 16) return 0;
+    if (n_out / 16 < 512)
+        for (int ks : {12, 8})
+            if (k % (ks * kSkinnyPair) == 0) return ks;
+    return k % (4 * kSkinnyPair) == 0 ? 4 : 0;
+}
+
+template <bool ACC, bool OUT_F32>
+int launch_skinny(qasr_decoder* d, int ks, int rows, int n_out, int k, const void* W,
+                  const f16* x, void* y) {
+    const dim3 grid(n_out / 16);
+    switch (ks) {
+        case 4:
+            hipLaunchKernelGGL((skinny_gemm_kernel<4, ACC, OUT_F32>), grid, dim3(4 * 64), 0,
+                               d->stream, (const f16*)W, x, y, rows, n_out, k);
+            break;
+        case 8:
+            hipLaunchKernelGGL((skinny_gemm_kernel<8, ACC, OUT_F32>), grid, dim3(8 * 64), 0,
+                               d->stream, (const f16*)W, x, y, rows, n_out, k);
+            break;
+        case 12:
+            hipLaunchKernelGGL((skinny_gemm_kernel<12, ACC, OUT_F32>), grid, dim3(12 * 64), 0,
+                               d->stream, (const f16*)W, x, y, rows, n_out, k);
+            break;
+        default:
+            return fail(QASR_EINVAL, "skinny GEMM: %d waves", ks);
+    }
+    HIP_TRY(hipGetLastError(), "projection launch");
+    return QASR_OK;
 }
 
 int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f16* x, f16* y,
              bool accumulate) {
-    if (skinny_ok(d, rows, n_out, k)) {
-        const dim3 grid(n_out / 16), block(kSkinnyWaves * 64);
-        if (accumulate)
-            hipLaunchKernelGGL((skinny_gemm_kernel<true, false>), grid, block, 0, d->stream,
-                               (const f16*)W, x, (void*)y, rows, n_out, k);
-        else
-            hipLaunchKernelGGL((skinny_gemm_kernel<false, false>), grid, block, 0, d->stream,
-                               (const f16*)W, x, (void*)y, rows, n_out, k);
-        HIP_TRY(hipGetLastError(), "projection launch");
-        return QASR_OK;
-    }
+    if (const int ks = skinny_waves(d, rows, n_out, k))
+        return accumulate ? launch_skinny<true, false>(d, ks, rows, n_out, k, W, x, y)
+                          : launch_skinny<false, false>(d, ks, rows, n_out, k, W, x, y);
     const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
     const rocblas_status st = rocblas_gemm_ex(
         d->blas, rocblas_operation_transpose, rocblas_operation_none, n_out, rows, k, &alpha, W,
@@ -367,13 +391,8 @@ int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f
 // logits[rows][vocab] (f32) = n[rows][hs] . E[vocab][hs]^T.
 int gemm_logits(qasr_decoder* d, int rows, const f16* nrows, float* out) {
     const int hs = d->cfg.hidden_size, vocab = d->cfg.vocab_size;
-    if (skinny_ok(d, rows, vocab, hs)) {
-        hipLaunchKernelGGL((skinny_gemm_kernel<false, true>), dim3(vocab / 16),
-                           dim3(kSkinnyWaves * 64), 0, d->stream, d->embed, nrows, (void*)out, rows,
-                           vocab, hs);
-        HIP_TRY(hipGetLastError(), "logits launch");
-        return QASR_OK;
-    }
+    if (const int ks = skinny_waves(d, rows, vocab, hs))
+        return launch_skinny<false, true>(d, ks, rows, vocab, hs, d->embed, nrows, out);
     const float alpha = 1.0f, beta = 0.0f;
     const rocblas_status st = rocblas_gemm_ex(
         d->blas, rocblas_operation_transpose, rocblas_operation_none, vocab, rows, hs, &alpha,
