@@ -205,17 +205,24 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
 // activation rows are the MFMA's A operand (lane l: row l%16, k 8*(l/16)..+8;
 // rows >= M read zeros through the buffer range), 16 weight rows its B
 // operand (lane l: W row n0 + l%16, the same k), and lane l holds
-// D[4*(l/16) + i][l%16].  Workgroup = 16 output columns; its KS waves take
-// one K slice each (KS = 4 when there are enough column tiles to fill the
-// GPU, up to 12 for the narrow o_proj / down_proj), two stages of 4 k-steps
-// (16 x 1 KiB loads) in flight, and are summed in wave order
-// (deterministic), then rounded once -- with the residual y added in f32
-// first when ACC, or kept f32 when OUT_F32 (logits).
+// D[4*(l/16) + i][l%16].  Workgroup (tile, group) = 16 output columns x one
+// of `groups` K ranges; its KS waves take one K slice each, two stages of 4
+// k-steps (16 x 1 KiB loads) in flight, and are summed in wave order.  With
+// groups > 1 (projections with few column tiles, so that a launch still has
+// ~512 workgroups) each workgroup publishes its 16 x 16 partial with
+// device-coherent stores and the last of the tile's workgroups to arrive
+// (ticket) sums the partials in group order: deterministic, no second launch.
+// The result is rounded once -- with the residual y added in f32 first when
+// ACC, or kept f32 when OUT_F32 (logits).
 constexpr int kSkinnyRows = 16;
 constexpr int kSkinnyUnroll = 4;               // k-steps per stage
 constexpr int kSkinnyPair = 2 * 32 * kSkinnyUnroll;  // K per wave: a multiple (even stage count)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kSc1 = 16;              // buffer cache policy: device-coherent (sc1)
+constexpr int kSkinnyMaxTiles = 512;  // column tiles of a split (groups > 1) projection
+constexpr int kSkinnyMaxGroups = 12;
+constexpr int kSkinnyTargetWgs = 512;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
@@ -226,62 +233,96 @@ __device__ __forceinline__ qasr::half8v load8(__amdgpu_buffer_rsrc_t r, int off)
     return __builtin_bit_cast(qasr::half8v, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+struct SkinnyArgs {
+    const f16* W;  // [N][K]
+    const f16* X;  // [M][K]
+    void* Y;       // [M][N] f16, or f32 logits
+    int M, N, K, groups;
+    float* ws;           // split partials
+    uint32_t* counters;  // split tickets
+};
+
 template <int KS, bool ACC, bool OUT_F32>
-__global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(
-    const f16* __restrict__ W, const f16* __restrict__ X, void* __restrict__ Y, int M, int N,
-    int K) {
+__global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
     __shared__ qasr::float4v s_red[KS][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * 16;
-    const int kw = K / KS;
-    const int kbeg = wave * kw;
-    const __amdgpu_buffer_rsrc_t wres = rsrc(W + (int64_t)n0 * K, (int64_t)16 * K * 2);
-    const __amdgpu_buffer_rsrc_t xres = rsrc(X, (int64_t)M * K * 2);
+    const int M = p.M, N = p.N, K = p.K, groups = p.groups;
+    const int tile = blockIdx.x, n0 = tile * 16;
+    const int kw = K / (KS * groups);
+    const int kbeg = (blockIdx.y * KS + wave) * kw;
+    const __amdgpu_buffer_rsrc_t wres = rsrc(p.W + (int64_t)n0 * K, (int64_t)16 * K * 2);
+    const __amdgpu_buffer_rsrc_t xres = rsrc(p.X, (int64_t)M * K * 2);
     const int off = r * K * 2 + g * 16;  // bytes: row r, k 8g (W and X rows are both K long)
+
     // Stages of kSkinnyUnroll k-steps, double buffered: stage st+1's loads
     // are issued before stage st's MFMAs.
+    struct Stage {
+        qasr::half8v b[kSkinnyUnroll], x[kSkinnyUnroll];
+    };
     const int nst = kw / (32 * kSkinnyUnroll);
-    auto load_stage = [&](int st, qasr::half8v (&a)[kSkinnyUnroll], qasr::half8v (&b)[kSkinnyUnroll]) {
+    auto load_stage = [&](int st, Stage& S) {
         const int k0 = kbeg + st * 32 * kSkinnyUnroll;
 #pragma unroll
         for (int u = 0; u < kSkinnyUnroll; ++u) {
-            b[u] = load8(wres, off + (k0 + 32 * u) * 2);
-            a[u] = load8(xres, off + (k0 + 32 * u) * 2);
+            const int kk = k0 + 32 * u;
+            S.b[u] = load8(wres, off + kk * 2);
+            S.x[u] = load8(xres, off + kk * 2);
         }
     };
     qasr::float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto mma_stage = [&](const qasr::half8v (&a)[kSkinnyUnroll], const qasr::half8v (&b)[kSkinnyUnroll]) {
+    auto mma_stage = [&](const Stage& S) {
 #pragma unroll
         for (int u = 0; u < kSkinnyUnroll; ++u)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], b[u], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(S.x[u], S.b[u], acc, 0, 0, 0);
     };
     // nst is even (K / KS is a multiple of kSkinnyPair): no conditional load,
     // so every wait leaves the other buffer's loads in flight.
-    qasr::half8v a0[kSkinnyUnroll], b0[kSkinnyUnroll], a1[kSkinnyUnroll], b1[kSkinnyUnroll];
-    load_stage(0, a0, b0);
+    Stage s0, s1;
+    load_stage(0, s0);
     int st = 0;
     for (; st + 2 < nst; st += 2) {
-        load_stage(st + 1, a1, b1);
+        load_stage(st + 1, s1);
         __builtin_amdgcn_sched_barrier(0);
-        mma_stage(a0, b0);
+        mma_stage(s0);
         __builtin_amdgcn_sched_barrier(0);
-        load_stage(st + 2, a0, b0);
+        load_stage(st + 2, s0);
         __builtin_amdgcn_sched_barrier(0);
-        mma_stage(a1, b1);
+        mma_stage(s1);
         __builtin_amdgcn_sched_barrier(0);
     }
-    load_stage(st + 1, a1, b1);
+    load_stage(st + 1, s1);
     __builtin_amdgcn_sched_barrier(0);
-    mma_stage(a0, b0);
+    mma_stage(s0);
     __builtin_amdgcn_sched_barrier(0);
-    mma_stage(a1, b1);
+    mma_stage(s1);
     s_red[wave][lane] = acc;
     __syncthreads();
     if (wave != 0) return;
     qasr::float4v sum = s_red[0][lane];
 #pragma unroll
     for (int w = 1; w < KS; ++w) sum += s_red[w][lane];
+    if (groups > 1) {
+        // Only wave 0 is left: its stores complete (vmcnt(0)) before the
+        // ticket, and the last arrival reads every group's partial with
+        // device-coherent loads.
+        float* mine = p.ws + ((int64_t)tile * groups + blockIdx.y) * 256 + lane * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qasr::store_dev(&mine[i], sum[i]);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        uint32_t old = 0;
+        if (lane == 0) old = qasr::ticket_add(&p.counters[tile]);
+        old = __builtin_amdgcn_readfirstlane(old);
+        if (old != (uint32_t)(groups - 1)) return;
+        const __amdgpu_buffer_rsrc_t pres = rsrc(p.ws + (int64_t)tile * groups * 256, (int64_t)groups * 1024);
+        sum = qasr::float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int grp = 0; grp < groups; ++grp)
+            sum += __builtin_bit_cast(qasr::float4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         pres, (grp * 64 + lane) * 16, 0, kSc1));
+        if (lane == 0) qasr::ticket_reset(&p.counters[tile]);
+    }
     const int n = n0 + r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -289,9 +330,9 @@ __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(
         if (m >= M) continue;
         const int64_t idx = (int64_t)m * N + n;
         if constexpr (OUT_F32) {
-            ((float*)Y)[idx] = sum[i];
+            ((float*)p.Y)[idx] = sum[i];
         } else {
-            f16* y = (f16*)Y;
+            f16* y = (f16*)p.Y;
             y[idx] = (f16)(ACC ? (float)y[idx] + sum[i] : sum[i]);
         }
     }
@@ -322,6 +363,10 @@ struct qasr_decoder {
     float* logits = nullptr;  // [kHeadRows][vocab]
     float* am_v = nullptr;    // argmax candidates [kHeadRows][kArgmaxChunks]
     int* am_i = nullptr;
+    // split projections: partials [tile][group][64 lanes][4] and one arrival
+    // ticket per column tile (zero at rest: the last arrival resets it)
+    float* sk_ws = nullptr;
+    uint32_t* sk_ctr = nullptr;
 };
 
 namespace {
@@ -330,7 +375,7 @@ void free_decoder(qasr_decoder* d) {
     if (d->blas) (void)rocblas_destroy_handle(d->blas);
     for (void* p : {(void*)d->blas_ws, (void*)d->x, (void*)d->n, (void*)d->qkv, (void*)d->qw,
                     (void*)d->attn, (void*)d->gu, (void*)d->h, (void*)d->logits, (void*)d->am_v,
-                    (void*)d->am_i})
+                    (void*)d->am_i, (void*)d->sk_ws, (void*)d->sk_ctr})
         if (p) (void)hipFree(p);
     delete d;
 }
@@ -338,46 +383,76 @@ void free_decoder(qasr_decoder* d) {
 // y[rows][n_out] = f16(x[rows][k] . W[n_out][k]^T (+ y)), f32 accumulation.
 // Row-major [rows][k] is column-major k x rows, so y^T = W . x^T is
 // op(A) = W^T of the column-major k x n_out array W.
-// Waves per workgroup for an n_out x k projection: 4 when the column tiles
-// alone fill the GPU, else the most of {12, 8} that splits K into whole
-// stage pairs; 0 when no split fits (rocBLAS then).
-int skinny_waves(qasr_decoder* d, int rows, int n_out, int k) {
-    if (d->force_blas || rows > kSkinnyRows || n_out % 16) return 0;
-    if (n_out / 16 < 512)
-        for (int ks : {12, 8})
-            if (k % (ks * kSkinnyPair) == 0) return ks;
-    return k % (4 * kSkinnyPair) == 0 ? 4 : 0;
+// Launch shape of an n_out x k projection (measured on MI355X at the 0.6B and
+// 1.7B shapes): column tiles that fill the GPU (>= kSkinnyTargetWgs) take 4
+// waves; fewer tiles take the most of {12, 8, 4} waves whose K slices are
+// whole stage pairs, and a long K (>= 4096) is also cut into `groups` ranges
+// across workgroups until the launch has kSkinnyTargetWgs workgroups (the
+// partial merge costs ~2 us, repaid only by a long stream).  ks = 0: not a
+// skinny shape (rocBLAS then).
+struct SkinnyShape {
+    int ks = 0, groups = 1;
+};
+
+SkinnyShape skinny_shape(qasr_decoder* d, int rows, int n_out, int k) {
+    if (d->force_blas || rows > kSkinnyRows || n_out % 16) return SkinnyShape{};
+    const int tiles = n_out / 16;
+    if (tiles >= kSkinnyTargetWgs) return SkinnyShape{k % (4 * kSkinnyPair) ? 0 : 4, 1};
+    if (k >= 4096)
+        for (int g : {2, 3, 4, 6, 8, 12})
+            if (k % (4 * g * kSkinnyPair) == 0 && (tiles * g >= kSkinnyTargetWgs || g == 12))
+                return SkinnyShape{4, g};
+    for (int ks : {12, 8, 4})
+        if (k % (ks * kSkinnyPair) == 0) return SkinnyShape{ks, 1};
+    return SkinnyShape{};
 }
 
 template <bool ACC, bool OUT_F32>
-int launch_skinny(qasr_decoder* d, int ks, int rows, int n_out, int k, const void* W,
-                  const f16* x, void* y) {
-    const dim3 grid(n_out / 16);
-    switch (ks) {
+int launch_skinny(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
+    const dim3 grid(a.N / 16, sh.groups);
+    switch (sh.ks) {
         case 4:
             hipLaunchKernelGGL((skinny_gemm_kernel<4, ACC, OUT_F32>), grid, dim3(4 * 64), 0,
-                               d->stream, (const f16*)W, x, y, rows, n_out, k);
+                               d->stream, a);
             break;
         case 8:
             hipLaunchKernelGGL((skinny_gemm_kernel<8, ACC, OUT_F32>), grid, dim3(8 * 64), 0,
-                               d->stream, (const f16*)W, x, y, rows, n_out, k);
+                               d->stream, a);
             break;
         case 12:
-            hipLaunchKernelGGL((skinny_gemm_kernel<12, ACC, OUT_F32>), grid, dim3(12 * 64), 0,
-                               d->stream, (const f16*)W, x, y, rows, n_out, k);
+            hipLaunchKernelGGL((skinny_gemm_kernel<12, ACC, OUT_F32>), grid, dim3(12 * 64),
+                               0, d->stream, a);
             break;
         default:
-            return fail(QASR_EINVAL, "skinny GEMM: %d waves", ks);
+            return fail(QASR_EINVAL, "skinny GEMM: %d waves", sh.ks);
     }
     HIP_TRY(hipGetLastError(), "projection launch");
     return QASR_OK;
 }
 
+SkinnyArgs skinny_args(qasr_decoder* d, SkinnyShape sh, int rows, int n_out, int k, const void* W,
+                       const f16* x, void* y) {
+    SkinnyArgs a{};
+    a.W = (const f16*)W;
+    a.X = x;
+    a.Y = y;
+    a.M = rows;
+    a.N = n_out;
+    a.K = k;
+    a.groups = sh.groups;
+    a.ws = d->sk_ws;
+    a.counters = d->sk_ctr;
+    return a;
+}
+
 int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f16* x, f16* y,
              bool accumulate) {
-    if (const int ks = skinny_waves(d, rows, n_out, k))
-        return accumulate ? launch_skinny<true, false>(d, ks, rows, n_out, k, W, x, y)
-                          : launch_skinny<false, false>(d, ks, rows, n_out, k, W, x, y);
+    const SkinnyShape sh = skinny_shape(d, rows, n_out, k);
+    if (sh.ks) {
+        const SkinnyArgs a = skinny_args(d, sh, rows, n_out, k, W, x, y);
+        return accumulate ? launch_skinny<true, false>(d, sh, a)
+                          : launch_skinny<false, false>(d, sh, a);
+    }
     const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
     const rocblas_status st = rocblas_gemm_ex(
         d->blas, rocblas_operation_transpose, rocblas_operation_none, n_out, rows, k, &alpha, W,
@@ -391,8 +466,10 @@ int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f
 // logits[rows][vocab] (f32) = n[rows][hs] . E[vocab][hs]^T.
 int gemm_logits(qasr_decoder* d, int rows, const f16* nrows, float* out) {
     const int hs = d->cfg.hidden_size, vocab = d->cfg.vocab_size;
-    if (const int ks = skinny_waves(d, rows, vocab, hs))
-        return launch_skinny<false, true>(d, ks, rows, vocab, hs, d->embed, nrows, out);
+    const SkinnyShape sh = skinny_shape(d, rows, vocab, hs);
+    if (sh.ks)
+        return launch_skinny<false, true>(
+            d, sh, skinny_args(d, sh, rows, vocab, hs, d->embed, nrows, out));
     const float alpha = 1.0f, beta = 0.0f;
     const rocblas_status st = rocblas_gemm_ex(
         d->blas, rocblas_operation_transpose, rocblas_operation_none, vocab, rows, hs, &alpha,
@@ -510,12 +587,21 @@ int qasr_decoder_create(qasr_ctx* ctx, const qasr_decoder_cfg* cfg, const void* 
         {(void**)&d->am_v, (size_t)kHeadRows * kArgmaxChunks * 4},
         {(void**)&d->am_i, (size_t)kHeadRows * kArgmaxChunks * 4},
         {&d->blas_ws, kBlasWorkspace},
+        {(void**)&d->sk_ws, (size_t)kSkinnyMaxTiles * kSkinnyMaxGroups * 1024},
+        {(void**)&d->sk_ctr, (size_t)kSkinnyMaxTiles * 4},
     };
     for (const Alloc& al : allocs) {
         const hipError_t e = hipMalloc(al.p, al.bytes);
         if (e != hipSuccess) {
             free_decoder(d);
             return hip_fail(e, "decoder workspace");
+        }
+    }
+    {
+        const hipError_t e = hipMemset(d->sk_ctr, 0, (size_t)kSkinnyMaxTiles * 4);
+        if (e != hipSuccess) {
+            free_decoder(d);
+            return hip_fail(e, "decoder counters");
         }
     }
     rocblas_status st = rocblas_create_handle(&d->blas);

@@ -170,7 +170,8 @@ def test_native_decoder_step_graph_replays_equal_eager(O, gpu):
 @pytest.mark.parametrize("model,batch", [("1.7B", 16), ("0.6B", 1), ("0.6B", 5)])
 def test_skinny_projections_match_rocblas(gpu, model, batch, monkeypatch):
     """The decode-step projections (at most 16 rows: this library's MFMA
-    skinny GEMM) against rocBLAS for the same steps (QASR_DECODER_BLAS=1):
+    skinny GEMM, split across workgroups for a long K) against rocBLAS for
+    the same steps (QASR_DECODER_BLAS=1):
     logits within rounding of each other, the same tokens wherever the top-2
     margin is clear."""
     import torch
@@ -186,8 +187,8 @@ def test_skinny_projections_match_rocblas(gpu, model, batch, monkeypatch):
     slots, pos = list(range(batch)), [dec.pos[i] for i in range(batch)]
     tok = torch.tensor([dec.last[i] for i in range(batch)], dtype=torch.int32, device="cuda")
     out = {}
-    for name, env in (("skinny", "0"), ("rocblas", "1")):
-        monkeypatch.setenv("QASR_DECODER_BLAS", env)
+    for name, blas in (("skinny", "0"), ("rocblas", "1")):
+        monkeypatch.setenv("QASR_DECODER_BLAS", blas)
         nxt = torch.empty(batch, dtype=torch.int32, device="cuda")
         lg = torch.empty((batch, cfg["vocab"]), dtype=torch.float32, device="cuda")
         say(f"{model} batch {batch}: step via {name}")
@@ -195,14 +196,17 @@ def test_skinny_projections_match_rocblas(gpu, model, batch, monkeypatch):
         torch.cuda.synchronize()
         out[name] = (nxt.cpu().numpy(), lg.cpu().numpy())
     dec.close()
-    (t1, l1), (t2, l2) = out["skinny"], out["rocblas"]
+    t2, l2 = out["rocblas"]
     spread = float(np.std(l2))
-    diff = float(np.max(np.abs(l1 - l2)))
-    say(f"max logit diff {diff:.3g} (spread {spread:.3g})")
-    # f16 roundings between the layers turn summation-order differences into
-    # last-bit flips; a wrong operand layout would differ by the spread itself.
-    assert diff <= 2e-2 * spread
-    for b in range(batch):
-        top = np.partition(l2[b], -2)[-2:]
-        if top[1] - top[0] > 2 * diff:
-            assert t1[b] == t2[b], f"entry {b}: {t1[b]} vs {t2[b]} at a clear margin"
+    for name in ("skinny",):
+        t1, l1 = out[name]
+        diff = float(np.max(np.abs(l1 - l2)))
+        say(f"{name}: max logit diff {diff:.3g} (spread {spread:.3g})")
+        # f16 roundings between the layers turn summation-order differences
+        # into last-bit flips; a wrong operand layout would differ by the
+        # spread itself.
+        assert diff <= 2e-2 * spread
+        for b in range(batch):
+            top = np.partition(l2[b], -2)[-2:]
+            if top[1] - top[0] > 2 * diff:
+                assert t1[b] == t2[b], f"{name} entry {b}: {t1[b]} vs {t2[b]} at a clear margin"
