@@ -406,16 +406,19 @@ class TextDecoder:
     "embed" [vocab][hs] (tied lm_head), "norm" [hs], and (layer, name) for the
     names in LAYER_WEIGHT_NAMES, row-major [out][in].  q/k/v and gate/up are
     concatenated here into the fused layouts the library takes; the caller's
-    tensors are not modified.
+    tensors are not modified.  `checkpoint.open_text_decoder` builds one from a
+    Qwen3-ASR model directory (config.json + safetensors).
     """
 
     def __init__(self, weights, nqh=16, nkvh=8, head_dim=128, layers=28, eps=1e-6,
-                 max_seq=DECODER_MAX_SEQ, slots=1, max_rows=512, cap=KV_INITIAL_CAP, device=0):
+                 max_seq=DECODER_MAX_SEQ, slots=1, max_rows=512, cap=KV_INITIAL_CAP, device=0,
+                 rope_theta=1e6, mrope_section=(24, 20, 20), mrope_interleaved=True):
         import torch
 
         self.t = torch
         self.ctx = Context(nqh, nkvh, head_dim, layers, eps, max_seq, device)
-        cs, sn = mrope_text_tables(max_seq, head_dim)
+        cs, sn = mrope_text_tables(max_seq, head_dim, rope_theta, tuple(mrope_section),
+                                   mrope_interleaved)
         self.ctx.set_rope_tables(cs, sn)
         self.kv = KVPool(self.ctx, slots, min(cap, max_seq))
         self.max_seq = max_seq

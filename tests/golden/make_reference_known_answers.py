@@ -6,6 +6,7 @@ Sources (paths relative to the reference checkout):
   src/config.rs:102-110 text-decoder defaults (vocab, heads, head_dim, eps, theta)
   src/config.rs:177-195 mrope_section default [24, 20, 20], interleaved default true
   src/config.rs:261-290 HF-native config layout test (text_config values)
+  src/config.rs:212-258, 331-341 mrope_section / mrope_interleaved from rope_scaling
 
 The reference ships no numeric vectors for attention itself (its numeric gate
 is transcript identity on audio fixtures kept outside the repository), so
@@ -39,6 +40,46 @@ KNOWN = {
         "num_attention_heads": 16, "num_key_value_heads": 8, "head_dim": 128,
         "rms_norm_eps": 1e-6, "rope_theta": 1000000, "num_hidden_layers": 28, "hidden_size": 1024,
     },
+    # config.json inputs and the text-decoder values the reference derives from
+    # them: the HF-native test's own JSON, and the rope_scaling cases of the
+    # mrope tests written as the text_config JSON their structs stand for.
+    "config_parsing": [
+        {"source": "src/config.rs:262-290",
+         "json": {"audio_config": {"d_model": 896, "encoder_layers": 18, "encoder_attention_heads": 14,
+                                   "encoder_ffn_dim": 3584, "num_mel_bins": 128, "n_window": 50,
+                                   "n_window_infer": 800, "conv_chunksize": 500, "output_dim": 1024},
+                  "audio_token_id": 151676,
+                  "text_config": {"vocab_size": 151936, "hidden_size": 1024, "intermediate_size": 3072,
+                                  "num_hidden_layers": 28, "num_attention_heads": 16,
+                                  "num_key_value_heads": 8, "head_dim": 128, "rms_norm_eps": 1e-6,
+                                  "rope_parameters": {"rope_theta": 1000000, "rope_type": "default"}}},
+         "expect": {"hidden_size": 1024, "num_hidden_layers": 28, "rope_theta": 1e6,
+                    "mrope_section": [24, 20, 20], "mrope_interleaved": True}},
+        {"source": "src/config.rs:212-216, 230-234 (no rope_scaling)",
+         "json": {"thinker_config": {"audio_config": {}, "text_config": {}}},
+         "expect": {"vocab_size": 151936, "hidden_size": 1024, "intermediate_size": 3072,
+                    "rope_theta": 1e6, "mrope_section": [24, 20, 20], "mrope_interleaved": True}},
+        {"source": "src/config.rs:218-228",
+         "json": {"thinker_config": {"audio_config": {}, "text_config": {
+             "rope_scaling": {"rope_type": "mrope", "mrope_section": [4, 4, 8],
+                              "interleaved": False, "mrope_interleaved": False}}}},
+         "expect": {"mrope_section": [4, 4, 8], "mrope_interleaved": False}},
+        {"source": "src/config.rs:236-246",
+         "json": {"thinker_config": {"audio_config": {}, "text_config": {
+             "rope_scaling": {"rope_type": "mrope", "mrope_section": [24, 20, 20],
+                              "interleaved": False, "mrope_interleaved": True}}}},
+         "expect": {"mrope_section": [24, 20, 20], "mrope_interleaved": True}},
+        {"source": "src/config.rs:248-258",
+         "json": {"thinker_config": {"audio_config": {}, "text_config": {
+             "rope_scaling": {"rope_type": "mrope", "mrope_section": [24, 20, 20],
+                              "interleaved": True, "mrope_interleaved": False}}}},
+         "expect": {"mrope_interleaved": True}},
+        {"source": "src/config.rs:331-341",
+         "json": {"thinker_config": {"audio_config": {}, "text_config": {
+             "rope_scaling": {"rope_type": "mrope", "mrope_section": [24, 20, 20],
+                              "interleaved": False, "mrope_interleaved": False}}}},
+         "expect": {"mrope_interleaved": False}},
+    ],
 }
 
 if __name__ == "__main__":

@@ -210,3 +210,56 @@ def test_skinny_projections_match_rocblas(gpu, model, batch, monkeypatch):
             top = np.partition(l2[b], -2)[-2:]
             if top[1] - top[0] > 2 * diff:
                 assert t1[b] == t2[b], f"{name} entry {b}: {t1[b]} vs {t2[b]} at a clear margin"
+
+
+def test_decoder_from_checkpoint_equals_decoder_from_weights(gpu, tmp_path):
+    """checkpoint.open_text_decoder over a synthetic HF-native checkpoint (two
+    shards + index, some tensors stored as f32 holding f16 values, config.json
+    in the transformers-native layout) runs the same decoder as TextDecoder
+    over the in-memory weights: identical tokens and logits, bitwise."""
+    import json
+
+    import torch
+    from safetensors.torch import save_file
+
+    import checkpoint
+    from gpu_helpers import say
+
+    cfg = dict(CFG_0P6B, layers=2, vocab=4096)
+    W = synth_weights(cfg, SEED_BASE + 970, device="cuda")
+    names = {"embed": "model.language_model.embed_tokens.weight",
+             "norm": "model.language_model.norm.weight"}
+    for l in range(cfg["layers"]):
+        for key, suffix in checkpoint._LAYER_TENSORS:
+            names[(l, key)] = f"model.language_model.layers.{l}.{suffix}"
+    shards = [{}, {}]
+    index = {}
+    for i, (k, n) in enumerate(sorted(names.items(), key=lambda kv: kv[1])):
+        t = W[k].cpu()
+        shards[i % 2][n] = t.float() if i % 3 == 0 else t  # f32 copies of f16 values are exact
+        index[n] = f"model-0000{i % 2 + 1}-of-00002.safetensors"
+    for j, sh in enumerate(shards):
+        save_file(sh, str(tmp_path / f"model-0000{j + 1}-of-00002.safetensors"))
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": index}))
+    (tmp_path / "config.json").write_text(json.dumps({"text_config": {
+        "vocab_size": cfg["vocab"], "hidden_size": cfg["hs"], "intermediate_size": cfg["inter"],
+        "num_hidden_layers": cfg["layers"], "num_attention_heads": cfg["nqh"],
+        "num_key_value_heads": cfg["nkvh"], "head_dim": cfg["hd"], "rms_norm_eps": cfg["eps"],
+        "rope_parameters": {"rope_theta": 1000000, "rope_type": "default"}}}))
+
+    hidden = _prompt(SEED_BASE + 971, 33, cfg["hs"])
+    runs = []
+    for label in ("weights", "checkpoint"):
+        say(f"decoder from {label}")
+        dec = (_native(cfg, W, 1, 1024) if label == "weights"
+               else checkpoint.open_text_decoder(str(tmp_path), slots=1, max_rows=512))
+        lg = torch.empty((1, cfg["vocab"]), dtype=torch.float32, device="cuda")
+        toks = [dec.prefill(hidden, 0, logits=lg[0])]
+        lgs = [lg.cpu().numpy().copy()]
+        for _ in range(6):
+            toks.append(dec.step(logits=lg)[0])
+            lgs.append(lg.cpu().numpy().copy())
+        dec.close()
+        runs.append((toks, np.stack(lgs)))
+    assert runs[0][0] == runs[1][0]
+    assert np.array_equal(runs[0][1], runs[1][1])
