@@ -199,9 +199,12 @@ DECODERS = {"0.6B": dict(hs=1024, inter=3072), "1.7B": dict(hs=2048, inter=6144)
 VOCAB = 151936
 
 
-def decoder_weights(hs: int, inter: int, layers: int = LAYERS, seed: int = 7):
+def decoder_weights(hs: int, inter: int, layers: int = LAYERS, seed: int = 7, int8: bool = False):
     """Random f16 weights of the Qwen3 text decoder shapes (values do not
-    change the timing; no checkpoint exists offline)."""
+    change the timing; no checkpoint exists offline).  With `int8` the seven
+    linears of each layer are stored as the reference's int8 checkpoints hold
+    them: int8 [out][in] with an f32 scale per row (embedding and norms stay
+    f16)."""
     import torch
 
     g = torch.Generator(device="cuda")
@@ -223,10 +226,16 @@ def decoder_weights(hs: int, inter: int, layers: int = LAYERS, seed: int = 7):
         W[(l, "o_proj")] = mat(hs, qd)
         W[(l, "gate_proj")], W[(l, "up_proj")] = mat(inter, hs), mat(inter, hs)
         W[(l, "down_proj")] = mat(hs, inter)
+    if int8:
+        for key in [k for k in W if isinstance(k, tuple) and k[1].endswith("_proj")]:
+            w = W[key].float()
+            s = w.abs().amax(dim=1).clamp_min(1e-8) / 127.0
+            W[key] = torch.round(w / s[:, None]).clamp(-128, 127).to(torch.int8)
+            W[(key[0], key[1] + "_scale")] = s
     return W
 
 
-def bench_text_decoder(model: str, lengths, steps: int, warmup: int):
+def bench_text_decoder(model: str, lengths, steps: int, warmup: int, int8: bool = False):
     """One greedy token step of the whole text decoder (qasr_decoder_step:
     28 layers of norms, projections, this library's attention, MLP; logits and
     argmax) for len(lengths) slots at those cached lengths, HIP-graph replay.
@@ -237,8 +246,8 @@ def bench_text_decoder(model: str, lengths, steps: int, warmup: int):
     import qasr_attn
 
     dims = DECODERS[model]
-    W = decoder_weights(dims["hs"], dims["inter"])
-    wbytes = sum(t.numel() * 2 for t in W.values())
+    W = decoder_weights(dims["hs"], dims["inter"], int8=int8)
+    wbytes = sum(t.numel() * t.element_size() for t in W.values())
     b = len(lengths)
     dec = qasr_attn.TextDecoder(W, NQH, NKVH, HD, LAYERS, 1e-6, 16384, slots=b, max_rows=max(b, 16),
                                 cap=cap_for(max(lengths) + 1))
@@ -250,7 +259,8 @@ def bench_text_decoder(model: str, lengths, steps: int, warmup: int):
     del graph
     dec.close()
     torch.cuda.empty_cache()
-    return {"model": model, "slots": b, "us_per_step": ms * 1e3, "weight_bytes": wbytes,
+    return {"model": model, "slots": b, "weights": "int8" if int8 else "f16",
+            "us_per_step": ms * 1e3, "weight_bytes": wbytes,
             "weight_GBps": wbytes / (ms * 1e-3) / 1e9}
 
 
@@ -333,6 +343,8 @@ def main():
             "copycal": lambda: copy_calibration(K),
             "decoder16": lambda: bench_text_decoder("1.7B", lens3, K, W),
             "decoder1": lambda: bench_text_decoder("0.6B", [511], K, W),
+            "decoder16_int8": lambda: bench_text_decoder("1.7B", lens3, K, W, int8=True),
+            "decoder1_int8": lambda: bench_text_decoder("0.6B", [511], K, W, int8=True),
         }
         log(json.dumps({only: runs[only]()}))
         return
@@ -355,6 +367,10 @@ def main():
         log("[bench] text decoder steps (whole decoder around the attention path)")
         extra["text_decoder_1p7b_16slots"] = bench_text_decoder("1.7B", lens3, max(5, K // 5), W)
         extra["text_decoder_0p6b_1slot"] = bench_text_decoder("0.6B", [511], max(5, K // 5), W)
+        extra["text_decoder_1p7b_16slots_int8"] = bench_text_decoder("1.7B", lens3, max(5, K // 5),
+                                                                     W, int8=True)
+        extra["text_decoder_0p6b_1slot_int8"] = bench_text_decoder("0.6B", [511], max(5, K // 5),
+                                                                   W, int8=True)
         for k, v in extra.items():
             log(f"[bench] {k}: {json.dumps(v)}")
 

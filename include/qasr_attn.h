@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define QASR_ABI_VERSION 1
+#define QASR_ABI_VERSION 2
 
 /* Status codes. */
 #define QASR_OK 0
@@ -184,7 +184,13 @@ int qasr_prefill_layer(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_s
  * so logits agree to rounding, not bitwise.
  *
  * Weights are device pointers owned by the caller and must outlive the
- * decoder; f16 bits, row-major [out][in] as in the checkpoint. */
+ * decoder; f16 bits, row-major [out][in] as in the checkpoint.  A projection
+ * whose *_scale pointer is set is int8 instead (the reference's resident-int8
+ * checkpoints, weights.rs:296-427, decoder.rs:4364-4395): signed int8
+ * [out][in] with one f32 scale per output row, each weight used as
+ * f16(q * scale[row]) rounded to nearest even -- the value the reference's
+ * W8 kernels form per weight.  Fused rows keep their parts' order for the
+ * scales too. */
 typedef struct qasr_layer_weights {
     const void* input_norm;   /* [hs] (input_layernorm) */
     const void* qkv_proj;     /* [(nqh + 2*nkvh)*hd][hs]: q_proj rows, then k_proj, then v_proj */
@@ -194,6 +200,10 @@ typedef struct qasr_layer_weights {
     const void* post_norm;    /* [hs] (post_attention_layernorm) */
     const void* gate_up_proj; /* [2*inter][hs]: gate_proj rows, then up_proj */
     const void* down_proj;    /* [hs][inter] */
+    const float* qkv_scale;     /* NULL, or [(nqh + 2*nkvh)*hd]: qkv_proj is int8 */
+    const float* o_scale;       /* NULL, or [hs]: o_proj is int8 */
+    const float* gate_up_scale; /* NULL, or [2*inter]: gate_up_proj is int8 */
+    const float* down_scale;    /* NULL, or [hs]: down_proj is int8 */
 } qasr_layer_weights;
 
 typedef struct qasr_decoder_cfg {

@@ -16,8 +16,11 @@ Host-side mirror of the reference's loading path for the text decoder:
     f32 -> f16 RNE), done here on the device.
 
 The decoder computes its logits against the tied embedding (cpu_decoder.rs:
-458-471), so `embed_tokens` is also the lm_head; int8 checkpoints (the
-reference's resident-int8 layout) are refused.
+458-471), so `embed_tokens` is also the lm_head.  Int8 checkpoints (the
+reference's resident-int8 layout, weights.rs:296-427, decoder.rs:4352-4395)
+keep their I8 [out][in] linears with the F32 [out] `<name>.weight_scale`
+siblings; like the reference, the decoder's linears are int8 all together or
+not at all.
 
 `load_text_weights` returns the weight dictionary `qasr_attn.TextDecoder`
 takes; `open_text_decoder` builds the decoder from a model directory.
@@ -33,6 +36,9 @@ TEXT_DEFAULTS = dict(vocab_size=151936, hidden_size=1024, intermediate_size=3072
                      head_dim=128, rms_norm_eps=1e-6, rope_theta=1e6)
 DEFAULT_MROPE_SECTION = (24, 20, 20)
 TEXT_PREFIX = "thinker.model"
+
+INT8_SCALE_SUFFIX = ".weight_scale"
+_LINEARS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
 
 # (name in the weight dictionary, tensor under thinker.model.layers.{l})
 _LAYER_TENSORS = (
@@ -109,14 +115,15 @@ def _to_f16(t, device):
         return t.to(device)
     if t.dtype in (torch.bfloat16, torch.float32):
         return t.to(device).float().half()
-    raise CheckpointError(f"unsupported dtype {t.dtype} for a text-decoder weight "
-                          "(int8 checkpoints are not supported by this build)")
+    raise CheckpointError(f"unsupported dtype {t.dtype} for a floating-point weight")
 
 
 def load_text_weights(model_dir: str, num_layers: Optional[int] = None,
                       device: str = "cuda") -> Dict:
-    """Text-decoder tensors of a checkpoint directory as f16 tensors on
-    `device`, keyed "embed", "norm" and (layer, name)."""
+    """Text-decoder tensors of a checkpoint directory on `device`, keyed
+    "embed", "norm" and (layer, name): f16, except int8 linears (torch.int8)
+    with their f32 scales under (layer, name + "_scale")."""
+    import torch
     from safetensors import safe_open
 
     if num_layers is None:
@@ -125,14 +132,33 @@ def load_text_weights(model_dir: str, num_layers: Optional[int] = None,
     for l in range(num_layers):
         for key, suffix in _LAYER_TENSORS:
             wanted[f"{TEXT_PREFIX}.layers.{l}.{suffix}"] = (l, key)
-    out = {}
+            if key in _LINEARS:
+                scale = suffix[:-len(".weight")] + INT8_SCALE_SUFFIX
+                wanted[f"{TEXT_PREFIX}.layers.{l}.{scale}"] = (l, key + "_scale")
+    raw = {}
     for path in _shards(model_dir):
         with safe_open(path, framework="pt") as f:
             for name in f.keys():
                 dst = wanted.get(remap_name(name))
                 if dst is not None:
-                    out[dst] = _to_f16(f.get_tensor(name), device)
-    missing = [n for n, k in wanted.items() if k not in out]
+                    raw[dst] = f.get_tensor(name)
+    linears = [(l, k) for l in range(num_layers) for k in _LINEARS]
+    int8 = [k for k in linears if k in raw and raw[k].dtype == torch.int8]
+    if int8 and len(int8) != len([k for k in linears if k in raw]):
+        raise CheckpointError(f"{int8[0]} is int8 in an otherwise floating-point checkpoint; "
+                              "quantise every decoder linear or none")
+    out = {}
+    for key, t in raw.items():
+        if isinstance(key, tuple) and key[1].endswith("_scale"):
+            if int8:
+                out[key] = t.to(device).float().contiguous()
+        elif t.dtype == torch.int8:
+            out[key] = t.to(device).contiguous()
+        else:
+            out[key] = _to_f16(t, device)
+    need = [n for n, k in wanted.items()
+            if not (isinstance(k, tuple) and k[1].endswith("_scale")) or int8]
+    missing = [n for n in need if wanted[n] not in out]
     if missing:
         raise CheckpointError(f"{len(missing)} text-decoder tensors missing, e.g. {missing[0]}")
     return out

@@ -215,7 +215,7 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
 // The result is rounded once -- with the residual y added in f32 first when
 // ACC, or kept f32 when OUT_F32 (logits).
 constexpr int kSkinnyRows = 16;
-constexpr int kSkinnyUnroll = 4;               // k-steps per stage
+constexpr int kSkinnyUnroll = 4;                     // k-steps per stage (8 measured no faster)
 constexpr int kSkinnyPair = 2 * 32 * kSkinnyUnroll;  // K per wave: a multiple (even stage count)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -223,6 +223,7 @@ constexpr int kSc1 = 16;              // buffer cache policy: device-coherent (s
 constexpr int kSkinnyMaxTiles = 512;  // column tiles of a split (groups > 1) projection
 constexpr int kSkinnyMaxGroups = 12;
 constexpr int kSkinnyTargetWgs = 512;
+constexpr int kSkinnySplitWgs = 256;  // a split projection: one workgroup per CU
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
@@ -233,8 +234,39 @@ __device__ __forceinline__ qasr::half8v load8(__amdgpu_buffer_rsrc_t r, int off)
     return __builtin_bit_cast(qasr::half8v, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+// One int8 weight row segment (8 values, two dwords) as the f16 values the
+// reference's W8 kernels use: f16(q * s) with q * s rounded to f32 once.
+// Each byte is offset by 128 (xor 0x80) so v_cvt_f32_ubyte reads q + 128
+// exactly, and fma((q + 128), s, -128 s) = q s before its single rounding.
+__device__ __forceinline__ qasr::half8v dequant8(uint32_t lo, uint32_t hi, float s, float s128) {
+    qasr::half8v h;
+    const uint32_t d[2] = {lo ^ 0x80808080u, hi ^ 0x80808080u};
+#pragma unroll
+    for (int w = 0; w < 2; ++w)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float u = (float)((d[w] >> (8 * j)) & 0xffu);
+            h[4 * w + j] = (f16)fmaf(u, s, s128);
+        }
+    return h;
+}
+
+// Prefill-side int8 projections: the layer's weights dequantized once into a
+// scratch f16 matrix for rocBLAS, out[n][k] = f16(q[n][k] * scale[n]).
+__global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restrict__ q,
+                                                           const float* __restrict__ scale,
+                                                           int64_t n_rows, int k,
+                                                           f16* __restrict__ out) {
+    const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;  // 8 weights
+    if (i >= n_rows * k) return;
+    const float s = scale[i / k];
+    const uint2 v = *(const uint2*)(q + i);
+    *(qasr::half8v*)(out + i) = dequant8(v.x, v.y, s, -128.0f * s);
+}
+
 struct SkinnyArgs {
-    const f16* W;  // [N][K]
+    const void* W;        // [N][K] f16, or int8 when `scale` is set
+    const float* scale;   // int8 weights: [N] per-row scales
     const f16* X;  // [M][K]
     void* Y;       // [M][N] f16, or f32 logits
     int M, N, K, groups;
@@ -242,7 +274,7 @@ struct SkinnyArgs {
     uint32_t* counters;  // split tickets
 };
 
-template <int KS, bool ACC, bool OUT_F32>
+template <int KS, int U, bool W8, bool ACC, bool OUT_F32>
 __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
     __shared__ qasr::float4v s_red[KS][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -251,32 +283,51 @@ __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
     const int tile = blockIdx.x, n0 = tile * 16;
     const int kw = K / (KS * groups);
     const int kbeg = (blockIdx.y * KS + wave) * kw;
-    const __amdgpu_buffer_rsrc_t wres = rsrc(p.W + (int64_t)n0 * K, (int64_t)16 * K * 2);
+    constexpr int wbytes = W8 ? 1 : 2;  // bytes per weight
+    const __amdgpu_buffer_rsrc_t wres =
+        rsrc((const char*)p.W + (int64_t)n0 * K * wbytes, (int64_t)16 * K * wbytes);
+    float ws = 0.0f, ws128 = 0.0f;  // W8: this lane's row's scale, and -128 x it
+    if constexpr (W8) {
+        ws = p.scale[n0 + r];
+        ws128 = -128.0f * ws;
+    }
     const __amdgpu_buffer_rsrc_t xres = rsrc(p.X, (int64_t)M * K * 2);
     const int off = r * K * 2 + g * 16;  // bytes: row r, k 8g (W and X rows are both K long)
 
-    // Stages of kSkinnyUnroll k-steps, double buffered: stage st+1's loads
+    // Stages of U k-steps, double buffered: stage st+1's loads
     // are issued before stage st's MFMAs.
     struct Stage {
-        qasr::half8v b[kSkinnyUnroll], x[kSkinnyUnroll];
+        qasr::half8v b[U], x[U];
+        uint2 q[U];  // W8: the raw int8 weights
     };
-    const int nst = kw / (32 * kSkinnyUnroll);
+    const int nst = kw / (32 * U);
     auto load_stage = [&](int st, Stage& S) {
-        const int k0 = kbeg + st * 32 * kSkinnyUnroll;
+        const int k0 = kbeg + st * 32 * U;
 #pragma unroll
-        for (int u = 0; u < kSkinnyUnroll; ++u) {
+        for (int u = 0; u < U; ++u) {
             const int kk = k0 + 32 * u;
-            S.b[u] = load8(wres, off + kk * 2);
+            if constexpr (W8) {
+                S.q[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                       wres, r * K + g * 8 + kk, 0, 0));
+            } else {
+                S.b[u] = load8(wres, off + kk * 2);
+            }
             S.x[u] = load8(xres, off + kk * 2);
         }
     };
     qasr::float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
     auto mma_stage = [&](const Stage& S) {
 #pragma unroll
-        for (int u = 0; u < kSkinnyUnroll; ++u)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(S.x[u], S.b[u], acc, 0, 0, 0);
+        for (int u = 0; u < U; ++u) {
+            if constexpr (W8) {
+                const qasr::half8v b = dequant8(S.q[u].x, S.q[u].y, ws, ws128);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(S.x[u], b, acc, 0, 0, 0);
+            } else {
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(S.x[u], S.b[u], acc, 0, 0, 0);
+            }
+        }
     };
-    // nst is even (K / KS is a multiple of kSkinnyPair): no conditional load,
+    // nst is even (the wave's K slice is a multiple of 64 U): no conditional load,
     // so every wait leaves the other buffer's loads in flight.
     Stage s0, s1;
     load_stage(0, s0);
@@ -367,6 +418,8 @@ struct qasr_decoder {
     // ticket per column tile (zero at rest: the last arrival resets it)
     float* sk_ws = nullptr;
     uint32_t* sk_ctr = nullptr;
+    f16* wdq = nullptr;      // int8 projections of prefill calls: one dequantised matrix
+    int64_t wdq_elems = 0;
 };
 
 namespace {
@@ -375,7 +428,7 @@ void free_decoder(qasr_decoder* d) {
     if (d->blas) (void)rocblas_destroy_handle(d->blas);
     for (void* p : {(void*)d->blas_ws, (void*)d->x, (void*)d->n, (void*)d->qkv, (void*)d->qw,
                     (void*)d->attn, (void*)d->gu, (void*)d->h, (void*)d->logits, (void*)d->am_v,
-                    (void*)d->am_i, (void*)d->sk_ws, (void*)d->sk_ctr})
+                    (void*)d->am_i, (void*)d->sk_ws, (void*)d->sk_ctr, (void*)d->wdq})
         if (p) (void)hipFree(p);
     delete d;
 }
@@ -387,9 +440,10 @@ void free_decoder(qasr_decoder* d) {
 // 1.7B shapes): column tiles that fill the GPU (>= kSkinnyTargetWgs) take 4
 // waves; fewer tiles take the most of {12, 8, 4} waves whose K slices are
 // whole stage pairs, and a long K (>= 4096) is also cut into `groups` ranges
-// across workgroups until the launch has kSkinnyTargetWgs workgroups (the
-// partial merge costs ~2 us, repaid only by a long stream).  ks = 0: not a
-// skinny shape (rocBLAS then).
+// across workgroups until the launch has kSkinnySplitWgs workgroups (the
+// partial merge costs ~2 us, repaid only by a long stream; at 2048 x 6144,
+// 2 groups beat 1, 3 and 6 by 20-65 us per 28-layer step, f16 and int8
+// alike).  ks = 0: not a skinny shape (rocBLAS then).
 struct SkinnyShape {
     int ks = 0, groups = 1;
 };
@@ -400,27 +454,28 @@ SkinnyShape skinny_shape(qasr_decoder* d, int rows, int n_out, int k) {
     if (tiles >= kSkinnyTargetWgs) return SkinnyShape{k % (4 * kSkinnyPair) ? 0 : 4, 1};
     if (k >= 4096)
         for (int g : {2, 3, 4, 6, 8, 12})
-            if (k % (4 * g * kSkinnyPair) == 0 && (tiles * g >= kSkinnyTargetWgs || g == 12))
+            if (k % (4 * g * kSkinnyPair) == 0 && (tiles * g >= kSkinnySplitWgs || g == 12))
                 return SkinnyShape{4, g};
     for (int ks : {12, 8, 4})
         if (k % (ks * kSkinnyPair) == 0) return SkinnyShape{ks, 1};
     return SkinnyShape{};
 }
 
-template <bool ACC, bool OUT_F32>
-int launch_skinny(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
+template <bool W8, bool ACC, bool OUT_F32>
+int launch_skinny_w(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
     const dim3 grid(a.N / 16, sh.groups);
+    constexpr int U = kSkinnyUnroll;
     switch (sh.ks) {
         case 4:
-            hipLaunchKernelGGL((skinny_gemm_kernel<4, ACC, OUT_F32>), grid, dim3(4 * 64), 0,
+            hipLaunchKernelGGL((skinny_gemm_kernel<4, U, W8, ACC, OUT_F32>), grid, dim3(4 * 64), 0,
                                d->stream, a);
             break;
         case 8:
-            hipLaunchKernelGGL((skinny_gemm_kernel<8, ACC, OUT_F32>), grid, dim3(8 * 64), 0,
+            hipLaunchKernelGGL((skinny_gemm_kernel<8, U, W8, ACC, OUT_F32>), grid, dim3(8 * 64), 0,
                                d->stream, a);
             break;
         case 12:
-            hipLaunchKernelGGL((skinny_gemm_kernel<12, ACC, OUT_F32>), grid, dim3(12 * 64),
+            hipLaunchKernelGGL((skinny_gemm_kernel<12, U, W8, ACC, OUT_F32>), grid, dim3(12 * 64),
                                0, d->stream, a);
             break;
         default:
@@ -430,10 +485,17 @@ int launch_skinny(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
     return QASR_OK;
 }
 
+template <bool ACC, bool OUT_F32>
+int launch_skinny(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
+    return a.scale ? launch_skinny_w<true, ACC, OUT_F32>(d, sh, a)
+                   : launch_skinny_w<false, ACC, OUT_F32>(d, sh, a);
+}
+
 SkinnyArgs skinny_args(qasr_decoder* d, SkinnyShape sh, int rows, int n_out, int k, const void* W,
-                       const f16* x, void* y) {
+                       const f16* x, void* y, const float* scale = nullptr) {
     SkinnyArgs a{};
-    a.W = (const f16*)W;
+    a.W = W;
+    a.scale = scale;
     a.X = x;
     a.Y = y;
     a.M = rows;
@@ -445,13 +507,25 @@ SkinnyArgs skinny_args(qasr_decoder* d, SkinnyShape sh, int rows, int n_out, int
     return a;
 }
 
+// y = x . W^T (+ y).  W is f16, or int8 with per-row `scale`.  Skinny shapes
+// run the MFMA skinny kernel (int8 dequantised in registers); others go to
+// rocBLAS, an int8 W first dequantised into the scratch matrix.
 int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f16* x, f16* y,
-             bool accumulate) {
+             bool accumulate, const float* scale = nullptr) {
     const SkinnyShape sh = skinny_shape(d, rows, n_out, k);
     if (sh.ks) {
-        const SkinnyArgs a = skinny_args(d, sh, rows, n_out, k, W, x, y);
+        const SkinnyArgs a = skinny_args(d, sh, rows, n_out, k, W, x, y, scale);
         return accumulate ? launch_skinny<true, false>(d, sh, a)
                           : launch_skinny<false, false>(d, sh, a);
+    }
+    if (scale) {
+        if (!d->wdq || (int64_t)n_out * k > d->wdq_elems)
+            return fail(QASR_EINVAL, "int8 projection %dx%d without dequantisation scratch", n_out, k);
+        const int64_t groups8 = (int64_t)n_out * k / 8;
+        hipLaunchKernelGGL(dequant_rows_kernel, dim3((unsigned)((groups8 + 255) / 256)), dim3(256),
+                           0, d->stream, (const int8_t*)W, scale, (int64_t)n_out, k, d->wdq);
+        HIP_TRY(hipGetLastError(), "dequantisation launch");
+        W = d->wdq;
     }
     const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
     const rocblas_status st = rocblas_gemm_ex(
@@ -494,17 +568,17 @@ int layer_tail(qasr_decoder* d, const qasr_layer_weights& L, int rows, hipStream
     const qasr_attn_cfg& a = d->ctx->cfg;
     const int hs = d->cfg.hidden_size, inter = d->cfg.intermediate_size;
     const int qdim = a.num_attention_heads * a.head_dim;
-    int rc = gemm_f16(d, rows, hs, qdim, L.o_proj, d->attn, d->x, true);
+    int rc = gemm_f16(d, rows, hs, qdim, L.o_proj, d->attn, d->x, true, L.o_scale);
     if (rc) return rc;
     rc = launch_rms_norm(d->x, hs, L.post_norm, d->n, rows, hs, a.rms_norm_eps, st);
     if (rc) return rc;
-    rc = gemm_f16(d, rows, 2 * inter, hs, L.gate_up_proj, d->n, d->gu, false);
+    rc = gemm_f16(d, rows, 2 * inter, hs, L.gate_up_proj, d->n, d->gu, false, L.gate_up_scale);
     if (rc) return rc;
     const int64_t threads = (int64_t)rows * (inter / 8);
     hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
                        d->gu, inter, rows, d->h);
     HIP_TRY(hipGetLastError(), "silu_mul launch");
-    return gemm_f16(d, rows, hs, inter, L.down_proj, d->h, d->x, true);
+    return gemm_f16(d, rows, hs, inter, L.down_proj, d->h, d->x, true, L.down_scale);
 }
 
 // Final norm of `rows` rows starting at x_rows, logits, argmax to next_dev;
@@ -590,6 +664,23 @@ int qasr_decoder_create(qasr_ctx* ctx, const qasr_decoder_cfg* cfg, const void* 
         {(void**)&d->sk_ws, (size_t)kSkinnyMaxTiles * kSkinnyMaxGroups * 1024},
         {(void**)&d->sk_ctr, (size_t)kSkinnyMaxTiles * 4},
     };
+    // The largest int8 projection sets the prefill dequantisation scratch.
+    int64_t wdq = 0;
+    for (int l = 0; l < a.num_hidden_layers; ++l) {
+        const qasr_layer_weights& L = layers[l];
+        if (L.qkv_scale) wdq = std::max<int64_t>(wdq, (int64_t)qkvdim * hs);
+        if (L.o_scale) wdq = std::max<int64_t>(wdq, (int64_t)hs * qdim);
+        if (L.gate_up_scale) wdq = std::max<int64_t>(wdq, 2LL * inter * hs);
+        if (L.down_scale) wdq = std::max<int64_t>(wdq, (int64_t)hs * inter);
+    }
+    if (wdq) {
+        const hipError_t e = hipMalloc(&d->wdq, (size_t)wdq * 2);
+        if (e != hipSuccess) {
+            free_decoder(d);
+            return hip_fail(e, "decoder dequantisation scratch");
+        }
+        d->wdq_elems = wdq;
+    }
     for (const Alloc& al : allocs) {
         const hipError_t e = hipMalloc(al.p, al.bytes);
         if (e != hipSuccess) {
@@ -644,7 +735,7 @@ int qasr_decoder_step(qasr_decoder* dec, qasr_kv* kv, int batch, const int32_t* 
         const qasr_layer_weights& L = dec->layers[l];
         rc = launch_rms_norm(dec->x, hs, L.input_norm, dec->n, batch, hs, a.rms_norm_eps, st);
         if (rc) return rc;
-        rc = gemm_f16(dec, batch, qkvdim, hs, L.qkv_proj, dec->n, dec->qkv, false);
+        rc = gemm_f16(dec, batch, qkvdim, hs, L.qkv_proj, dec->n, dec->qkv, false, L.qkv_scale);
         if (rc) return rc;
         rc = qasr_decode_step(dec->ctx, kv, l, batch, slots, pos, dec->qkv, L.q_norm, L.k_norm,
                               dec->attn, stream);
@@ -676,7 +767,7 @@ int qasr_decoder_prefill(qasr_decoder* dec, qasr_kv* kv, int slot, int kv_start,
         const qasr_layer_weights& L = dec->layers[l];
         rc = launch_rms_norm(dec->x, hs, L.input_norm, dec->n, s, hs, a.rms_norm_eps, st);
         if (rc) return rc;
-        rc = gemm_f16(dec, s, qkvdim, hs, L.qkv_proj, dec->n, dec->qkv, false);
+        rc = gemm_f16(dec, s, qkvdim, hs, L.qkv_proj, dec->n, dec->qkv, false, L.qkv_scale);
         if (rc) return rc;
         rc = qasr_prefill_layer(dec->ctx, kv, l, slot, kv_start, s, dec->qkv, L.q_norm, L.k_norm,
                                 dec->qw, dec->attn, stream);

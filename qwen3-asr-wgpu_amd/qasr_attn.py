@@ -79,7 +79,7 @@ class KvInfo(ctypes.Structure):
 class LayerWeights(ctypes.Structure):
     _fields_ = [(name, ctypes.c_void_p) for name in (
         "input_norm", "qkv_proj", "q_norm", "k_norm", "o_proj", "post_norm", "gate_up_proj",
-        "down_proj")]
+        "down_proj", "qkv_scale", "o_scale", "gate_up_scale", "down_scale")]
 
 
 class DecoderCfg(ctypes.Structure):
@@ -404,9 +404,12 @@ class TextDecoder:
 
     `weights`: f16 CUDA tensors keyed like a checkpoint's tensors --
     "embed" [vocab][hs] (tied lm_head), "norm" [hs], and (layer, name) for the
-    names in LAYER_WEIGHT_NAMES, row-major [out][in].  q/k/v and gate/up are
-    concatenated here into the fused layouts the library takes; the caller's
-    tensors are not modified.  `checkpoint.open_text_decoder` builds one from a
+    names in LAYER_WEIGHT_NAMES, row-major [out][in].  A projection may be int8
+    ([out][in] torch.int8) with its f32 per-row scales under (layer, name +
+    "_scale") -- the reference's resident-int8 checkpoints; q/k/v and gate/up
+    must then be int8 together.  q/k/v and gate/up are concatenated here into
+    the fused layouts the library takes (int8 rows with their scales, in the
+    same order); the caller's tensors are not modified.  `checkpoint.open_text_decoder` builds one from a
     Qwen3-ASR model directory (config.json + safetensors).
     """
 
@@ -430,12 +433,34 @@ class TextDecoder:
         table = (LayerWeights * layers)()
         for l in range(layers):
             w = {n: weights[(l, n)] for n in LAYER_WEIGHT_NAMES}
-            qkv = torch.cat([w["q_proj"], w["k_proj"], w["v_proj"]]).contiguous()
-            gate_up = torch.cat([w["gate_proj"], w["up_proj"]]).contiguous()
-            parts = dict(input_norm=w["input_layernorm"], qkv_proj=qkv, q_norm=w["q_norm"],
-                         k_norm=w["k_norm"], o_proj=w["o_proj"],
-                         post_norm=w["post_attention_layernorm"], gate_up_proj=gate_up,
-                         down_proj=w["down_proj"])
+
+            def proj(names, field):
+                """Fuse one projection group: f16 rows, or int8 rows + scales."""
+                ts = [w[n] for n in names]
+                int8 = [t.dtype == torch.int8 for t in ts]
+                if any(int8) and not all(int8):
+                    raise QasrError(QASR_EINVAL, f"layer {l}: {names} mix int8 and f16")
+                mat = torch.cat(ts).contiguous()
+                scale = None
+                if all(int8):
+                    scale = torch.cat([weights[(l, n + "_scale")].float() for n in names])
+                    scale = scale.contiguous()
+                    if scale.numel() != mat.shape[0]:
+                        raise QasrError(QASR_EINVAL, f"layer {l}: {names} scales do not match rows")
+                    setattr(table[l], field + "_scale", _dev(scale, f"layer {l} {field} scale",
+                                                             torch.float32))
+                    self._keep.append(scale)
+                    setattr(table[l], field + "_proj", _dev(mat, f"layer {l} {field}", torch.int8))
+                else:
+                    setattr(table[l], field + "_proj", _dev(mat, f"layer {l} {field}"))
+                self._keep.append(mat)
+
+            proj(["q_proj", "k_proj", "v_proj"], "qkv")
+            proj(["o_proj"], "o")
+            proj(["gate_proj", "up_proj"], "gate_up")
+            proj(["down_proj"], "down")
+            parts = dict(input_norm=w["input_layernorm"], q_norm=w["q_norm"], k_norm=w["k_norm"],
+                         post_norm=w["post_attention_layernorm"])
             for name, t in parts.items():
                 setattr(table[l], name, _dev(t, f"layer {l} {name}"))
                 self._keep.append(t)

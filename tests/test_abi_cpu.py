@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     lib = qasr_attn.load()
     for name in declared_functions():
         assert hasattr(lib, name), name
-    assert lib.qasr_abi_version() == 1
+    assert lib.qasr_abi_version() == 2
 
 
 def test_library_is_gfx950_hip_code():

@@ -136,22 +136,63 @@ def test_load_text_weights_narrows_and_maps(tmp_path, hf_names, shards):
         assert np.array_equal(got.view(np.uint16), _expected_f16(v, dt).view(np.uint16)), name
 
 
-def test_missing_or_int8_tensors_are_refused(tmp_path):
-    import torch
-    from safetensors.torch import save_file
-
+def test_missing_tensors_are_refused(tmp_path):
     rng = np.random.default_rng(6)
     vals = _tensors(rng, True)
     drop = "model.language_model.layers.1.mlp.down_proj.weight"
-    d1 = tmp_path / "missing"
+    _write_checkpoint(str(tmp_path), {k: v for k, v in vals.items() if k != drop}, 1)
+    with pytest.raises(C.CheckpointError, match="missing"):
+        C.load_text_weights(str(tmp_path), SHAPES["layers"], device="cpu")
+
+
+def _int8_checkpoint(tmp, vals, skip_scale=None, float_linear=None):
+    """Every decoder linear as I8 with an F32 `.weight_scale` (the reference's
+    int8 export layout); returns the int8 arrays and scales written."""
+    import torch
+    from safetensors.torch import save_file
+
+    rng = np.random.default_rng(8)
+    ts, q8 = {}, {}
+    for n, (v, _) in vals.items():
+        base = n[:-len(".weight")]
+        if any(n.endswith(f"{p}.weight") for p in C._LINEARS) and n != float_linear:
+            q = rng.integers(-128, 128, size=v.shape, dtype=np.int8)
+            sc = (rng.random(v.shape[0]).astype(np.float32) + 0.5) * 1e-3
+            ts[n] = torch.from_numpy(q)
+            if n != skip_scale:
+                ts[base + C.INT8_SCALE_SUFFIX] = torch.from_numpy(sc)
+            q8[n] = (q, sc)
+        else:
+            ts[n] = torch.from_numpy(v).to(torch.float16)
+    save_file(ts, os.path.join(tmp, "model.safetensors"))
+    return q8
+
+
+def test_int8_checkpoint_keeps_int8_and_scales(tmp_path):
+    vals = _tensors(np.random.default_rng(7), True)
+    q8 = _int8_checkpoint(str(tmp_path), vals)
+    W = C.load_text_weights(str(tmp_path), SHAPES["layers"], device="cpu")
+    for l in range(SHAPES["layers"]):
+        for key, suffix in C._LAYER_TENSORS:
+            n = f"model.language_model.layers.{l}.{suffix}"
+            if key in C._LINEARS:
+                q, sc = q8[n]
+                assert W[(l, key)].dtype.__str__() == "torch.int8"
+                assert np.array_equal(W[(l, key)].numpy(), q)
+                assert np.array_equal(W[(l, key + "_scale")].numpy(), sc)
+            else:
+                assert W[(l, key)].numpy().dtype == np.float16
+
+
+def test_int8_checkpoint_errors(tmp_path):
+    vals = _tensors(np.random.default_rng(9), True)
+    d1 = tmp_path / "noscale"
     d1.mkdir()
-    _write_checkpoint(str(d1), {k: v for k, v in vals.items() if k != drop}, 1)
+    _int8_checkpoint(str(d1), vals, skip_scale="model.language_model.layers.0.self_attn.k_proj.weight")
     with pytest.raises(C.CheckpointError, match="missing"):
         C.load_text_weights(str(d1), SHAPES["layers"], device="cpu")
-    d2 = tmp_path / "int8"
+    d2 = tmp_path / "mixed"
     d2.mkdir()
-    ts = {n: torch.from_numpy(v).to(torch.float16) for n, (v, _) in vals.items()}
-    ts[drop] = torch.zeros(vals[drop][0].shape, dtype=torch.int8)
-    save_file(ts, str(d2 / "model.safetensors"))
+    _int8_checkpoint(str(d2), vals, float_linear="model.language_model.layers.1.mlp.up_proj.weight")
     with pytest.raises(C.CheckpointError, match="int8"):
         C.load_text_weights(str(d2), SHAPES["layers"], device="cpu")

@@ -263,3 +263,57 @@ def test_decoder_from_checkpoint_equals_decoder_from_weights(gpu, tmp_path):
         runs.append((toks, np.stack(lgs)))
     assert runs[0][0] == runs[1][0]
     assert np.array_equal(runs[0][1], runs[1][1])
+
+
+PROJECTIONS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+def _quantize_rows(w):
+    """Symmetric per-row int8 of an f16 [out][in] matrix: (q, f32 scales)."""
+    import torch
+
+    s = (w.float().abs().amax(dim=1) / 127.0).clamp_min(1e-8)
+    q = torch.round(w.float() / s[:, None]).clamp(-128, 127).to(torch.int8)
+    return q.contiguous(), s.contiguous()
+
+
+@pytest.mark.parametrize("model,batch,blas", [("1.7B", 16, "0"), ("0.6B", 1, "0"), ("0.6B", 3, "1")])
+def test_int8_projections_equal_dequantized_f16(gpu, model, batch, blas, monkeypatch):
+    """Resident int8 projections (per-row f32 scale; the reference's int8
+    checkpoints, weights.rs:296-427) against the same decoder over f16
+    weights dequantized on the host as f16(q * s): the decode steps (int8
+    skinny GEMM that dequantizes in registers, or rocBLAS over a dequantized
+    copy when QASR_DECODER_BLAS=1) and the prefill (dequantized copy +
+    rocBLAS) must give identical tokens and logits, bitwise."""
+    import torch
+
+    from decoder_model import CFG_1P7B
+    from gpu_helpers import say
+
+    monkeypatch.setenv("QASR_DECODER_BLAS", blas)
+    cfg = dict(CFG_1P7B if model == "1.7B" else CFG_0P6B, layers=3, vocab=8192)
+    W = synth_weights(cfg, SEED_BASE + 980 + batch, device="cuda")
+    W8, Wdq = dict(W), dict(W)
+    for key in list(W):
+        if isinstance(key, tuple) and key[1] in PROJECTIONS:
+            q, s = _quantize_rows(W[key])
+            W8[key], W8[(key[0], key[1] + "_scale")] = q, s
+            Wdq[key] = (q.float() * s[:, None]).half()
+    del W
+    runs = []
+    for label, weights in (("int8", W8), ("f16", Wdq)):
+        say(f"{model} batch {batch} blas={blas}: decoder over {label} weights")
+        dec = _native(cfg, weights, batch, 1024, max_rows=64)
+        lg = torch.empty((batch, cfg["vocab"]), dtype=torch.float32, device="cuda")
+        toks, lgs = [], []
+        for i in range(batch):
+            toks.append(dec.prefill(_prompt(SEED_BASE + 990 + i, 70 + 9 * i, cfg["hs"]), 0,
+                                    slot=i, logits=lg[i]))
+        lgs.append(lg.cpu().numpy().copy())
+        for _ in range(5):
+            toks.extend(dec.step(logits=lg))
+            lgs.append(lg.cpu().numpy().copy())
+        dec.close()
+        runs.append((toks, np.stack(lgs)))
+    assert runs[0][0] == runs[1][0]
+    assert np.array_equal(runs[0][1], runs[1][1])
