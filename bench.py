@@ -264,6 +264,46 @@ def bench_text_decoder(model: str, lengths, steps: int, warmup: int, int8: bool 
             "weight_GBps": wbytes / (ms * 1e-3) / 1e9}
 
 
+def bench_serving(model: str, segments: int, width: int, max_new: int, seed: int = 21):
+    """A batch job through the slot scheduler (serving.decode_batch: prompts
+    prefilled together, longest first, all live slots stepped together, a
+    finished slot refilled at once) against the same job one segment at a
+    time (width 1).  Prompts of U[150, 450] rows (12-36 s of audio); random
+    weights never emit an EOS id, so every segment generates max_new tokens.
+    Wall-clock, host scheduling included."""
+    import numpy as np
+    import torch
+
+    import qasr_attn
+    import serving
+
+    dims = DECODERS[model]
+    W = decoder_weights(dims["hs"], dims["inter"])
+    dec = qasr_attn.TextDecoder(W, NQH, NKVH, HD, LAYERS, 1e-6, 16384, slots=1, max_rows=4096,
+                                cap=1024)
+    del W
+    rng = np.random.default_rng(seed)
+    lens = [int(x) for x in rng.integers(150, 450, size=segments)]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    plans = [torch.randn((n, dims["hs"]), device="cuda", generator=g).half() for n in lens]
+    out = {"model": model, "segments": segments, "max_new": max_new,
+           "prompt_rows": int(sum(lens))}
+    serving.decode_batch(dec, plans[:2], [4, 4], 2)  # warm-up: rocBLAS, allocator
+    for w in (width, 1):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        res = serving.decode_batch(dec, plans, [max_new] * segments, w)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        toks = sum(len(r.ids) for r in res)
+        out[f"width{w}"] = {"seconds": dt, "tokens": toks, "tokens_per_s": toks / dt}
+    dec.close()
+    torch.cuda.empty_cache()
+    out["speedup"] = out[f"width{width}"]["tokens_per_s"] / out["width1"]["tokens_per_s"]
+    return out
+
+
 def cpu_baseline(lengths, budget_s: float = 10.0):
     """Reference CPU path (C++ restatement of cpu_decoder.rs, oracle/) on config
     3: stage (a) + attention for each of the 16 slots, one layer at a time,
@@ -345,6 +385,7 @@ def main():
             "decoder1": lambda: bench_text_decoder("0.6B", [511], K, W),
             "decoder16_int8": lambda: bench_text_decoder("1.7B", lens3, K, W, int8=True),
             "decoder1_int8": lambda: bench_text_decoder("0.6B", [511], K, W, int8=True),
+            "serving": lambda: bench_serving("1.7B", 32, 16, 48),
         }
         log(json.dumps({only: runs[only]()}))
         return
@@ -371,6 +412,8 @@ def main():
                                                                      W, int8=True)
         extra["text_decoder_0p6b_1slot_int8"] = bench_text_decoder("0.6B", [511], max(5, K // 5),
                                                                    W, int8=True)
+        log("[bench] batch job through the slot scheduler (32 segments, width 16 vs 1)")
+        extra["serving_1p7b_32seg_width16"] = bench_serving("1.7B", 32, 16, 48)
         for k, v in extra.items():
             log(f"[bench] {k}: {json.dumps(v)}")
 

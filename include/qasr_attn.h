@@ -242,6 +242,18 @@ int qasr_decoder_prefill(qasr_decoder* dec, qasr_kv* kv, int slot, int kv_start,
                          const void* hidden_dev, int32_t* next_dev, float* logits_dev,
                          void* stream);
 
+/* Prefill of several segments at once (prefill_batch / prefill_multi,
+ * decoder.rs:3599-3700): segment i writes segs[i].rows rows into slot
+ * segs[i].slot at positions segs[i].pos0 ..; the hidden rows of all segments
+ * are concatenated in segment order ([sum rows][hs] f16, device).  Every
+ * projection runs once over all rows (row-independent), attention per
+ * segment; next_dev[i] receives the argmax token after segment i's last row,
+ * logits_dev (optional) its f32 logits [nseg][vocab].  Slots must be
+ * distinct, every segment at least one row, the rows together <= max_rows. */
+int qasr_decoder_prefill_batch(qasr_decoder* dec, qasr_kv* kv, const qasr_segment* segs,
+                               int nseg, const void* hidden_dev, int32_t* next_dev,
+                               float* logits_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

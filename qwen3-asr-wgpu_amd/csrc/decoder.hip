@@ -45,6 +45,7 @@ constexpr int kArgmaxThreads = 256;
 constexpr int kArgmaxChunks = 32;  // workgroups per logits row in the first argmax pass
 constexpr int kHeadRows = 128;     // rows per logits GEMM + argmax (bounds the logits scratch)
 constexpr size_t kBlasWorkspace = size_t(64) << 20;
+constexpr int kMaxPrefillSegs = 64;  // segments of one batched prefill call
 
 // ---- block reductions (wave64 shuffles, then one LDS pass) ---------------
 __device__ __forceinline__ float wave_sum(float v) {
@@ -84,6 +85,20 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const f16* __restrict__
     const uint4* src = (const uint4*)(embed + (int64_t)t * hs);
     uint4* dst = (uint4*)(x + (int64_t)r * hs);
     for (int c = threadIdx.x; c < hs / 8; c += blockDim.x) dst[c] = src[c];
+}
+
+// The last row of every segment of a batched prefill, packed: dst[r] =
+// src[rows.idx[r]] (rows of hs f16; hs a multiple of 8).
+struct RowList {
+    int32_t idx[kMaxPrefillSegs];
+};
+
+__global__ __launch_bounds__(256) void gather_rows_kernel(const f16* __restrict__ src, int hs,
+                                                          RowList rows, f16* __restrict__ dst) {
+    const int r = blockIdx.x;
+    const uint4* from = (const uint4*)(src + (int64_t)rows.idx[r] * hs);
+    uint4* to = (uint4*)(dst + (int64_t)r * hs);
+    for (int c = threadIdx.x; c < hs / 8; c += blockDim.x) to[c] = from[c];
 }
 
 // out[r] = f16((x * inv) * w) with inv = 1 / sqrt(sum(x^2) / n + eps), f32
@@ -613,6 +628,90 @@ int bind_stream(qasr_decoder* d, void* stream) {
     return QASR_OK;
 }
 
+// Prefill of nseg segments whose hidden rows are concatenated in segment
+// order: norms and projections once over all rows, stage (a) in one launch,
+// attention per segment, then the head over each segment's last row.  Every
+// argument is checked before the first launch.
+int prefill_segments(qasr_decoder* dec, qasr_kv* kv, const qasr_segment* segs, int nseg,
+                     const void* hidden_dev, int32_t* next_dev, float* logits_dev,
+                     void* stream) {
+    if (!dec || !kv) return fail(QASR_EINVAL, "null decoder or KV pool");
+    if (kv->ctx != dec->ctx) return fail(QASR_EINVAL, "KV pool belongs to another context");
+    if (!hidden_dev || !next_dev) return fail(QASR_EINVAL, "null argument");
+    if (nseg > kMaxPrefillSegs)
+        return fail(QASR_EINVAL, "%d segments in one prefill call, at most %d", nseg,
+                    kMaxPrefillSegs);
+    const qasr_ctx* ctx = dec->ctx;
+    if (!ctx->cos) return fail(QASR_ESTATE, "RoPE tables not set (qasr_set_rope_tables)");
+    int64_t total = 0;
+    for (int i = 0; i < nseg; ++i) {
+        const qasr_segment& g = segs[i];
+        if (g.slot < 0 || g.slot >= kv->slots)
+            return fail(QASR_EINVAL, "segment %d: slot %d outside [0, %d)", i, g.slot, kv->slots);
+        if (g.pos0 < 0 || g.rows <= 0)
+            return fail(QASR_EINVAL, "segment %d: kv_start %d / rows %d", i, g.pos0, g.rows);
+        for (int j = 0; j < i; ++j)
+            if (segs[j].slot == g.slot)
+                return fail(QASR_EINVAL, "segments %d and %d share slot %d", j, i, g.slot);
+        const int64_t end = (int64_t)g.pos0 + g.rows;
+        if (end > ctx->cfg.max_seq)
+            return fail(QASR_ERANGE, "prefill needs %lld positions, max_seq is %d",
+                        (long long)end, ctx->cfg.max_seq);
+        if (end > kv->cap)
+            return fail(QASR_ERANGE, "prefill needs %lld positions, KV capacity is %d",
+                        (long long)end, kv->cap);
+        if (end > ctx->rope_rows)
+            return fail(QASR_ERANGE, "prefill needs %lld positions, the RoPE tables hold %d",
+                        (long long)end, ctx->rope_rows);
+        total += g.rows;
+    }
+    if (total > dec->cfg.max_rows)
+        return fail(QASR_EINVAL, "prefill rows %lld exceed max_rows %d", (long long)total,
+                    dec->cfg.max_rows);
+    DeviceScope ds(ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    const hipStream_t st = (hipStream_t)stream;
+    int rc = bind_stream(dec, stream);
+    if (rc) return rc;
+    const qasr_attn_cfg& a = ctx->cfg;
+    const int hs = dec->cfg.hidden_size, rows = (int)total;
+    const int qdim = a.num_attention_heads * a.head_dim;
+    const int qkvdim = (a.num_attention_heads + 2 * a.num_key_value_heads) * a.head_dim;
+    HIP_TRY(hipMemcpyAsync(dec->x, hidden_dev, (size_t)rows * hs * 2, hipMemcpyDeviceToDevice, st),
+            "prefill input copy");
+    for (int l = 0; l < a.num_hidden_layers; ++l) {
+        const qasr_layer_weights& L = dec->layers[l];
+        rc = launch_rms_norm(dec->x, hs, L.input_norm, dec->n, rows, hs, a.rms_norm_eps, st);
+        if (rc) return rc;
+        rc = gemm_f16(dec, rows, qkvdim, hs, L.qkv_proj, dec->n, dec->qkv, false, L.qkv_scale);
+        if (rc) return rc;
+        rc = qasr_qk_norm_rope_append(dec->ctx, kv, l, segs, nseg, dec->qkv, L.q_norm, L.k_norm,
+                                      dec->qw, stream);
+        if (rc) return rc;
+        int64_t r0 = 0;
+        for (int i = 0; i < nseg; ++i) {
+            rc = qasr_prefill_attn(dec->ctx, kv, l, segs[i].slot, segs[i].pos0, segs[i].rows,
+                                   dec->qw + r0 * qdim, dec->attn + r0 * qdim, stream);
+            if (rc) return rc;
+            r0 += segs[i].rows;
+        }
+        rc = layer_tail(dec, L, rows, st);
+        if (rc) return rc;
+    }
+    if (nseg == 1) return head(dec, dec->x + (int64_t)(rows - 1) * hs, 1, next_dev, logits_dev, st);
+    // Last rows into the gate|up scratch ([max_rows][2 inter], free after the
+    // last layer; hs <= 2 inter is checked at creation), then the head.
+    RowList last{};
+    int64_t r0 = 0;
+    for (int i = 0; i < nseg; ++i) {
+        r0 += segs[i].rows;
+        last.idx[i] = (int32_t)(r0 - 1);
+    }
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(nseg), dim3(256), 0, st, dec->x, hs, last, dec->gu);
+    HIP_TRY(hipGetLastError(), "row gather launch");
+    return head(dec, dec->gu, nseg, next_dev, logits_dev, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -629,6 +728,8 @@ int qasr_decoder_create(qasr_ctx* ctx, const qasr_decoder_cfg* cfg, const void* 
     if (hs <= 0 || hs % 8 || inter <= 0 || inter % 8 || vocab <= 0 || cfg->max_rows <= 0)
         return fail(QASR_EINVAL, "hidden %d / intermediate %d must be positive multiples of 8, "
                     "vocab %d and max_rows %d positive", hs, inter, vocab, cfg->max_rows);
+    if (hs > 2 * inter)
+        return fail(QASR_EINVAL, "hidden %d above 2 x intermediate %d", hs, inter);
     if (cfg->max_rows > 4096)
         return fail(QASR_EINVAL, "max_rows %d above the prefill limit of 4096 rows per call",
                     cfg->max_rows);
@@ -749,33 +850,16 @@ int qasr_decoder_step(qasr_decoder* dec, qasr_kv* kv, int batch, const int32_t* 
 int qasr_decoder_prefill(qasr_decoder* dec, qasr_kv* kv, int slot, int kv_start, int s,
                          const void* hidden_dev, int32_t* next_dev, float* logits_dev,
                          void* stream) {
-    if (!dec || !kv) return fail(QASR_EINVAL, "null decoder or KV pool");
-    if (s <= 0 || s > dec->cfg.max_rows)
-        return fail(QASR_EINVAL, "prefill rows %d outside [1, max_rows %d]", s, dec->cfg.max_rows);
-    if (!hidden_dev || !next_dev) return fail(QASR_EINVAL, "null argument");
-    DeviceScope ds(dec->ctx->device);
-    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
-    const hipStream_t st = (hipStream_t)stream;
-    int rc = bind_stream(dec, stream);
-    if (rc) return rc;
-    const qasr_attn_cfg& a = dec->ctx->cfg;
-    const int hs = dec->cfg.hidden_size;
-    const int qkvdim = (a.num_attention_heads + 2 * a.num_key_value_heads) * a.head_dim;
-    HIP_TRY(hipMemcpyAsync(dec->x, hidden_dev, (size_t)s * hs * 2, hipMemcpyDeviceToDevice, st),
-            "prefill input copy");
-    for (int l = 0; l < a.num_hidden_layers; ++l) {
-        const qasr_layer_weights& L = dec->layers[l];
-        rc = launch_rms_norm(dec->x, hs, L.input_norm, dec->n, s, hs, a.rms_norm_eps, st);
-        if (rc) return rc;
-        rc = gemm_f16(dec, s, qkvdim, hs, L.qkv_proj, dec->n, dec->qkv, false, L.qkv_scale);
-        if (rc) return rc;
-        rc = qasr_prefill_layer(dec->ctx, kv, l, slot, kv_start, s, dec->qkv, L.q_norm, L.k_norm,
-                                dec->qw, dec->attn, stream);
-        if (rc) return rc;
-        rc = layer_tail(dec, L, s, st);
-        if (rc) return rc;
-    }
-    return head(dec, dec->x + (int64_t)(s - 1) * hs, 1, next_dev, logits_dev, st);
+    const qasr_segment seg{slot, kv_start, s};
+    return prefill_segments(dec, kv, &seg, 1, hidden_dev, next_dev, logits_dev, stream);
+}
+
+int qasr_decoder_prefill_batch(qasr_decoder* dec, qasr_kv* kv, const qasr_segment* segs,
+                               int nseg, const void* hidden_dev, int32_t* next_dev,
+                               float* logits_dev, void* stream) {
+    if (nseg < 0 || (nseg > 0 && !segs)) return fail(QASR_EINVAL, "bad segment list");
+    if (nseg == 0) return QASR_OK;
+    return prefill_segments(dec, kv, segs, nseg, hidden_dev, next_dev, logits_dev, stream);
 }
 
 }  // extern "C"

@@ -36,7 +36,9 @@ ABI_SYMBOLS = (
     "qasr_kv_get_info", "qasr_kv_ensure_capacity", "qasr_qk_norm_rope_append",
     "qasr_decode_attn", "qasr_decode_step", "qasr_prefill_attn", "qasr_prefill_layer",
     "qasr_decoder_create", "qasr_decoder_destroy", "qasr_decoder_step", "qasr_decoder_prefill",
+    "qasr_decoder_prefill_batch",
 )
+MAX_PREFILL_SEGMENTS = 64  # segments per qasr_decoder_prefill_batch call
 
 
 class QasrError(RuntimeError):
@@ -137,6 +139,8 @@ def load(path: str = LIB_PATH):
     L.qasr_decoder_step.argtypes = [_vp, _vp, ctypes.c_int, _i32p, _i32p, _vp, _vp, _vp, _vp]
     L.qasr_decoder_prefill.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp,
                                        _vp, _vp, _vp]
+    L.qasr_decoder_prefill_batch.argtypes = [_vp, _vp, ctypes.POINTER(Segment), ctypes.c_int, _vp,
+                                             _vp, _vp, _vp]
     _lib = L
     return L
 
@@ -478,6 +482,24 @@ class TextDecoder:
     def set_rope_tables(self, cos_u16, sin_u16):
         self.ctx.set_rope_tables(cos_u16, sin_u16)
 
+    @property
+    def slots(self) -> int:
+        return len(self.pos)
+
+    def reset_pool(self, slots: int, cap: int):
+        """A fresh KV pool of `slots` slots with room for `cap` positions each
+        (the reference's fork_capped per slot, decoder.rs:2453-2457); every
+        slot starts empty."""
+        import torch
+
+        cap = min(max(cap, 1), self.max_seq)
+        self.kv.close()
+        self.kv = KVPool(self.ctx, slots, cap)
+        self.pos = [0] * slots
+        self.last = [0] * slots
+        self._tok = torch.zeros(max(slots, 1), dtype=torch.int32, device="cuda")
+        self._next = torch.zeros(max(slots, 1), dtype=torch.int32, device="cuda")
+
     def ensure_capacity(self, need: int) -> int:
         """Grow-only, KV_STEP granular; keeps every row already written."""
         return self.kv.ensure_capacity(need, max(self.pos))
@@ -503,6 +525,69 @@ class TextDecoder:
         self.pos[slot] = kv_start + s
         self.last[slot] = tok
         return tok
+
+    def prefill_batch(self, items, logits=None):
+        """Prefill several slots at once (prefill_batch, decoder.rs:3599-3637):
+        `items` is a sequence of (slot, hidden) or (slot, hidden, kv_start),
+        hidden a [s][hs] f16 CUDA tensor.  The projections of segments that fit
+        one call together (max_rows rows, 64 segments) run once over all their
+        rows; a segment longer than max_rows is prefilled alone in chunks.
+        Returns the greedy token after each segment (and fills row i of
+        `logits`, [len(items)][vocab] f32, if given)."""
+        items = [(int(it[0]), it[1], int(it[2]) if len(it) > 2 else 0) for it in items]
+        if len({slot for slot, _, _ in items}) != len(items):
+            raise QasrError(QASR_EINVAL, "prefill_batch: two segments share a slot")
+        for slot, hidden, start in items:
+            if start + int(hidden.shape[0]) > self.max_seq:
+                raise QasrError(QASR_ERANGE, f"prefill needs {start + int(hidden.shape[0])} "
+                                             f"positions, max_seq is {self.max_seq}")
+        if not items:
+            return []
+        self.ensure_capacity(max(start + int(h.shape[0]) for _, h, start in items))
+        toks = [0] * len(items)
+        group = []
+
+        def flush():
+            if not group:
+                return
+            idx = [i for i, _ in group]
+            rows = [r for _, r in group]
+            hidden = self.t.cat([items[i][1] for i in idx]).contiguous()
+            segs = (Segment * len(idx))(*[Segment(items[i][0], items[i][2], r)
+                                          for i, r in zip(idx, rows)])
+            nxt = self.t.zeros(len(idx), dtype=self.t.int32, device="cuda")
+            lg, lg_rows = None, None
+            if logits is not None:
+                lg_rows = self.t.empty((len(idx), self.vocab), dtype=self.t.float32, device="cuda")
+                lg = _dev(lg_rows, "logits", self.t.float32)
+            _check(load().qasr_decoder_prefill_batch(self.handle, self.kv.handle, segs, len(idx),
+                                                     _dev(hidden, "hidden"),
+                                                     _dev(nxt, "next", self.t.int32), lg,
+                                                     _stream(None)))
+            got = nxt.tolist()
+            for k, i in enumerate(idx):
+                toks[i] = got[k]
+                if lg_rows is not None:
+                    logits[i].copy_(lg_rows[k])
+            group.clear()
+
+        used = 0
+        for i, (slot, hidden, start) in enumerate(items):
+            s = int(hidden.shape[0])
+            if s > self.max_rows:
+                toks[i] = self.prefill(hidden, start, slot=slot,
+                                       logits=logits[i] if logits is not None else None)
+                continue
+            if used + s > self.max_rows or len(group) == MAX_PREFILL_SEGMENTS:
+                flush()
+                used = 0
+            group.append((i, s))
+            used += s
+        flush()
+        for i, (slot, hidden, start) in enumerate(items):
+            self.pos[slot] = start + int(hidden.shape[0])
+            self.last[slot] = toks[i]
+        return toks
 
     def step_tokens(self, slots: Sequence[int], pos: Sequence[int], tokens_dev, next_dev,
                     logits=None, stream=None):

@@ -1,0 +1,194 @@
+"""Batched serving on the GPU: qasr_decoder_prefill_batch (prefill_batch /
+prefill_multi, decoder.rs:3599-3700) and the slot scheduler (serving.py,
+inference.rs:707-764, 1944-2227) against this library's single-sequence
+path, on seeded random weights of the 0.6B decoder shape (3 layers).
+
+With at most 16 rows a projection runs the skinny GEMM, whose rows are
+independent, and a context of a few dozen keys is one decode chunk whatever
+the batch holds: there, batched and single paths must agree bitwise.  Longer
+prompts go through rocBLAS with a different row count and the decode plan
+depends on the batch, so there logits must agree to rounding and a greedy
+stream may part from the single path's only at a near-tie."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from decoder_model import CFG_0P6B, synth_weights
+from workloads import SEED_BASE
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(CFG_0P6B, layers=3, vocab=4096)
+
+
+def _prompt(seed, rows):
+    import torch
+
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return torch.randn((rows, CFG["hs"]), device="cuda", generator=g).half()
+
+
+def _decoder(W, slots, max_rows=512, cap=1024):
+    import qasr_attn
+
+    c = CFG
+    return qasr_attn.TextDecoder(W, c["nqh"], c["nkvh"], c["hd"], c["layers"], c["eps"],
+                                 c["max_seq"], slots=slots, max_rows=max_rows, cap=cap)
+
+
+@pytest.fixture(scope="module")
+def weights(gpu):
+    return synth_weights(CFG, SEED_BASE + 1100, device="cuda")
+
+
+def _prefill_both(W, lens, seed):
+    import torch
+
+    from gpu_helpers import say
+
+    hidden = [_prompt(seed + i, n) for i, n in enumerate(lens)]
+    n = len(lens)
+    say(f"prefill_batch of {n} segments, rows {lens}")
+    a = _decoder(W, n)
+    lg_a = torch.empty((n, CFG["vocab"]), dtype=torch.float32, device="cuda")
+    tok_a = a.prefill_batch([(i, h) for i, h in enumerate(hidden)], logits=lg_a)
+    b = _decoder(W, n)
+    lg_b = torch.empty_like(lg_a)
+    tok_b = [b.prefill(h, 0, slot=i, logits=lg_b[i]) for i, h in enumerate(hidden)]
+    torch.cuda.synchronize()
+    return a, b, tok_a, tok_b, lg_a.cpu().numpy(), lg_b.cpu().numpy()
+
+
+def test_prefill_batch_short_segments_bitwise(weights):
+    """16 rows in all: the same bits as one prefill per slot, logits and KV."""
+    a, b, tok_a, tok_b, lg_a, lg_b = _prefill_both(weights, [2, 5, 3, 6], SEED_BASE + 1110)
+    assert tok_a == tok_b
+    assert np.array_equal(lg_a, lg_b)
+    ka, kb = a.kv.tensor(), b.kv.tensor()
+    for i, n in enumerate([2, 5, 3, 6]):
+        assert ka[i, :, :, :, :n].equal(kb[i, :, :, :, :n]), f"slot {i} KV differs"
+    assert a.pos == b.pos and a.last == b.last
+    # a step of all four slots after either prefill is the same step
+    assert a.step() == b.step()
+    a.close()
+    b.close()
+
+
+def test_prefill_batch_long_segments_within_rounding(weights):
+    """474 rows (rocBLAS projections): logits within rounding of the single
+    prefills, equal tokens wherever the top-2 margin is clear."""
+    lens = [100, 37, 260, 77]
+    a, b, tok_a, tok_b, lg_a, lg_b = _prefill_both(weights, lens, SEED_BASE + 1120)
+    spread = float(np.std(lg_b))
+    diff = float(np.max(np.abs(lg_a - lg_b)))
+    assert diff <= 2e-2 * spread, (diff, spread)
+    for i in range(len(lens)):
+        top = np.partition(lg_b[i], -2)[-2:]
+        if top[1] - top[0] > 2 * diff:
+            assert tok_a[i] == tok_b[i]
+    ka, kb = a.kv.tensor(), b.kv.tensor()
+    for i, n in enumerate(lens):
+        d = (ka[i, :, :, :, :n].float() - kb[i, :, :, :, :n].float()).abs().max().item()
+        assert d <= 2e-2, f"slot {i}: KV differs by {d}"
+    a.close()
+    b.close()
+
+
+def test_prefill_batch_rejects_bad_segments(weights):
+    import qasr_attn
+
+    dec = _decoder(weights, 2, max_rows=64)
+    h = _prompt(SEED_BASE + 1130, 40)
+    with pytest.raises(qasr_attn.QasrError, match="share a slot"):
+        dec.prefill_batch([(0, h), (0, h)])
+    # 80 rows over max_rows 64: split into two calls, same result as separate
+    toks = dec.prefill_batch([(0, h), (1, h)])
+    assert toks[0] == toks[1]
+    dec.close()
+
+
+def _single_with_margins(dec, plans, max_news, eos):
+    """The single path (serving.generate) with the top-2 margin of every token
+    and the spread (standard deviation) of each prompt's first logits."""
+    import torch
+
+    import serving
+
+    out = []
+    for h, m in zip(plans, max_news):
+        dec.reset_pool(1, serving.kv_cap(int(h.shape[0]), m))
+        lg = torch.empty((1, CFG["vocab"]), dtype=torch.float32, device="cuda")
+        first = dec.prefill(h, 0, slot=0, logits=lg[0])
+        spread = float(lg[0].std())
+        ids, margins = [], []
+
+        def margin():
+            t = torch.topk(lg[0], 2).values
+            return float(t[0] - t[1])
+
+        if first not in eos:
+            ids.append(first)
+            margins.append(margin())
+            for _ in range(1, m):
+                tok = dec.step([0], logits=lg)[0]
+                margins.append(margin())
+                if tok in eos:
+                    break
+                ids.append(tok)
+        out.append((ids, margins, spread))
+    return out
+
+
+def _run_both(weights, lens, max_news, width, seed, eos=()):
+    import serving
+    from gpu_helpers import say
+
+    plans = [_prompt(seed + i, n) for i, n in enumerate(lens)]
+    dec = _decoder(weights, 1)
+    say(f"single path over {len(lens)} segments")
+    single = _single_with_margins(dec, plans, max_news, eos)
+    plain = serving.decode_batch(dec, plans, max_news, 1, eos=eos)
+    say(f"scheduler at width {width}")
+    batched = serving.decode_batch(dec, plans, max_news, width, eos=eos)
+    dec.close()
+    return single, plain, batched
+
+
+def test_scheduler_short_prompts_bitwise(weights):
+    """Prompts of 2-6 rows (the first admission is 16 rows): every segment's
+    tokens from width 3 equal the single path's, including EOS stops."""
+    lens = [4, 5, 6, 3, 2, 5, 4, 4]
+    max_news = [9, 12, 7, 10, 12, 8, 11, 6]
+    single, plain, _ = _run_both(weights, lens, max_news, 3, SEED_BASE + 1140)
+    # an EOS id that occurs in some streams, so some segments stop early
+    eos = (single[0][0][3], single[5][0][2])
+    single, plain, batched = _run_both(weights, lens, max_news, 3, SEED_BASE + 1140, eos=eos)
+    stopped_early = 0
+    for g in range(len(lens)):
+        assert plain[g].ids == single[g][0], g
+        assert batched[g].ids == single[g][0], g
+        stopped_early += len(batched[g].ids) < max_news[g]
+    assert stopped_early >= 2
+
+
+def test_scheduler_long_prompts_part_only_at_near_ties(weights):
+    """Prompts of 40-300 rows at width 4 (rocBLAS prefill, batch-dependent
+    decode plans): a stream may part from the single path's only where the
+    single path's top-2 margin is within rounding (2% of the logit spread)."""
+    rng = np.random.default_rng(11)
+    lens = [int(x) for x in rng.integers(40, 300, size=10)]
+    max_news = [int(x) for x in rng.integers(8, 24, size=10)]
+    single, plain, batched = _run_both(weights, lens, max_news, 4, SEED_BASE + 1150)
+    same = 0
+    for g in range(len(lens)):
+        ids, margins, spread = single[g]
+        assert plain[g].ids == ids
+        got = batched[g].ids
+        if got == ids:
+            same += 1
+            continue
+        j = next(k for k in range(min(len(got), len(ids))) if got[k] != ids[k])
+        assert margins[j] < 2e-2 * spread, f"segment {g} parts at token {j}, margin {margins[j]}"
+    assert same >= len(lens) // 2
