@@ -142,6 +142,21 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const f16* __res
 
 // h[r][i] = f16(g / (1 + exp(-g)) * u), g|u = gu[r][i], gu[r][inter + i]
 // (cpu_decoder.rs:442-448).  8 elements per thread.
+// f16(x) of an f32 value that is first rounded to f32: the reference's
+// f16::from_f32 of an f32 result.  Without the register barrier the compiler
+// folds the product or fma producing x into v_fma_mixlo_f16, which rounds the
+// exact result once, straight to f16, and differs from f16(f32(.)) on about
+// 2 in 10^5 products (measured on gfx950).
+__device__ __forceinline__ f16 f16_of_f32(float x) {
+    asm volatile("" : "+v"(x));
+    return (f16)x;
+}
+
+// SiLU(g) * u in f32 (silu, cpu_decoder.rs): g / (1 + e^-g), then times u.
+__device__ __forceinline__ float silu_times(float g, float u) {
+    return g / (1.0f + expf(-g)) * u;
+}
+
 __global__ __launch_bounds__(256) void silu_mul_kernel(const f16* __restrict__ gu, int inter,
                                                        int rows, f16* __restrict__ h) {
     const int per_row = inter / 8;
@@ -154,9 +169,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const f16* __restrict__ g
     u.u = ((const uint4*)(grow + inter))[c];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const float gf = (float)g.e[e];
-        const float silu = gf / (1.0f + expf(-gf));
-        o.e[e] = (f16)(silu * (float)u.e[e]);
+        o.e[e] = f16_of_f32(silu_times((float)g.e[e], (float)u.e[e]));
     }
     ((uint4*)(h + (int64_t)r * inter))[c] = o.u;
 }
@@ -227,8 +240,14 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
 // ~512 workgroups) each workgroup publishes its 16 x 16 partial with
 // device-coherent stores and the last of the tile's workgroups to arrive
 // (ticket) sums the partials in group order: deterministic, no second launch.
-// The result is rounded once -- with the residual y added in f32 first when
-// ACC, or kept f32 when OUT_F32 (logits).
+// The result is rounded once -- with the residual y added in f32 first
+// (kOutAcc), or kept f32 (kOutF32, logits).  kOutGlu is gate|up followed by
+// SiLU(gate) * up: tile t takes gate rows 8t..8t+7 and up rows
+// N/2+8t..N/2+8t+7 (lanes r and r+8 hold gate and up of one column), rounds
+// both to f16 like the projection, and writes h = f16(SiLU(g) u) to column
+// 8t + r of Y[m][N/2] -- the same values silu_mul_kernel makes from the
+// gate|up rows.
+constexpr int kOutF16 = 0, kOutAcc = 1, kOutF32 = 2, kOutGlu = 3;
 constexpr int kSkinnyRows = 16;
 constexpr int kSkinnyUnroll = 4;                     // k-steps per stage (8 measured no faster)
 constexpr int kSkinnyPair = 2 * 32 * kSkinnyUnroll;  // K per wave: a multiple (even stage count)
@@ -261,7 +280,7 @@ __device__ __forceinline__ qasr::half8v dequant8(uint32_t lo, uint32_t hi, float
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float u = (float)((d[w] >> (8 * j)) & 0xffu);
-            h[4 * w + j] = (f16)fmaf(u, s, s128);
+            h[4 * w + j] = f16_of_f32(fmaf(u, s, s128));
         }
     return h;
 }
@@ -289,7 +308,7 @@ struct SkinnyArgs {
     uint32_t* counters;  // split tickets
 };
 
-template <int KS, int U, bool W8, bool ACC, bool OUT_F32>
+template <int KS, int U, bool W8, int OUT>
 __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
     __shared__ qasr::float4v s_red[KS][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -299,15 +318,23 @@ __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
     const int kw = K / (KS * groups);
     const int kbeg = (blockIdx.y * KS + wave) * kw;
     constexpr int wbytes = W8 ? 1 : 2;  // bytes per weight
+    // This lane's weight row: n0 + r, or for kOutGlu gate row 8t + r (r < 8)
+    // and up row N/2 + 8t + r - 8, as an offset rr from the resource's first
+    // row w0.
+    constexpr bool kGlu = OUT == kOutGlu;
+    const int w0 = kGlu ? 8 * tile : n0;
+    const int rr = kGlu ? (r < 8 ? r : N / 2 + r - 8) : r;
+    const int64_t wrows = kGlu ? (int64_t)(N / 2 + 8) : 16;
     const __amdgpu_buffer_rsrc_t wres =
-        rsrc((const char*)p.W + (int64_t)n0 * K * wbytes, (int64_t)16 * K * wbytes);
+        rsrc((const char*)p.W + (int64_t)w0 * K * wbytes, wrows * K * wbytes);
     float ws = 0.0f, ws128 = 0.0f;  // W8: this lane's row's scale, and -128 x it
     if constexpr (W8) {
-        ws = p.scale[n0 + r];
+        ws = p.scale[w0 + rr];
         ws128 = -128.0f * ws;
     }
     const __amdgpu_buffer_rsrc_t xres = rsrc(p.X, (int64_t)M * K * 2);
-    const int off = r * K * 2 + g * 16;  // bytes: row r, k 8g (W and X rows are both K long)
+    const int woff = rr * K * 2 + g * 16;  // bytes: weight row rr, k 8g
+    const int xoff = r * K * 2 + g * 16;   // bytes: activation row r, k 8g
 
     // Stages of U k-steps, double buffered: stage st+1's loads
     // are issued before stage st's MFMAs.
@@ -323,11 +350,11 @@ __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
             const int kk = k0 + 32 * u;
             if constexpr (W8) {
                 S.q[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                       wres, r * K + g * 8 + kk, 0, 0));
+                                                       wres, rr * K + g * 8 + kk, 0, 0));
             } else {
-                S.b[u] = load8(wres, off + kk * 2);
+                S.b[u] = load8(wres, woff + kk * 2);
             }
-            S.x[u] = load8(xres, off + kk * 2);
+            S.x[u] = load8(xres, xoff + kk * 2);
         }
     };
     qasr::float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -393,13 +420,22 @@ __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int m = 4 * g + i;
+        if constexpr (kGlu) {
+            // Lanes r and r^8 (same rows) exchange gate and up; every lane of
+            // the wave takes part in the shuffle.
+            const float v = (float)(f16)sum[i];
+            const float up = __shfl_xor(v, 8);
+            if (r < 8 && m < M)
+                ((f16*)p.Y)[(int64_t)m * (N / 2) + 8 * tile + r] = f16_of_f32(silu_times(v, up));
+            continue;
+        }
         if (m >= M) continue;
         const int64_t idx = (int64_t)m * N + n;
-        if constexpr (OUT_F32) {
+        if constexpr (OUT == kOutF32) {
             ((float*)p.Y)[idx] = sum[i];
         } else {
             f16* y = (f16*)p.Y;
-            y[idx] = (f16)(ACC ? (float)y[idx] + sum[i] : sum[i]);
+            y[idx] = (f16)(OUT == kOutAcc ? (float)y[idx] + sum[i] : sum[i]);
         }
     }
 }
@@ -418,6 +454,7 @@ struct qasr_decoder {
     void* blas_ws = nullptr;
     hipStream_t stream = nullptr;  // of the call in progress
     bool force_blas = false;       // QASR_DECODER_BLAS=1: every projection through rocBLAS
+    bool fuse = true;              // QASR_DECODER_FUSE=0: no fused epilogues (same results)
     // activations, max_rows rows each
     f16* x = nullptr;     // residual stream [rows][hs]
     f16* n = nullptr;     // normed rows [rows][hs]
@@ -476,21 +513,21 @@ SkinnyShape skinny_shape(qasr_decoder* d, int rows, int n_out, int k) {
     return SkinnyShape{};
 }
 
-template <bool W8, bool ACC, bool OUT_F32>
+template <bool W8, int OUT>
 int launch_skinny_w(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
     const dim3 grid(a.N / 16, sh.groups);
     constexpr int U = kSkinnyUnroll;
     switch (sh.ks) {
         case 4:
-            hipLaunchKernelGGL((skinny_gemm_kernel<4, U, W8, ACC, OUT_F32>), grid, dim3(4 * 64), 0,
+            hipLaunchKernelGGL((skinny_gemm_kernel<4, U, W8, OUT>), grid, dim3(4 * 64), 0,
                                d->stream, a);
             break;
         case 8:
-            hipLaunchKernelGGL((skinny_gemm_kernel<8, U, W8, ACC, OUT_F32>), grid, dim3(8 * 64), 0,
+            hipLaunchKernelGGL((skinny_gemm_kernel<8, U, W8, OUT>), grid, dim3(8 * 64), 0,
                                d->stream, a);
             break;
         case 12:
-            hipLaunchKernelGGL((skinny_gemm_kernel<12, U, W8, ACC, OUT_F32>), grid, dim3(12 * 64),
+            hipLaunchKernelGGL((skinny_gemm_kernel<12, U, W8, OUT>), grid, dim3(12 * 64),
                                0, d->stream, a);
             break;
         default:
@@ -500,10 +537,9 @@ int launch_skinny_w(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
     return QASR_OK;
 }
 
-template <bool ACC, bool OUT_F32>
+template <int OUT>
 int launch_skinny(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
-    return a.scale ? launch_skinny_w<true, ACC, OUT_F32>(d, sh, a)
-                   : launch_skinny_w<false, ACC, OUT_F32>(d, sh, a);
+    return a.scale ? launch_skinny_w<true, OUT>(d, sh, a) : launch_skinny_w<false, OUT>(d, sh, a);
 }
 
 SkinnyArgs skinny_args(qasr_decoder* d, SkinnyShape sh, int rows, int n_out, int k, const void* W,
@@ -530,8 +566,7 @@ int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f
     const SkinnyShape sh = skinny_shape(d, rows, n_out, k);
     if (sh.ks) {
         const SkinnyArgs a = skinny_args(d, sh, rows, n_out, k, W, x, y, scale);
-        return accumulate ? launch_skinny<true, false>(d, sh, a)
-                          : launch_skinny<false, false>(d, sh, a);
+        return accumulate ? launch_skinny<kOutAcc>(d, sh, a) : launch_skinny<kOutF16>(d, sh, a);
     }
     if (scale) {
         if (!d->wdq || (int64_t)n_out * k > d->wdq_elems)
@@ -552,12 +587,26 @@ int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f
     return QASR_OK;
 }
 
+// h[rows][inter] = SiLU(x . Wg^T) * (x . Wu^T) for the fused gate|up W in
+// one skinny launch (kOutGlu); *fused = false (nothing launched) when the
+// shape takes the library GEMM instead.
+int glu_skinny(qasr_decoder* d, int rows, int inter, int k, const void* W, const f16* x, f16* h,
+               const float* scale, bool* fused) {
+    *fused = false;
+    if (!d->fuse) return QASR_OK;
+    const SkinnyShape sh = skinny_shape(d, rows, 2 * inter, k);
+    const int64_t span = (int64_t)(inter + 8) * k * (scale ? 1 : 2);
+    if (!sh.ks || span >= (int64_t(1) << 31)) return QASR_OK;
+    *fused = true;
+    return launch_skinny<kOutGlu>(d, sh, skinny_args(d, sh, rows, 2 * inter, k, W, x, h, scale));
+}
+
 // logits[rows][vocab] (f32) = n[rows][hs] . E[vocab][hs]^T.
 int gemm_logits(qasr_decoder* d, int rows, const f16* nrows, float* out) {
     const int hs = d->cfg.hidden_size, vocab = d->cfg.vocab_size;
     const SkinnyShape sh = skinny_shape(d, rows, vocab, hs);
     if (sh.ks)
-        return launch_skinny<false, true>(
+        return launch_skinny<kOutF32>(
             d, sh, skinny_args(d, sh, rows, vocab, hs, d->embed, nrows, out));
     const float alpha = 1.0f, beta = 0.0f;
     const rocblas_status st = rocblas_gemm_ex(
@@ -587,12 +636,17 @@ int layer_tail(qasr_decoder* d, const qasr_layer_weights& L, int rows, hipStream
     if (rc) return rc;
     rc = launch_rms_norm(d->x, hs, L.post_norm, d->n, rows, hs, a.rms_norm_eps, st);
     if (rc) return rc;
-    rc = gemm_f16(d, rows, 2 * inter, hs, L.gate_up_proj, d->n, d->gu, false, L.gate_up_scale);
+    bool fused = false;
+    rc = glu_skinny(d, rows, inter, hs, L.gate_up_proj, d->n, d->h, L.gate_up_scale, &fused);
     if (rc) return rc;
-    const int64_t threads = (int64_t)rows * (inter / 8);
-    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
-                       d->gu, inter, rows, d->h);
-    HIP_TRY(hipGetLastError(), "silu_mul launch");
+    if (!fused) {
+        rc = gemm_f16(d, rows, 2 * inter, hs, L.gate_up_proj, d->n, d->gu, false, L.gate_up_scale);
+        if (rc) return rc;
+        const int64_t threads = (int64_t)rows * (inter / 8);
+        hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                           st, d->gu, inter, rows, d->h);
+        HIP_TRY(hipGetLastError(), "silu_mul launch");
+    }
     return gemm_f16(d, rows, hs, inter, L.down_proj, d->h, d->x, true, L.down_scale);
 }
 
@@ -623,6 +677,8 @@ int bind_stream(qasr_decoder* d, void* stream) {
     d->stream = (hipStream_t)stream;
     const char* e = std::getenv("QASR_DECODER_BLAS");
     d->force_blas = e && *e == '1';
+    const char* f = std::getenv("QASR_DECODER_FUSE");
+    d->fuse = !(f && *f == '0');
     const rocblas_status st = rocblas_set_stream(d->blas, (hipStream_t)stream);
     if (st != rocblas_status_success) return fail(QASR_EDEVICE, "rocblas_set_stream: %s", blas_msg(st));
     return QASR_OK;

@@ -317,3 +317,41 @@ def test_int8_projections_equal_dequantized_f16(gpu, model, batch, blas, monkeyp
         runs.append((toks, np.stack(lgs)))
     assert runs[0][0] == runs[1][0]
     assert np.array_equal(runs[0][1], runs[1][1])
+
+
+@pytest.mark.parametrize("model,batch,int8", [("1.7B", 16, False), ("0.6B", 1, False),
+                                              ("1.7B", 16, True), ("0.6B", 5, True)])
+def test_fused_epilogues_equal_unfused(gpu, model, batch, int8, monkeypatch):
+    """The decode step's fused epilogues (gate|up with SiLU * up in one skinny
+    launch) against the same step with them off (QASR_DECODER_FUSE=0:
+    gate|up, then silu_mul_kernel): identical logits and tokens, bitwise --
+    the fusion moves where values are rounded to f16, not how."""
+    import torch
+
+    from decoder_model import CFG_1P7B
+    from gpu_helpers import say
+
+    cfg = dict(CFG_1P7B if model == "1.7B" else CFG_0P6B, layers=3, vocab=8192)
+    W = synth_weights(cfg, SEED_BASE + 1200 + batch, device="cuda")
+    if int8:
+        for key in list(W):
+            if isinstance(key, tuple) and key[1] in PROJECTIONS:
+                q, s = _quantize_rows(W[key])
+                W[key], W[(key[0], key[1] + "_scale")] = q, s
+    dec = _native(cfg, W, batch, 1024, max_rows=16)
+    for i in range(batch):
+        dec.prefill(_prompt(SEED_BASE + 1210 + i, 9 + 3 * i, cfg["hs"]), 0, slot=i)
+    slots, pos = list(range(batch)), [dec.pos[i] for i in range(batch)]
+    tok = torch.tensor([dec.last[i] for i in range(batch)], dtype=torch.int32, device="cuda")
+    out = {}
+    for name, fuse in (("fused", "1"), ("unfused", "0")):
+        monkeypatch.setenv("QASR_DECODER_FUSE", fuse)
+        nxt = torch.empty(batch, dtype=torch.int32, device="cuda")
+        lg = torch.empty((batch, cfg["vocab"]), dtype=torch.float32, device="cuda")
+        say(f"{model} batch {batch} int8={int8}: {name} step")
+        dec.step_tokens(slots, pos, tok, nxt, lg)
+        torch.cuda.synchronize()
+        out[name] = (nxt.cpu().numpy(), lg.cpu().numpy())
+    dec.close()
+    assert np.array_equal(out["fused"][0], out["unfused"][0])
+    assert np.array_equal(out["fused"][1], out["unfused"][1])
