@@ -254,6 +254,15 @@ int qasr_decoder_prefill_batch(qasr_decoder* dec, qasr_kv* kv, const qasr_segmen
                                int nseg, const void* hidden_dev, int32_t* next_dev,
                                float* logits_dev, void* stream);
 
+/* out[r][c] = f16(f32(q[r][c]) * scale[r]) with RNE (dequant_i8,
+ * weights.rs:366-385): the f16 copy of a resident-int8 checkpoint weight,
+ * the same values the decoder's int8 projections compute with.  q (int8
+ * [rows][cols]), scale (f32 [rows]) and out (f16 [rows][cols]) are device
+ * pointers on ctx's device; cols a multiple of 8, q 8-byte and out 16-byte
+ * aligned. */
+int qasr_dequant_i8(qasr_ctx* ctx, const void* q_dev, const float* scale_dev, int64_t rows,
+                    int32_t cols, void* out_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

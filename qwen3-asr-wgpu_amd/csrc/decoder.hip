@@ -272,15 +272,15 @@ __device__ __forceinline__ qasr::half8v load8(__amdgpu_buffer_rsrc_t r, int off)
 // reference's W8 kernels use: f16(q * s) with q * s rounded to f32 once.
 // Each byte is offset by 128 (xor 0x80) so v_cvt_f32_ubyte reads q + 128
 // exactly, and fma((q + 128), s, -128 s) = q s before its single rounding.
-__device__ __forceinline__ qasr::half8v dequant8(uint32_t lo, uint32_t hi, float s, float s128) {
+__device__ __forceinline__ qasr::half8v dequant8(uint32_t lo, uint32_t hi, float s) {
     qasr::half8v h;
-    const uint32_t d[2] = {lo ^ 0x80808080u, hi ^ 0x80808080u};
+    const uint32_t d[2] = {lo, hi};
 #pragma unroll
     for (int w = 0; w < 2; ++w)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float u = (float)((d[w] >> (8 * j)) & 0xffu);
-            h[4 * w + j] = f16_of_f32(fmaf(u, s, s128));
+            const float q = (float)(int8_t)(d[w] >> (8 * j));  // exact
+            h[4 * w + j] = f16_of_f32(q * s);
         }
     return h;
 }
@@ -295,7 +295,7 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restr
     if (i >= n_rows * k) return;
     const float s = scale[i / k];
     const uint2 v = *(const uint2*)(q + i);
-    *(qasr::half8v*)(out + i) = dequant8(v.x, v.y, s, -128.0f * s);
+    *(qasr::half8v*)(out + i) = dequant8(v.x, v.y, s);
 }
 
 struct SkinnyArgs {
@@ -327,10 +327,9 @@ __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
     const int64_t wrows = kGlu ? (int64_t)(N / 2 + 8) : 16;
     const __amdgpu_buffer_rsrc_t wres =
         rsrc((const char*)p.W + (int64_t)w0 * K * wbytes, wrows * K * wbytes);
-    float ws = 0.0f, ws128 = 0.0f;  // W8: this lane's row's scale, and -128 x it
+    float ws = 0.0f;  // W8: this lane's row's scale
     if constexpr (W8) {
         ws = p.scale[w0 + rr];
-        ws128 = -128.0f * ws;
     }
     const __amdgpu_buffer_rsrc_t xres = rsrc(p.X, (int64_t)M * K * 2);
     const int woff = rr * K * 2 + g * 16;  // bytes: weight row rr, k 8g
@@ -362,7 +361,7 @@ __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if constexpr (W8) {
-                const qasr::half8v b = dequant8(S.q[u].x, S.q[u].y, ws, ws128);
+                const qasr::half8v b = dequant8(S.q[u].x, S.q[u].y, ws);
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(S.x[u], b, acc, 0, 0, 0);
             } else {
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(S.x[u], S.b[u], acc, 0, 0, 0);
@@ -916,6 +915,28 @@ int qasr_decoder_prefill_batch(qasr_decoder* dec, qasr_kv* kv, const qasr_segmen
     if (nseg < 0 || (nseg > 0 && !segs)) return fail(QASR_EINVAL, "bad segment list");
     if (nseg == 0) return QASR_OK;
     return prefill_segments(dec, kv, segs, nseg, hidden_dev, next_dev, logits_dev, stream);
+}
+
+int qasr_dequant_i8(qasr_ctx* ctx, const void* q_dev, const float* scale_dev, int64_t rows,
+                    int32_t cols, void* out_dev, void* stream) {
+    if (!ctx) return fail(QASR_EINVAL, "null context");
+    if (rows < 0 || cols < 0 || cols % 8)
+        return fail(QASR_EINVAL, "int8 matrix %lld x %d: cols must be a multiple of 8",
+                    (long long)rows, cols);
+    if (rows == 0 || cols == 0) return QASR_OK;
+    if (!q_dev || !scale_dev || !out_dev) return fail(QASR_EINVAL, "null device pointer");
+    if ((uintptr_t)q_dev % 8 || (uintptr_t)out_dev % 16)
+        return fail(QASR_EINVAL, "q must be 8-byte and out 16-byte aligned");
+    const int64_t groups8 = rows * cols / 8;
+    if ((groups8 + 255) / 256 > (int64_t)UINT32_MAX)
+        return fail(QASR_EINVAL, "int8 matrix of %lld elements is too large", (long long)(rows * cols));
+    DeviceScope ds(ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    hipLaunchKernelGGL(dequant_rows_kernel, dim3((unsigned)((groups8 + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (const int8_t*)q_dev, scale_dev, rows, (int)cols,
+                       (f16*)out_dev);
+    HIP_TRY(hipGetLastError(), "dequantisation launch");
+    return QASR_OK;
 }
 
 }  // extern "C"

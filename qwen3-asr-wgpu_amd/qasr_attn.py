@@ -36,7 +36,7 @@ ABI_SYMBOLS = (
     "qasr_kv_get_info", "qasr_kv_ensure_capacity", "qasr_qk_norm_rope_append",
     "qasr_decode_attn", "qasr_decode_step", "qasr_prefill_attn", "qasr_prefill_layer",
     "qasr_decoder_create", "qasr_decoder_destroy", "qasr_decoder_step", "qasr_decoder_prefill",
-    "qasr_decoder_prefill_batch",
+    "qasr_decoder_prefill_batch", "qasr_dequant_i8",
 )
 MAX_PREFILL_SEGMENTS = 64  # segments per qasr_decoder_prefill_batch call
 
@@ -141,6 +141,7 @@ def load(path: str = LIB_PATH):
                                        _vp, _vp, _vp]
     L.qasr_decoder_prefill_batch.argtypes = [_vp, _vp, ctypes.POINTER(Segment), ctypes.c_int, _vp,
                                              _vp, _vp, _vp]
+    L.qasr_dequant_i8.argtypes = [_vp, _vp, _vp, ctypes.c_int64, ctypes.c_int32, _vp, _vp]
     _lib = L
     return L
 
@@ -391,6 +392,20 @@ class AttnBackend:
             for s in slots:
                 self.pos[s] += 1
         return out
+
+
+def dequant_i8(ctx: Context, q, scale, out=None):
+    """f16 copy of an int8 [rows][cols] matrix with f32 row scales (the
+    reference's dequant_i8, weights.rs:366-385), on the GPU."""
+    import torch
+
+    rows, cols = int(q.shape[0]), int(q.shape[1])
+    if out is None:
+        out = torch.empty((rows, cols), dtype=torch.float16, device=q.device)
+    _check(load().qasr_dequant_i8(ctx.handle, _dev(q, "q", torch.int8),
+                                  _dev(scale, "scale", torch.float32), rows, cols,
+                                  _dev(out, "out"), _stream(None)))
+    return out
 
 
 LAYER_WEIGHT_NAMES = ("input_layernorm", "q_proj", "k_proj", "v_proj", "q_norm", "k_norm",

@@ -7,6 +7,7 @@ Sources (paths relative to the reference checkout):
   src/config.rs:177-195 mrope_section default [24, 20, 20], interleaved default true
   src/config.rs:261-290 HF-native config layout test (text_config values)
   src/config.rs:212-258, 331-341 mrope_section / mrope_interleaved from rope_scaling
+  src/weights.rs:588-625 int8 dequantisation tests (f16(q * scale) per row)
 
 The reference ships no numeric vectors for attention itself (its numeric gate
 is transcript identity on audio fixtures kept outside the repository), so
@@ -79,6 +80,14 @@ KNOWN = {
              "rope_scaling": {"rope_type": "mrope", "mrope_section": [24, 20, 20],
                               "interleaved": False, "mrope_interleaved": False}}}},
          "expect": {"mrope_interleaved": False}},
+    ],
+    # int8 [rows][cols] with f32 row scales -> the f16 values the reference's
+    # get_f16 / get_matrix return for them.
+    "int8_dequant": [
+        {"source": "src/weights.rs:588-603", "rows": 2, "cols": 2, "q": [4, -8, -2, 3],
+         "scale": [0.25, -0.5], "expect": [1.0, -2.0, 1.0, -1.5]},
+        {"source": "src/weights.rs:613-625 (asserts row 0; row 1 by the same rule)", "rows": 2, "cols": 2, "q": [127, 0, 0, 127],
+         "scale": [1.0, 2.0], "expect": [127.0, 0.0, 0.0, 254.0]},
     ],
 }
 
