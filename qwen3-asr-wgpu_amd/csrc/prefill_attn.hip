@@ -56,10 +56,6 @@ static_assert(kGroupKeys == 64, "a key group's half tile is one 64-key wave step
 constexpr int kTileHalves = kTileKeys * kHeadDim;  // one 32 KB K or V tile
 constexpr float kNegInf = -__builtin_inff();
 constexpr float kRescaleSlack = 8.0f;  // log2 of the largest p before the max moves
-#ifndef QASR_MFMA_PRIO
-#define QASR_MFMA_PRIO 1
-#endif
-constexpr int kMfmaPrio = QASR_MFMA_PRIO;  // wave priority while issuing a block of MFMAs
 
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -159,7 +155,6 @@ template <bool MASK>
 __device__ __forceinline__ void step_s(Wave& w, const f16* kt, int k0, half8v (&pb)[4]) {
     // S^T: keys kb*32 + (8*(i/4) + 4*g + i%4) x query n, accumulated over dims.
     float16v s[2] = {(float16v){}, (float16v){}};
-    if (kMfmaPrio) __builtin_amdgcn_s_setprio(kMfmaPrio);
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
@@ -176,10 +171,6 @@ __device__ __forceinline__ void step_s(Wave& w, const f16* kt, int k0, half8v (&
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    if (kMfmaPrio) {
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_setprio(0);
-    }
     float mx = kNegInf;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -227,10 +218,6 @@ __device__ __forceinline__ void step_s(Wave& w, const f16* kt, int k0, half8v (&
 // Second half: O^T += V^T P^T with V rows vt[0..63] (slab stride
 // kTileKeys*32 halves).
 __device__ __forceinline__ void step_pv(Wave& w, const f16* vt, const half8v (&pb)[4]) {
-    if (kMfmaPrio) {
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_setprio(kMfmaPrio);
-    }
 #pragma unroll
     for (int w4 = 0; w4 < 4; ++w4)
 #pragma unroll
@@ -249,10 +236,6 @@ __device__ __forceinline__ void step_pv(Wave& w, const f16* vt, const half8v (&p
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-    if (kMfmaPrio) {
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_setprio(0);
-    }
 }
 
 // Merge of the nsp split-K partials of one wave's 32 rows (lane = query row),
