@@ -406,11 +406,11 @@ def main():
         lens5 = splitmix_lengths(SEED_BASE + 5, 64, 64, 4096)
         extra["config5_decode"] = bench_decode(64, lens5, max(5, K // 5), W)
         log("[bench] text decoder steps (whole decoder around the attention path)")
-        extra["text_decoder_1p7b_16slots"] = bench_text_decoder("1.7B", lens3, max(5, K // 5), W)
-        extra["text_decoder_0p6b_1slot"] = bench_text_decoder("0.6B", [511], max(5, K // 5), W)
-        extra["text_decoder_1p7b_16slots_int8"] = bench_text_decoder("1.7B", lens3, max(5, K // 5),
+        extra["text_decoder_1p7b_16slots"] = bench_text_decoder("1.7B", lens3, K, W)
+        extra["text_decoder_0p6b_1slot"] = bench_text_decoder("0.6B", [511], K, W)
+        extra["text_decoder_1p7b_16slots_int8"] = bench_text_decoder("1.7B", lens3, K,
                                                                      W, int8=True)
-        extra["text_decoder_0p6b_1slot_int8"] = bench_text_decoder("0.6B", [511], max(5, K // 5),
+        extra["text_decoder_0p6b_1slot_int8"] = bench_text_decoder("0.6B", [511], K,
                                                                    W, int8=True)
         log("[bench] batch job through the slot scheduler (32 segments, width 16 vs 1)")
         extra["serving_1p7b_32seg_width16"] = bench_serving("1.7B", 32, 16, 48)
