@@ -378,6 +378,7 @@ def main():
             "decode1": lambda: bench_decode(1, [511], K, W),
             "decode4": lambda: bench_decode(1, [8192], K, W),
             "decode5": lambda: bench_decode(64, splitmix_lengths(SEED_BASE + 5, 64, 64, 4096), K, W),
+            "decode16x2k": lambda: bench_decode(16, [2048] * 16, K, W),
             "prefill2": lambda: bench_prefill(420, 0, K, W),
             "prefill4": lambda: bench_prefill(512, 7680, K, W),
             "copycal": lambda: copy_calibration(K),
@@ -405,6 +406,8 @@ def main():
         log("[bench] config 5")
         lens5 = splitmix_lengths(SEED_BASE + 5, 64, 64, 4096)
         extra["config5_decode"] = bench_decode(64, lens5, max(5, K // 5), W)
+        log("[bench] 16 slots at a uniform 2048-token context (the target's ~2k context)")
+        extra["decode_16slots_2k_context"] = bench_decode(16, [2048] * 16, K, W)
         log("[bench] text decoder steps (whole decoder around the attention path)")
         extra["text_decoder_1p7b_16slots"] = bench_text_decoder("1.7B", lens3, K, W)
         extra["text_decoder_0p6b_1slot"] = bench_text_decoder("0.6B", [511], K, W)
