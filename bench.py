@@ -304,6 +304,42 @@ def bench_serving(model: str, segments: int, width: int, max_new: int, seed: int
     return out
 
 
+def bench_prefill_batch(model: str, segments: int, steps: int, warmup: int, seed: int = 23):
+    """qasr_decoder_prefill_batch over `segments` prompts of U[150, 450] rows
+    (projections once over all rows, attention per segment), 28 layers:
+    prompt rows per second and projection TFLOP/s (2 x weights x rows)."""
+    import numpy as np
+    import torch
+
+    import qasr_attn
+
+    dims = DECODERS[model]
+    W = decoder_weights(dims["hs"], dims["inter"])
+    proj_params = sum(t.numel() for k, t in W.items() if isinstance(k, tuple) and k[1].endswith("_proj"))
+    dec = qasr_attn.TextDecoder(W, NQH, NKVH, HD, LAYERS, 1e-6, 16384, slots=segments,
+                                max_rows=4096, cap=1024)
+    del W
+    rng = np.random.default_rng(seed)
+    lens = [int(x) for x in rng.integers(150, 450, size=segments)]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    items = [(i, torch.randn((n, dims["hs"]), device="cuda", generator=g).half())
+             for i, n in enumerate(lens)]
+    for _ in range(warmup):
+        dec.prefill_batch(items)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dec.prefill_batch(items)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    dec.close()
+    torch.cuda.empty_cache()
+    rows = sum(lens)
+    return {"model": model, "segments": segments, "rows": rows, "ms": dt * 1e3,
+            "rows_per_s": rows / dt, "projection_TFLOPs": 2.0 * proj_params * rows / dt / 1e12}
+
+
 def cpu_baseline(lengths, budget_s: float = 10.0):
     """Reference CPU path (C++ restatement of cpu_decoder.rs, oracle/) on config
     3: stage (a) + attention for each of the 16 slots, one layer at a time,
@@ -387,6 +423,7 @@ def main():
             "decoder16_int8": lambda: bench_text_decoder("1.7B", lens3, K, W, int8=True),
             "decoder1_int8": lambda: bench_text_decoder("0.6B", [511], K, W, int8=True),
             "serving": lambda: bench_serving("1.7B", 32, 16, 48),
+            "prefill_batch": lambda: bench_prefill_batch("1.7B", 16, max(3, K // 10), 1),
         }
         log(json.dumps({only: runs[only]()}))
         return

@@ -163,6 +163,16 @@ int qasr_decode_step(qasr_ctx* ctx, qasr_kv* kv, int layer, int batch, const int
 int qasr_prefill_attn(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, int s,
                       const void* q_dev, void* out_dev, void* stream);
 
+/* Stage (c) for several segments in one call (the attention loop of
+ * prefill_multi, decoder.rs:3642-3700, one dispatch per segment there):
+ * segment i's roped q rows are rows row_i .. of q_dev (segments concatenated
+ * in order), its output the same rows of out_dev, at positions
+ * segs[i].pos0 .. of slot segs[i].slot, whose K/V are already appended.
+ * Segments of short key ranges go out in one launch; the rest as in
+ * qasr_prefill_attn.  Same checks as qasr_prefill_attn, before any launch. */
+int qasr_prefill_attn_batch(qasr_ctx* ctx, qasr_kv* kv, int layer, const qasr_segment* segs,
+                            int nseg, const void* q_dev, void* out_dev, void* stream);
+
 /* Stages (a)+(c) for one layer of one slot's prefill: stage (a) on s raw qkv
  * rows (q_work_dev receives the roped Q, [s][nqh*hd]), then stage (c).
  * Replaces prefill_impl's attention block (decoder.rs:4856-5098). */

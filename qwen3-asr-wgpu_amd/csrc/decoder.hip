@@ -730,7 +730,6 @@ int prefill_segments(qasr_decoder* dec, qasr_kv* kv, const qasr_segment* segs, i
     if (rc) return rc;
     const qasr_attn_cfg& a = ctx->cfg;
     const int hs = dec->cfg.hidden_size, rows = (int)total;
-    const int qdim = a.num_attention_heads * a.head_dim;
     const int qkvdim = (a.num_attention_heads + 2 * a.num_key_value_heads) * a.head_dim;
     HIP_TRY(hipMemcpyAsync(dec->x, hidden_dev, (size_t)rows * hs * 2, hipMemcpyDeviceToDevice, st),
             "prefill input copy");
@@ -743,13 +742,8 @@ int prefill_segments(qasr_decoder* dec, qasr_kv* kv, const qasr_segment* segs, i
         rc = qasr_qk_norm_rope_append(dec->ctx, kv, l, segs, nseg, dec->qkv, L.q_norm, L.k_norm,
                                       dec->qw, stream);
         if (rc) return rc;
-        int64_t r0 = 0;
-        for (int i = 0; i < nseg; ++i) {
-            rc = qasr_prefill_attn(dec->ctx, kv, l, segs[i].slot, segs[i].pos0, segs[i].rows,
-                                   dec->qw + r0 * qdim, dec->attn + r0 * qdim, stream);
-            if (rc) return rc;
-            r0 += segs[i].rows;
-        }
+        rc = qasr_prefill_attn_batch(dec->ctx, kv, l, segs, nseg, dec->qw, dec->attn, stream);
+        if (rc) return rc;
         rc = layer_tail(dec, L, rows, st);
         if (rc) return rc;
     }

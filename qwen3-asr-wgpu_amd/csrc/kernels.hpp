@@ -115,7 +115,22 @@ constexpr int64_t kPrefillWaveMl = 2 * 64;       // m and l of each lane
 constexpr int64_t kPrefillItemFloats = kPrefillWaves * kPrefillWaveFloats;
 constexpr int64_t kPrefillItemMl = kPrefillWaves * kPrefillWaveMl;
 
+// Several segments in one launch (no key splits): segment i's rows are q/out
+// rows row_base[i] .. +rows[i] at positions kv_start[i] ..; its K/V blocks
+// start kv_off[i] elements past PrefillArgs::k / ::v; its items (kv head
+// minor, then row block) are item_base[i] .. item_base[i+1]-1.
+constexpr int kMaxPrefillSegs = 64;
+struct PrefillSegs {
+    int32_t n;
+    int32_t item_base[kMaxPrefillSegs + 1];
+    int32_t kv_start[kMaxPrefillSegs];
+    int32_t rows[kMaxPrefillSegs];
+    int32_t row_base[kMaxPrefillSegs];
+    int64_t kv_off[kMaxPrefillSegs];
+};
+
 PrefillPlan plan_prefill(int s, int kv_start, int nkvh, int tiles_per_split);
+hipError_t launch_prefill_attn_segs(const PrefillArgs& a, const PrefillSegs& S, hipStream_t stream);
 hipError_t launch_prefill_attn(const PrefillArgs& a, const PrefillPlan& P, const PrefillWs& ws,
                                hipStream_t stream);
 

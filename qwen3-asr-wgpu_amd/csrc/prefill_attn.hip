@@ -413,9 +413,10 @@ __device__ __forceinline__ void epilogue(Wave& w, const EpiArgs& e) {
     if (e.tid == 0) ticket_reset(ctr);
 }
 
+template <bool MULTI>
 __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
-    PrefillArgs a, PrefillPlan P, float* __restrict__ ws_o, float* __restrict__ ws_ml,
-    uint32_t* __restrict__ counters) {
+    PrefillArgs a, PrefillPlan P, PrefillSegs S, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml, uint32_t* __restrict__ counters) {
     // 128 KB: K and V tiles, double buffered.
     __shared__ __attribute__((aligned(16))) f16 K0[kTileHalves];
     __shared__ __attribute__((aligned(16))) f16 K1[kTileHalves];
@@ -430,25 +431,45 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     const int n = lane & 31;  // query column within the wave's 32 rows
     const int g = lane >> 5;  // k-slot group of the MFMA operands
 
-    const int kvh = blockIdx.x % a.nkvh;
-    const int rem = blockIdx.x / a.nkvh;
-    const int item = kvh * P.items_per_kvh + rem;  // canonical index (workspace)
-    int rb = 0;
-    {
+    int kvh, item, rb, sp, nsp, tps;
+    if constexpr (MULTI) {
+        // Segment = number of later segment starts at or before this item
+        // (one lane per segment, a ballot); then kv head minor, row block.
+        static_assert(kMaxPrefillSegs <= 64, "one lane per segment");
+        const int seg = __popcll(__ballot(lane + 1 < S.n && S.item_base[lane + 1] <= (int)blockIdx.x));
+        const int local = blockIdx.x - S.item_base[seg];
+        kvh = local % a.nkvh;
+        rb = local / a.nkvh;
+        item = 0;  // no split: the workspace is not used
+        sp = 0;
+        nsp = 1;
+        tps = kMaxRowBlocks * kRowsPerBlock;  // every tile of the row block
+        a.s = S.rows[seg];
+        a.kv_start = S.kv_start[seg];
+        a.q += (int64_t)S.row_base[seg] * a.nqh * kHeadDim;
+        a.out += (int64_t)S.row_base[seg] * a.nqh * kHeadDim;
+        a.k += S.kv_off[seg];
+        a.v += S.kv_off[seg];
+    } else {
+        kvh = blockIdx.x % a.nkvh;
+        const int rem = blockIdx.x / a.nkvh;
+        item = kvh * P.items_per_kvh + rem;  // canonical index (workspace)
+        rb = 0;
         int lo = 0, hi = P.nrb - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
             if (P.sp_base[mid] <= rem) lo = mid; else hi = mid - 1;
         }
         rb = lo;
+        sp = rem - P.sp_base[rb];
+        nsp = P.sp_base[rb + 1] - P.sp_base[rb];
+        tps = P.tps;
     }
-    const int sp = rem - P.sp_base[rb];
-    const int nsp = P.sp_base[rb + 1] - P.sp_base[rb];
     const int row0 = rb * kRowsPerBlock;
     const int kend = a.kv_start + min(row0 + kRowsPerBlock, a.s);  // keys < kend
     const int ntiles = (kend + kTileKeys - 1) / kTileKeys;
-    const int t_begin = sp * P.tps;
-    const int t_end = min(t_begin + P.tps, ntiles);
+    const int t_begin = sp * tps;
+    const int t_end = min(t_begin + tps, ntiles);
 
     const int head = kvh * kRep + (rw & 1);
     const int wrow0 = row0 + (rw >> 1) * 32;  // first row of this wave
@@ -560,8 +581,17 @@ hipError_t launch_prefill_attn(const PrefillArgs& a, const PrefillPlan& P, const
     const int items = P.items_per_kvh * a.nkvh;
     if (items <= 0) return hipSuccess;
     if (items > ws.items || P.nrb > kMaxRowBlocks) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(prefill_attn_kernel, dim3(items), dim3(kThreads), 0, stream, a, P, ws.o,
-                       ws.ml, ws.counters);
+    hipLaunchKernelGGL(prefill_attn_kernel<false>, dim3(items), dim3(kThreads), 0, stream, a, P,
+                       PrefillSegs{}, ws.o, ws.ml, ws.counters);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_attn_segs(const PrefillArgs& a, const PrefillSegs& S, hipStream_t stream) {
+    if (S.n <= 0 || S.n > kMaxPrefillSegs) return hipErrorInvalidValue;
+    const int items = S.item_base[S.n];
+    if (items <= 0) return hipSuccess;
+    hipLaunchKernelGGL(prefill_attn_kernel<true>, dim3(items), dim3(kThreads), 0, stream, a,
+                       PrefillPlan{}, S, nullptr, nullptr, nullptr);
     return hipGetLastError();
 }
 

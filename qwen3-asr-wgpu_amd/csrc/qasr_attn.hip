@@ -636,6 +636,81 @@ int qasr_prefill_attn(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_st
     return QASR_OK;
 }
 
+// Longest key range (kv_start + rows) of a segment that a one-launch batched
+// prefill takes: each row block's keys are then one workgroup's work.
+constexpr int kPrefillOneLaunchKeys = 2048;
+
+int qasr_prefill_attn_batch(qasr_ctx* ctx, qasr_kv* kv, int layer, const qasr_segment* segs,
+                            int nseg, const void* q_dev, void* out_dev, void* stream) {
+    int rc = check_common(ctx, kv, layer);
+    if (rc) return rc;
+    if (nseg < 0 || (nseg > 0 && !segs)) return fail(QASR_EINVAL, "bad segment list");
+    if (nseg == 0) return QASR_OK;
+    if (!q_dev || !out_dev) return fail(QASR_EINVAL, "null device pointer");
+    // Every segment checked before any launch.  One launch takes them all
+    // when each key range is short enough to be one workgroup's per row
+    // block (no split); otherwise one launch per segment, which splits long
+    // key ranges across workgroups.
+    bool one_launch = nseg > 1 && nseg <= qasr::kMaxPrefillSegs;
+    for (int i = 0; i < nseg; ++i) {
+        const qasr_segment& g = segs[i];
+        if (g.slot < 0 || g.slot >= kv->slots)
+            return fail(QASR_EINVAL, "segment %d: slot %d outside [0, %d)", i, g.slot, kv->slots);
+        if (g.pos0 < 0 || g.rows < 0) return fail(QASR_EINVAL, "segment %d: negative kv_start/rows", i);
+        const int64_t end = (int64_t)g.pos0 + g.rows;
+        if (end > ctx->cfg.max_seq)
+            return fail(QASR_ERANGE, "segment %d: prefill needs %lld positions, max_seq is %d", i,
+                        (long long)end, ctx->cfg.max_seq);
+        if (end > kv->cap)
+            return fail(QASR_ERANGE, "segment %d: prefill needs %lld positions, KV capacity is %d",
+                        i, (long long)end, kv->cap);
+        if (end > kPrefillOneLaunchKeys || g.rows > qasr::kMaxRowBlocks * qasr::kPrefillRows)
+            one_launch = false;
+    }
+    const int64_t ld = (int64_t)ctx->cfg.num_attention_heads * qasr::kHeadDim;
+    if (!one_launch) {
+        int64_t r0 = 0;
+        for (int i = 0; i < nseg; ++i) {
+            rc = qasr_prefill_attn(ctx, kv, layer, segs[i].slot, segs[i].pos0, segs[i].rows,
+                                   (const f16*)q_dev + r0 * ld, (f16*)out_dev + r0 * ld, stream);
+            if (rc) return rc;
+            r0 += segs[i].rows;
+        }
+        return QASR_OK;
+    }
+    DeviceScope ds(ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    const qasr_attn_cfg& c = ctx->cfg;
+    const qasr::CacheGeom g = geom(kv);
+    qasr::PrefillSegs S{};
+    S.n = nseg;
+    S.item_base[0] = 0;
+    int32_t r0 = 0;
+    for (int i = 0; i < nseg; ++i) {
+        const int nrb = (segs[i].rows + qasr::kPrefillRows - 1) / qasr::kPrefillRows;
+        S.item_base[i + 1] = S.item_base[i] + c.num_key_value_heads * nrb;
+        S.kv_start[i] = segs[i].pos0;
+        S.rows[i] = segs[i].rows;
+        S.row_base[i] = r0;
+        S.kv_off[i] = (int64_t)segs[i].slot * g.slot_stride + (int64_t)layer * g.layer_stride;
+        r0 += segs[i].rows;
+    }
+    qasr::PrefillArgs a;
+    a.q = (const f16*)q_dev;
+    a.out = (f16*)out_dev;
+    a.k = g.base;
+    a.v = g.base + g.kv_stride;
+    a.head_stride = g.head_stride;
+    a.nqh = c.num_attention_heads;
+    a.nkvh = c.num_key_value_heads;
+    a.s = 0;
+    a.kv_start = 0;
+    a.scale_log2 = ctx->scale_log2;
+    const hipError_t e = qasr::launch_prefill_attn_segs(a, S, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "prefill attention launch");
+    return QASR_OK;
+}
+
 int qasr_prefill_layer(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, int s,
                        const void* qkv_dev, const void* q_gain_dev, const void* k_gain_dev,
                        void* q_work_dev, void* out_dev, void* stream) {

@@ -36,7 +36,7 @@ ABI_SYMBOLS = (
     "qasr_kv_get_info", "qasr_kv_ensure_capacity", "qasr_qk_norm_rope_append",
     "qasr_decode_attn", "qasr_decode_step", "qasr_prefill_attn", "qasr_prefill_layer",
     "qasr_decoder_create", "qasr_decoder_destroy", "qasr_decoder_step", "qasr_decoder_prefill",
-    "qasr_decoder_prefill_batch", "qasr_dequant_i8",
+    "qasr_decoder_prefill_batch", "qasr_dequant_i8", "qasr_prefill_attn_batch",
 )
 MAX_PREFILL_SEGMENTS = 64  # segments per qasr_decoder_prefill_batch call
 
@@ -132,6 +132,8 @@ def load(path: str = LIB_PATH):
                                     ctypes.c_int, _vp, _vp, _vp]
     L.qasr_prefill_layer.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                      ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp]
+    L.qasr_prefill_attn_batch.argtypes = [_vp, _vp, ctypes.c_int, ctypes.POINTER(Segment),
+                                          ctypes.c_int, _vp, _vp, _vp]
     L.qasr_decoder_create.argtypes = [_vp, ctypes.POINTER(DecoderCfg), _vp, _vp,
                                       ctypes.POINTER(LayerWeights), ctypes.POINTER(_vp)]
     L.qasr_decoder_destroy.argtypes = [_vp]
@@ -333,6 +335,15 @@ def prefill_attn(ctx: Context, kv: KVPool, layer: int, slot: int, kv_start: int,
                  stream=None):
     _check(load().qasr_prefill_attn(ctx.handle, kv.handle, layer, slot, kv_start, s,
                                     _dev(q, "q"), _dev(out, "out"), _stream(stream)))
+
+
+def prefill_attn_batch(ctx: Context, kv: KVPool, layer: int, segments, q, out, stream=None):
+    """Stage (c) for segments [(slot, kv_start, rows)] whose q rows (and
+    output rows) are concatenated in order; one launch where the key ranges
+    are short."""
+    segs = (Segment * len(segments))(*[Segment(int(s), int(p), int(r)) for s, p, r in segments])
+    _check(load().qasr_prefill_attn_batch(ctx.handle, kv.handle, layer, segs, len(segments),
+                                          _dev(q, "q"), _dev(out, "out"), _stream(stream)))
 
 
 def prefill_layer(ctx: Context, kv: KVPool, layer: int, slot: int, kv_start: int, s: int, qkv,

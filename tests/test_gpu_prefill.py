@@ -145,3 +145,72 @@ def test_prefill_row_equals_decode_query(O, gpu):
                           slots=[0] * len(rows))
     assert_parity(host(dout), out[rows], "prefill vs decode")
     g.close()
+
+
+def _segments_setup(O, rng, lay, segments, cap):
+    """Pool with every segment's earlier keys appended; returns (Gpu, per-slot
+    oracles, the segments' qkv rows concatenated, roped q rows)."""
+    from gpu_helpers import Gpu
+
+    g = Gpu(slots=len(segments), cap=cap)
+    refs = []
+    for slot, kv_start, _ in segments:
+        ref = OracleSeq(O, cap, lay, tables(O))
+        if kv_start:
+            pre = rng.normal_f16((kv_start, TOT))
+            ref.append(pre, 0)
+            g.append(0, lay, [(slot, 0, kv_start)], pre)
+        refs.append(ref)
+    qkv = rng.normal_f16((sum(r for _, _, r in segments), TOT))
+    q = g.append(0, lay, list(segments), qkv)
+    return g, refs, qkv, q
+
+
+def test_prefill_attn_batch_equals_per_segment_launches(O, gpu):
+    """Key ranges of at most 256 (no split either way): one launch for all
+    segments gives the per-segment launches' output bit for bit."""
+    import qasr_attn
+    from gpu_helpers import dev, empty, host, say
+
+    from oracle import Rng
+
+    rng = Rng(SEED_BASE + 480)
+    lay = Layer(rng)
+    segments = [(0, 0, 37), (1, 0, 200), (2, 100, 120), (3, 0, 1), (4, 190, 66)]
+    g, _, _, q = _segments_setup(O, rng, lay, segments, 512)
+    total = q.shape[0]
+    say(f"prefill_attn_batch over {segments}")
+    out_b = empty(total, QDIM)
+    qasr_attn.prefill_attn_batch(g.ctx, g.kv, 0, segments, dev(q), out_b)
+    got = host(out_b)
+    r0 = 0
+    for slot, kv_start, rows in segments:
+        out_s = empty(rows, QDIM)
+        qasr_attn.prefill_attn(g.ctx, g.kv, 0, slot, kv_start, rows, dev(q[r0:r0 + rows]), out_s)
+        assert np.array_equal(got[r0:r0 + rows], host(out_s)), f"segment {slot}"
+        r0 += rows
+    g.close()
+
+
+def test_prefill_attn_batch_long_segments_against_oracle(O, gpu):
+    """Key ranges up to 2048 in one launch (each row block's keys in one
+    workgroup) against the oracle, segment by segment."""
+    import qasr_attn
+    from gpu_helpers import dev, empty, host, say
+
+    from oracle import Rng
+
+    rng = Rng(SEED_BASE + 481)
+    lay = Layer(rng)
+    segments = [(0, 0, 300), (1, 500, 700), (2, 0, 1500), (3, 1200, 64), (4, 2000, 48)]
+    g, refs, qkv, q = _segments_setup(O, rng, lay, segments, cap_for(2048))
+    say(f"prefill_attn_batch over {segments}")
+    out_b = empty(q.shape[0], QDIM)
+    qasr_attn.prefill_attn_batch(g.ctx, g.kv, 0, segments, dev(q), out_b)
+    got = host(out_b)
+    r0 = 0
+    for (slot, kv_start, rows), ref in zip(segments, refs):
+        _, want = ref.step(qkv[r0:r0 + rows], kv_start)
+        assert_parity(got[r0:r0 + rows], want, f"segment {slot} kv_start={kv_start} rows={rows}")
+        r0 += rows
+    g.close()
