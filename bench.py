@@ -279,7 +279,7 @@ def bench_serving(model: str, segments: int, width: int, max_new: int, seed: int
 
     dims = DECODERS[model]
     W = decoder_weights(dims["hs"], dims["inter"])
-    dec = qasr_attn.TextDecoder(W, NQH, NKVH, HD, LAYERS, 1e-6, 16384, slots=1, max_rows=4096,
+    dec = qasr_attn.TextDecoder(W, NQH, NKVH, HD, LAYERS, 1e-6, 16384, slots=1, max_rows=8192,
                                 cap=1024)
     del W
     rng = np.random.default_rng(seed)
@@ -304,6 +304,34 @@ def bench_serving(model: str, segments: int, width: int, max_new: int, seed: int
     return out
 
 
+def bench_prefill_one(model: str, rows: int, steps: int, warmup: int, seed: int = 29):
+    """qasr_decoder_prefill of one prompt of `rows` rows through 28 layers
+    (the time to the first token of one segment)."""
+    import torch
+
+    import qasr_attn
+
+    dims = DECODERS[model]
+    W = decoder_weights(dims["hs"], dims["inter"])
+    dec = qasr_attn.TextDecoder(W, NQH, NKVH, HD, LAYERS, 1e-6, 16384, slots=1, max_rows=4096,
+                                cap=cap_for(rows + 1))
+    del W
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    hidden = torch.randn((rows, dims["hs"]), device="cuda", generator=g).half()
+    for _ in range(warmup):
+        dec.prefill(hidden)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dec.prefill(hidden)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    dec.close()
+    torch.cuda.empty_cache()
+    return {"model": model, "rows": rows, "ms": dt * 1e3, "rows_per_s": rows / dt}
+
+
 def bench_prefill_batch(model: str, segments: int, steps: int, warmup: int, seed: int = 23):
     """qasr_decoder_prefill_batch over `segments` prompts of U[150, 450] rows
     (projections once over all rows, attention per segment), 28 layers:
@@ -317,7 +345,7 @@ def bench_prefill_batch(model: str, segments: int, steps: int, warmup: int, seed
     W = decoder_weights(dims["hs"], dims["inter"])
     proj_params = sum(t.numel() for k, t in W.items() if isinstance(k, tuple) and k[1].endswith("_proj"))
     dec = qasr_attn.TextDecoder(W, NQH, NKVH, HD, LAYERS, 1e-6, 16384, slots=segments,
-                                max_rows=4096, cap=1024)
+                                max_rows=8192, cap=1024)
     del W
     rng = np.random.default_rng(seed)
     lens = [int(x) for x in rng.integers(150, 450, size=segments)]
@@ -424,6 +452,7 @@ def main():
             "decoder1_int8": lambda: bench_text_decoder("0.6B", [511], K, W, int8=True),
             "serving": lambda: bench_serving("1.7B", 32, 16, 48),
             "prefill_batch": lambda: bench_prefill_batch("1.7B", 16, max(3, K // 10), 1),
+            "prefill_one": lambda: bench_prefill_one("1.7B", 420, max(5, K // 5), 2),
         }
         log(json.dumps({only: runs[only]()}))
         return

@@ -220,7 +220,7 @@ typedef struct qasr_decoder_cfg {
     int32_t hidden_size;       /* 1024 (0.6B) or 2048 (1.7B) */
     int32_t intermediate_size; /* 3072 or 6144 */
     int32_t vocab_size;        /* 151936 */
-    int32_t max_rows;          /* largest decode batch or prefill chunk one call runs */
+    int32_t max_rows;          /* largest decode batch or prefill chunk one call runs (<= 16384) */
 } qasr_decoder_cfg;
 
 typedef struct qasr_decoder qasr_decoder;

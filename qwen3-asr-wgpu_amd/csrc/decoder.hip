@@ -46,6 +46,9 @@ constexpr int kArgmaxChunks = 32;  // workgroups per logits row in the first arg
 constexpr int kHeadRows = 128;     // rows per logits GEMM + argmax (bounds the logits scratch)
 constexpr size_t kBlasWorkspace = size_t(64) << 20;
 constexpr int kMaxPrefillSegs = 64;  // segments of one batched prefill call
+// Rows of one call (decode batch or prefill): bounds the activation
+// workspace (about 61 KB per row at the 1.7B shape, 1 GB at the limit).
+constexpr int kMaxDecoderRows = 16384;
 
 // ---- block reductions (wave64 shuffles, then one LDS pass) ---------------
 __device__ __forceinline__ float wave_sum(float v) {
@@ -779,9 +782,9 @@ int qasr_decoder_create(qasr_ctx* ctx, const qasr_decoder_cfg* cfg, const void* 
                     "vocab %d and max_rows %d positive", hs, inter, vocab, cfg->max_rows);
     if (hs > 2 * inter)
         return fail(QASR_EINVAL, "hidden %d above 2 x intermediate %d", hs, inter);
-    if (cfg->max_rows > 4096)
-        return fail(QASR_EINVAL, "max_rows %d above the prefill limit of 4096 rows per call",
-                    cfg->max_rows);
+    if (cfg->max_rows > kMaxDecoderRows)
+        return fail(QASR_EINVAL, "max_rows %d above the limit of %d rows per call", cfg->max_rows,
+                    kMaxDecoderRows);
     for (int l = 0; l < a.num_hidden_layers; ++l) {
         const qasr_layer_weights& L = layers[l];
         if (!L.input_norm || !L.qkv_proj || !L.q_norm || !L.k_norm || !L.o_proj || !L.post_norm ||

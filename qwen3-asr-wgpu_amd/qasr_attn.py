@@ -597,6 +597,11 @@ class TextDecoder:
                     logits[i].copy_(lg_rows[k])
             group.clear()
 
+        # Calls of about equal row counts (a lone short remainder call would
+        # pay every layer's launches for a few rows).
+        short = [int(h.shape[0]) for _, h, _ in items if int(h.shape[0]) <= self.max_rows]
+        calls = max(1, -(-sum(short) // self.max_rows), -(-len(short) // MAX_PREFILL_SEGMENTS))
+        target = -(-sum(short) // calls)
         used = 0
         for i, (slot, hidden, start) in enumerate(items):
             s = int(hidden.shape[0])
@@ -604,7 +609,8 @@ class TextDecoder:
                 toks[i] = self.prefill(hidden, start, slot=slot,
                                        logits=logits[i] if logits is not None else None)
                 continue
-            if used + s > self.max_rows or len(group) == MAX_PREFILL_SEGMENTS:
+            if group and (used + s > self.max_rows or used >= target
+                          or len(group) == MAX_PREFILL_SEGMENTS):
                 flush()
                 used = 0
             group.append((i, s))
