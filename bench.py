@@ -481,6 +481,9 @@ def main():
                                                                      W, int8=True)
         extra["text_decoder_0p6b_1slot_int8"] = bench_text_decoder("0.6B", [511], K,
                                                                    W, int8=True)
+        log("[bench] whole-decoder prefill: one 420-row prompt, 16 prompts batched")
+        extra["decoder_prefill_1p7b_420rows"] = bench_prefill_one("1.7B", 420, max(5, K // 5), 2)
+        extra["decoder_prefill_batch_1p7b_16prompts"] = bench_prefill_batch("1.7B", 16, max(3, K // 10), 1)
         log("[bench] batch job through the slot scheduler (32 segments, width 16 vs 1)")
         extra["serving_1p7b_32seg_width16"] = bench_serving("1.7B", 32, 16, 48)
         for k, v in extra.items():
