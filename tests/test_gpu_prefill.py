@@ -214,3 +214,28 @@ def test_prefill_attn_batch_long_segments_against_oracle(O, gpu):
         assert_parity(got[r0:r0 + rows], want, f"segment {slot} kv_start={kv_start} rows={rows}")
         r0 += rows
     g.close()
+
+
+def test_prefill_attn_batch_refuses_bad_segments(gpu):
+    """Every segment is checked before any launch: a slot outside the pool,
+    positions past the pool's capacity or max_seq are refused with the
+    reference's error kinds, and nothing is written."""
+    import torch
+
+    import qasr_attn
+    from gpu_helpers import Gpu, empty
+
+    g = Gpu(slots=2, cap=512)
+    q = torch.zeros((40, QDIM), dtype=torch.float16, device="cuda")
+    out = empty(40, QDIM)
+    out.fill_(7.0)
+    cases = [([(0, 0, 20), (2, 0, 20)], qasr_attn.QASR_EINVAL),   # slot 2 of 2
+             ([(0, 0, 20), (1, 500, 20)], qasr_attn.QASR_ERANGE),  # past capacity 512
+             ([(0, -1, 20), (1, 0, 20)], qasr_attn.QASR_EINVAL)]   # negative kv_start
+    for segs, code in cases:
+        with pytest.raises(qasr_attn.QasrError) as e:
+            qasr_attn.prefill_attn_batch(g.ctx, g.kv, 0, segs, q, out)
+        assert e.value.code == code, (segs, e.value)
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all()), "a refused call wrote output"
+    g.close()

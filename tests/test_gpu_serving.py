@@ -192,3 +192,33 @@ def test_scheduler_long_prompts_part_only_at_near_ties(weights):
         j = next(k for k in range(min(len(got), len(ids))) if got[k] != ids[k])
         assert margins[j] < 2e-2 * spread, f"segment {g} parts at token {j}, margin {margins[j]}"
     assert same >= len(lens) // 2
+
+
+def test_decoder_prefill_batch_abi_refuses_bad_segments(weights):
+    """The C ABI's own checks (the Python wrapper catches some of these
+    first): a shared slot, an empty segment, more rows than max_rows, more
+    than 64 segments -- each refused with QASR_EINVAL before any launch."""
+    import ctypes
+
+    import torch
+
+    import qasr_attn
+
+    dec = _decoder(weights, 4, max_rows=64)
+    lib = qasr_attn.load()
+    hidden = torch.zeros((80, CFG["hs"]), dtype=torch.float16, device="cuda")
+    nxt = torch.zeros(70, dtype=torch.int32, device="cuda")
+
+    def call(segs):
+        arr = (qasr_attn.Segment * len(segs))(*[qasr_attn.Segment(*sg) for sg in segs])
+        return lib.qasr_decoder_prefill_batch(dec.handle, dec.kv.handle, arr, len(segs),
+                                              ctypes.c_void_p(hidden.data_ptr()),
+                                              ctypes.c_void_p(nxt.data_ptr()), None, None)
+
+    assert call([(0, 0, 10), (0, 0, 10)]) == qasr_attn.QASR_EINVAL
+    assert call([(0, 0, 10), (1, 0, 0)]) == qasr_attn.QASR_EINVAL
+    assert call([(0, 0, 40), (1, 0, 40)]) == qasr_attn.QASR_EINVAL  # 80 rows > max_rows 64
+    assert call([(i % 4, 0, 1) for i in range(65)]) == qasr_attn.QASR_EINVAL
+    assert call([(0, 0, 10), (1, 0, 10)]) == qasr_attn.QASR_OK
+    torch.cuda.synchronize()
+    dec.close()
