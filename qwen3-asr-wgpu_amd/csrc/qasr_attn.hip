@@ -278,6 +278,7 @@ int qasr_ctx_create(const qasr_attn_cfg* cfg, int device, qasr_ctx** out) {
 void qasr_ctx_destroy(qasr_ctx* ctx) {
     if (!ctx) return;
     DeviceScope ds(ctx->device);
+    (void)hipDeviceSynchronize();  // no launch in flight still reads the tables
     if (ctx->cos) (void)hipFree(ctx->cos);
     if (ctx->sin) (void)hipFree(ctx->sin);
     delete ctx;

@@ -504,6 +504,17 @@ class TextDecoder:
         self.last = [0] * slots
         self._tok = torch.zeros(max(slots, 1), dtype=torch.int32, device="cuda")
         self._next = torch.zeros(max(slots, 1), dtype=torch.int32, device="cuda")
+        self._init_feed(slots)
+
+    def _init_feed(self, slots: int):
+        """Device token feed of the pipelined steps (one per slot, written in
+        place by each step) and pinned host copies of their results."""
+        torch = self.t
+        self._feed = torch.zeros(max(slots, 1), dtype=torch.int32, device="cuda")
+        self._feed_slots = None  # the slot order _feed currently holds tokens for
+        self._pinned = [torch.zeros(max(slots, 1), dtype=torch.int32, pin_memory=True)
+                        for _ in range(4)]
+        self._ring = 0
 
     def set_rope_tables(self, cos_u16, sin_u16):
         self.ctx.set_rope_tables(cos_u16, sin_u16)
@@ -525,6 +536,7 @@ class TextDecoder:
         self.last = [0] * slots
         self._tok = torch.zeros(max(slots, 1), dtype=torch.int32, device="cuda")
         self._next = torch.zeros(max(slots, 1), dtype=torch.int32, device="cuda")
+        self._init_feed(slots)
 
     def ensure_capacity(self, need: int) -> int:
         """Grow-only, KV_STEP granular; keeps every row already written."""
@@ -550,6 +562,7 @@ class TextDecoder:
         tok = int(self._next[0].item())
         self.pos[slot] = kv_start + s
         self.last[slot] = tok
+        self._feed_slots = None
         return tok
 
     def prefill_batch(self, items, logits=None):
@@ -619,6 +632,7 @@ class TextDecoder:
         for i, (slot, hidden, start) in enumerate(items):
             self.pos[slot] = start + int(hidden.shape[0])
             self.last[slot] = toks[i]
+        self._feed_slots = None
         return toks
 
     def step_tokens(self, slots: Sequence[int], pos: Sequence[int], tokens_dev, next_dev,
@@ -630,6 +644,40 @@ class TextDecoder:
                                         _i32(pos), _dev(tokens_dev, "tokens", self.t.int32),
                                         _dev(next_dev, "next", self.t.int32), lg,
                                         _stream(stream)))
+
+    def step_async(self, slots: Sequence[int]):
+        """Launch one greedy step of `slots` without waiting for it (the
+        reference's pipelined decode, record_step/submit_step, decoder.rs:
+        2052-2123): each slot's input token comes from the device, where the
+        previous step of the same slots left it, so steps can be queued back to
+        back; a pinned copy of the results lands with an event.  Returns a
+        handle for step_result.  Positions advance at launch."""
+        slots = list(slots)
+        n = len(slots)
+        if any(self.pos[s] >= self.max_seq for s in slots):
+            raise QasrError(QASR_ERANGE, f"decode past max_seq {self.max_seq}")
+        self.ensure_capacity(max(self.pos[s] for s in slots) + 1)
+        if slots != self._feed_slots:
+            self._feed[:n].copy_(self.t.tensor([self.last[s] for s in slots], dtype=self.t.int32))
+            self._feed_slots = slots
+        self.step_tokens(slots, [self.pos[s] for s in slots], self._feed[:n], self._feed[:n])
+        host = self._pinned[self._ring]
+        self._ring = (self._ring + 1) % len(self._pinned)
+        host[:n].copy_(self._feed[:n], non_blocking=True)
+        ev = self.t.cuda.Event()
+        ev.record()
+        for s in slots:
+            self.pos[s] += 1
+        return (slots, host, ev)
+
+    def step_result(self, handle):
+        """The tokens of a step launched by step_async (waits for it)."""
+        slots, host, ev = handle
+        ev.synchronize()
+        toks = host[:len(slots)].tolist()
+        for s, t in zip(slots, toks):
+            self.last[s] = t
+        return toks
 
     def step(self, slots: Optional[Sequence[int]] = None, logits=None):
         """One greedy step of the given slots (default: all); returns their
@@ -643,6 +691,7 @@ class TextDecoder:
         self.step_tokens(slots, [self.pos[s] for s in slots], self._tok[:b], self._next[:b],
                          logits)
         toks = self._next[:b].tolist()
+        self._feed_slots = None
         for s, t in zip(slots, toks):
             self.pos[s] += 1
             self.last[s] = t

@@ -30,6 +30,7 @@ the generated token ids and the stop reason.  The decoder is duck-typed: a
 from __future__ import annotations
 
 import enum
+import os
 import sys
 from dataclasses import dataclass, field
 from typing import List, Optional, Sequence
@@ -76,6 +77,14 @@ class BatchEvents:
         pass
 
 
+def pipelined(decoder) -> bool:
+    """One step in flight (QASR_DEC_PIPE, on unless "0", "off" or "false";
+    pipelined_decode, inference.rs:2431-2439), when the decoder can launch a
+    step without waiting for it (step_async / step_result)."""
+    off = os.environ.get("QASR_DEC_PIPE", "") in ("0", "off", "false")
+    return not off and hasattr(decoder, "step_async")
+
+
 def kv_cap(seq_len: int, max_new: int) -> int:
     """Positions a segment may need: prompt + generation + 8, rounded up to
     KV_STEP (inference.rs:2036, 2127-2131)."""
@@ -118,12 +127,26 @@ def generate(decoder, hidden, max_new: int, eos: Sequence[int] = EOS_IDS) -> Gen
         gen.stop_reason = StopReason.EOS
         return gen
     gen.ids.append(first)
-    for _ in range(1, max_new):
-        tok = decoder.step([0])[0]
+    if not pipelined(decoder):
+        for _ in range(1, max_new):
+            tok = decoder.step([0])[0]
+            if tok in eos:
+                gen.stop_reason = StopReason.EOS
+                break
+            gen.ids.append(tok)
+        return gen
+    # The same max_new - 1 steps, the next one launched before this one's
+    # token is read (inference.rs:2311-2347); a step launched past an EOS is
+    # dropped.
+    h = decoder.step_async([0]) if max_new > 1 else None
+    for i in range(1, max_new):
+        nh = decoder.step_async([0]) if i + 1 < max_new else None
+        tok = decoder.step_result(h)[0]
         if tok in eos:
             gen.stop_reason = StopReason.EOS
             break
         gen.ids.append(tok)
+        h = nh
     return gen
 
 
@@ -210,27 +233,54 @@ def _attempt(decoder, plans, lens, max_news, run, width, eos, events, out):
                     active[s] = g
             frontier[0] += take
 
+    def take(s: int, tok: int) -> bool:
+        """Slot s's next token; True when it ended the slot's segment."""
+        g = active[s]
+        if tok in eos:
+            gen[g].stop_reason = StopReason.EOS
+        elif len(gen[g].ids) >= max_news[g]:
+            gen[g].stop_reason = StopReason.MAX_TOKENS
+        else:
+            gen[g].ids.append(tok)
+            return False
+        active[s] = None
+        out.done(g, gen[g])
+        return True
+
     try:
         fill()
-        while any(a is not None for a in active):
+        if not pipelined(decoder):
+            while any(a is not None for a in active):
+                if events.should_stop():
+                    return "stopped", None
+                live = [s for s in range(nslots) if active[s] is not None]
+                toks = dict(zip(live, decoder.step(live)))
+                for s in live:
+                    if take(s, toks[s]):
+                        fill()
+            return "all", None
+        # One step in flight.  While the live slots stay the same, each step
+        # is launched before the previous one's tokens are read.  When a slot
+        # ends, the step in flight (which still carried it) is read too, its
+        # token for the ended slot dropped, and the slots are refilled before
+        # the next launch.
+        live = [s for s in range(nslots) if active[s] is not None]
+        h = decoder.step_async(live) if live else None
+        while h is not None:
             if events.should_stop():
                 return "stopped", None
-            live = [s for s in range(nslots) if active[s] is not None]
-            toks = dict(zip(live, decoder.step(live)))
-            for s in live:
-                g = active[s]
-                tok = toks[s]
-                if tok in eos:
-                    gen[g].stop_reason = StopReason.EOS
-                    active[s] = None
-                elif len(gen[g].ids) >= max_news[g]:
-                    gen[g].stop_reason = StopReason.MAX_TOKENS
-                    active[s] = None
-                else:
-                    gen[g].ids.append(tok)
-                if active[s] is None:
-                    out.done(g, gen[g])
-                    fill()
+            nh = decoder.step_async(live)
+            ended = False
+            for s, tok in zip(live, decoder.step_result(h)):
+                ended |= take(s, tok)
+            if ended:
+                for s, tok in zip(live, decoder.step_result(nh)):
+                    if active[s] is not None:
+                        take(s, tok)
+                fill()
+                live = [s for s in range(nslots) if active[s] is not None]
+                nh = decoder.step_async(live) if live else None
+            h = nh
     except Exception as e:
         return "failed", e
     return "all", None

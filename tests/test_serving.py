@@ -80,6 +80,31 @@ class FakeDecoder:
         return out
 
 
+class PipeFakeDecoder(FakeDecoder):
+    """The same scripted decoder with the pipelined interface: step_async
+    launches a step (the tokens are fixed at launch, as the device feedback
+    fixes them), step_result hands them over; at most two steps in flight."""
+
+    def __init__(self, *a, **k):
+        super().__init__(*a, **k)
+        self.in_flight = 0
+        self.max_in_flight = 0
+
+    def reset_pool(self, slots, cap):
+        super().reset_pool(slots, cap)
+        self.in_flight = 0  # a new pool waits for every step in flight
+
+    def step_async(self, slots):
+        toks = self.step(slots)
+        self.in_flight += 1
+        self.max_in_flight = max(self.max_in_flight, self.in_flight)
+        return (list(slots), toks)
+
+    def step_result(self, handle):
+        self.in_flight -= 1
+        return handle[1]
+
+
 def _hidden(g, rows):
     h = np.zeros((rows, 4), np.float32)
     h[0, 0] = g
@@ -127,11 +152,15 @@ def _fill_filler(scripts, plans, max_news):
     return [sc + [1000 + g] * (max_news[g] + 2) for g, sc in enumerate(scripts)]
 
 
+@pytest.mark.parametrize("pipe", [False, True])
 @pytest.mark.parametrize("width", [1, 2, 3, 8, 16, 64])
-def test_every_width_gives_the_single_path_tokens(width):
+def test_every_width_gives_the_single_path_tokens(width, pipe):
     plans, max_news, scripts = _case(1, 37)
     scripts = _fill_filler(scripts, plans, max_news)
-    res = S.decode_batch(FakeDecoder(scripts), plans, max_news, width)
+    dec = PipeFakeDecoder(scripts) if pipe else FakeDecoder(scripts)
+    res = S.decode_batch(dec, plans, max_news, width)
+    if pipe:
+        assert dec.max_in_flight == 2 and dec.in_flight <= 1
     for g, r in enumerate(res):
         ids, stop = _single_expected(scripts[g], max_news[g])
         assert r.ids == ids, g
@@ -139,10 +168,11 @@ def test_every_width_gives_the_single_path_tokens(width):
         assert r.stop_reason == want_stop, g
 
 
-def test_single_path_generate_matches_reference_loop():
+@pytest.mark.parametrize("pipe", [False, True])
+def test_single_path_generate_matches_reference_loop(pipe):
     plans, max_news, scripts = _case(2, 12)
     scripts = _fill_filler(scripts, plans, max_news)
-    dec = FakeDecoder(scripts)
+    dec = PipeFakeDecoder(scripts) if pipe else FakeDecoder(scripts)
     for g in range(12):
         r = S.generate(dec, plans[g], max_news[g])
         assert (r.ids, r.stop_reason) == _single_expected(scripts[g], max_news[g])
@@ -195,6 +225,17 @@ def test_width_halves_until_the_pool_fits():
     dec = FakeDecoder(scripts, fail_slots_above=5)
     res = S.decode_batch(dec, plans, max_news, 16)
     assert [p[0] for p in dec.pools] == [4]
+    for g, r in enumerate(res):
+        assert r.ids == _single_expected(scripts[g], max_news[g])[0]
+
+
+def test_pipelining_can_be_switched_off(monkeypatch):
+    plans, max_news, scripts = _case(7, 9)
+    scripts = _fill_filler(scripts, plans, max_news)
+    monkeypatch.setenv("QASR_DEC_PIPE", "off")
+    dec = PipeFakeDecoder(scripts)
+    res = S.decode_batch(dec, plans, max_news, 4)
+    assert dec.max_in_flight == 0
     for g, r in enumerate(res):
         assert r.ids == _single_expected(scripts[g], max_news[g])[0]
 
