@@ -222,3 +222,52 @@ def test_decoder_prefill_batch_abi_refuses_bad_segments(weights):
     assert call([(0, 0, 10), (1, 0, 10)]) == qasr_attn.QASR_OK
     torch.cuda.synchronize()
     dec.close()
+
+
+def test_pipelined_steps_equal_synchronous_steps(weights):
+    """step_async / step_result (tokens fed back on the device, one step in
+    flight) give the synchronous step()'s tokens, step for step."""
+    prompts = [_prompt(SEED_BASE + 1160 + i, 20 + 13 * i) for i in range(3)]
+    runs = []
+    for mode in ("sync", "pipelined"):
+        dec = _decoder(weights, 3)
+        dec.prefill_batch([(i, h) for i, h in enumerate(prompts)])
+        toks = []
+        if mode == "sync":
+            for _ in range(12):
+                toks.append(dec.step())
+        else:
+            h = dec.step_async([0, 1, 2])
+            for k in range(12):
+                nh = dec.step_async([0, 1, 2]) if k + 1 < 12 else None
+                toks.append(dec.step_result(h))
+                h = nh
+        runs.append((toks, list(dec.pos)))
+        dec.close()
+    assert runs[0] == runs[1]
+
+
+def test_int8_prefill_batch_equals_dequantized_f16(weights):
+    """Int8 projections through the batched prefill (more than 16 rows: the
+    layer's matrix dequantised for rocBLAS) against f16 weights dequantised
+    on the host: identical tokens and logits, bitwise."""
+    import torch
+
+    W8, Wdq = dict(weights), dict(weights)
+    for key in list(weights):
+        if isinstance(key, tuple) and key[1].endswith("_proj"):
+            w = weights[key].float()
+            s = (w.abs().amax(dim=1) / 127.0).clamp_min(1e-8)
+            q = torch.round(w / s[:, None]).clamp(-128, 127).to(torch.int8)
+            W8[key], W8[(key[0], key[1] + "_scale")] = q, s
+            Wdq[key] = (q.float() * s[:, None]).half()
+    prompts = [_prompt(SEED_BASE + 1170 + i, n) for i, n in enumerate((30, 50, 20))]
+    out = []
+    for W in (W8, Wdq):
+        dec = _decoder(W, 3)
+        lg = torch.empty((3, CFG["vocab"]), dtype=torch.float32, device="cuda")
+        toks = dec.prefill_batch([(i, h) for i, h in enumerate(prompts)], logits=lg)
+        out.append((toks, lg.cpu().numpy()))
+        dec.close()
+    assert out[0][0] == out[1][0]
+    assert np.array_equal(out[0][1], out[1][1])
