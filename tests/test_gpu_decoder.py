@@ -320,7 +320,9 @@ def test_int8_projections_equal_dequantized_f16(gpu, model, batch, blas, monkeyp
 
 
 @pytest.mark.parametrize("model,batch,int8", [("1.7B", 16, False), ("0.6B", 1, False),
-                                              ("1.7B", 16, True), ("0.6B", 5, True)])
+                                              ("0.6B", 3, False), ("1.7B", 2, False),
+                                              ("1.7B", 16, True), ("0.6B", 5, True),
+                                              ("0.6B", 4, True)])
 def test_fused_epilogues_equal_unfused(gpu, model, batch, int8, monkeypatch):
     """The decode step's fused epilogues (gate|up with SiLU * up in one skinny
     launch) against the same step with them off (QASR_DECODER_FUSE=0:
