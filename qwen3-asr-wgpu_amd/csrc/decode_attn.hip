@@ -48,6 +48,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kNegInf = -__builtin_inff();
 constexpr int kSc1 = 16;  // buffer cache policy: sc1 (device-coherent, as agent-scope atomics)
+// Buffer cache policy nt (non-temporal) for the K/V stream: each byte is read
+// once per launch, and streaming it with the default policy measured 7-9%
+// slower (config 3: 23.3 against 21.7 us; 16 x 2048 keys: 29.2 against 26.5).
+constexpr int kNt = 2;
 
 __device__ __forceinline__ float dot8(const H8& a, const H8& b) {
     float s = 0.0f;
@@ -64,13 +68,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int b
 }
 
 // One wave pass (32 keys from t0) of K or V: 8 x 16 B per lane; load kk
-// covers keys t0 + 4*kk .. +4 (this lane: key t0 + 4*kk + row).
+// covers keys t0 + 4*kk .. +4 (this lane: key t0 + 4*kk + row).  Non-temporal.
 __device__ __forceinline__ void load_pass(__amdgpu_buffer_rsrc_t r, int t0, int row, int seg,
                                           H8 (&x)[8]) {
     const int voff = (t0 + row) * (kHeadDim * 2) + seg * 16;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + kk * 1024, 0, 0);
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + kk * 1024, 0, kNt);
         x[kk].u = make_uint4(v.x, v.y, v.z, v.w);
     }
 }
