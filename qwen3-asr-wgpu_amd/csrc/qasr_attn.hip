@@ -138,7 +138,9 @@ int ensure_prefill_ws(qasr_kv* kv, int64_t items) {
 }
 
 // Decode launch plan: a fixed number of workgroups (QASR_DECODE_WGS, default
-// two per CU: every CU then carries the same number of workgroups), whose
+// one per CU: every CU then carries the same number of workgroups; with the
+// K/V stream's non-temporal loads one per CU measured 1.3% faster than two
+// at 16 slots, and equal at 64), whose
 // chunks are as even as possible.  Entry b is cut into n_b equal chunks of
 // whole 32-key passes; starting from one chunk per entry, the entry with the
 // largest chunk gets one more until the workgroup budget is used (and the
@@ -151,7 +153,7 @@ int chunk_of(int L, int n) {
 }
 
 void plan_decode_chunks(qasr::DecodePlan& P, int nkvh, int cus) {
-    const int target = std::max(1, std::min(env_int("QASR_DECODE_WGS", 2 * cus), 4096));
+    const int target = std::max(1, std::min(env_int("QASR_DECODE_WGS", cus), 4096));
     const int min_chunk = std::max(32, env_int("QASR_DECODE_MIN_CHUNK", qasr::kDecodeMinChunk));
     const int max_split = std::max(1, std::min(env_int("QASR_DECODE_MAX_SPLIT", qasr::kDecodeMaxSplit),
                                                qasr::kDecodeMaxChunksPerEntry));
