@@ -17,7 +17,9 @@ the reference CPU path (the C++ restatement of cpu_decoder.rs in oracle/)
 timed on a bounded sample of config 3 on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
-                       [--only decode3|decode1|decode4|decode5|prefill2|prefill4]
+                       [--only decode3|decode1|decode4|decode5|decode16x2k|prefill2|prefill4|
+                               config4_whole|streamread|copycal|decoder16|decoder1|
+                               decoder16_int8|decoder1_int8|serving|prefill_batch|prefill_one]
 """
 from __future__ import annotations
 
@@ -193,6 +195,109 @@ def copy_calibration(steps: int):
     ms = start.elapsed_time(end) / max(1, steps)
     return {"bytes_read": x.numel() * 2, "bytes_written": y.numel() * 2, "ms": ms,
             "GBps_rw": 2 * x.numel() * 2 / (ms * 1e-3) / 1e9}
+
+
+def stream_read_calibration(nbytes: int, steps: int, warmup: int, copies: int = LAYERS,
+                            shapes=((256, 4), (256, 8), (512, 4), (512, 8), (1024, 4))):
+    """A bare streaming read of `nbytes` per launch (config 3's decode bytes
+    by default) by qasr_stream_read: non-temporal dwordx4 buffer loads as in
+    the decode kernel, one contiguous share per workgroup, no compute.
+    `copies` distinct buffers rotate (2.6 GB at config 3, beyond the 256 MB
+    Infinity Cache), 28 launches per HIP-graph replay as in bench_decode.
+    Returns the time per launch for each (workgroups, waves) shape: what HBM
+    delivers to one launch of this size, the ceiling the decode kernel's
+    bandwidth is read against."""
+    import torch
+
+    import qasr_attn
+
+    ctx = qasr_attn.Context(NQH, NKVH, HD, LAYERS, 1e-6, 16384, 0)
+    out = {"bytes_per_launch": None, "copies": copies, "shapes": {}}
+    best = None
+    for wgs, waves in shapes:
+        per = -(-nbytes // (wgs * 16)) * 16
+        total = per * wgs
+        out["bytes_per_launch"] = total
+        bufs = [torch.empty(total // 2, dtype=torch.float16, device="cuda").normal_()
+                for _ in range(copies)]
+        sink = torch.empty(wgs * waves, dtype=torch.int32, device="cuda")
+
+        def step():
+            for b in bufs:
+                qasr_attn.stream_read(ctx, b, wgs, waves, sink)
+
+        ms, graph = graph_time(torch, step, steps, warmup)
+        del graph
+        us = ms * 1e3 / copies
+        gbs = total / (us * 1e-6) / 1e9
+        out["shapes"][f"{wgs}x{waves}"] = {"us_per_launch": round(us, 3), "GBps": round(gbs, 1),
+                                           "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        if best is None or us < best[0]:
+            best = (us, gbs, f"{wgs}x{waves}")
+        del bufs
+        torch.cuda.empty_cache()
+    ctx.close()
+    out["best"] = {"shape": best[2], "us_per_launch": round(best[0], 3), "GBps": round(best[1], 1),
+                   "frac_of_peak": round(best[1] / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def bench_config4_whole(steps: int, warmup: int, layers: int = LAYERS, decode_steps: int = 64):
+    """Config 4 as its workload states it: per layer (each on its own cache),
+    16 chunked prefills of 512 rows at kv_start = 0, 512, .., 7680 (stage (a)
+    + attention per chunk), then 64 decode steps at positions 8192..8255
+    (fused stage (a)+(b)).  One replay = the prefill phase of all 28 layers
+    chunk by chunk, then the decode phase step by step (layer-major inside a
+    step, as a decoder runs them); both phases are timed separately."""
+    import torch
+
+    chunks, chunk, ctx_len = 16, 512, 8192
+    st = Setup(1, cap_for(ctx_len + decode_steps), layers)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(97)
+    qkv = torch.randn((layers, ctx_len, TOT), device="cuda", generator=g).half()
+    qw = torch.empty((layers, chunk, QDIM), device="cuda", dtype=torch.float16)
+    out = torch.empty((layers, chunk, QDIM), device="cuda", dtype=torch.float16)
+    dq = torch.randn((decode_steps, layers, 1, TOT), device="cuda", generator=g).half()
+    dout = torch.empty((layers, 1, QDIM), device="cuda", dtype=torch.float16)
+
+    def prefill_phase():
+        for c in range(chunks):
+            for l in range(layers):
+                st.q.prefill_layer(st.ctx, st.kv, l, 0, c * chunk, chunk,
+                                   qkv[l, c * chunk:(c + 1) * chunk], st.gains[l, 0],
+                                   st.gains[l, 1], qw[l], out[l])
+
+    def decode_phase():
+        for t in range(decode_steps):
+            for l in range(layers):
+                st.q.decode_step(st.ctx, st.kv, l, [ctx_len + t], dq[t, l], st.gains[l, 0],
+                                 st.gains[l, 1], dout[l])
+
+    ms_p, g1 = graph_time(torch, prefill_phase, steps, warmup)
+    ms_d, g2 = graph_time(torch, decode_phase, steps, warmup)
+    del g1, g2
+    st.close()
+    fl = sum(prefill_flops(chunk, c * chunk) for c in range(chunks)) * layers
+    dbytes = sum(decode_bytes([ctx_len + t + 1]) for t in range(decode_steps)) * layers
+    return {"prefill_ms": ms_p, "prefill_TFLOPs_attention_and_stage_a": fl / (ms_p * 1e-3) / 1e12,
+            "prefill_us_per_layer_chunk": ms_p * 1e3 / (layers * chunks),
+            "decode_ms": ms_d, "decode_us_per_layer_step": ms_d * 1e3 / (layers * decode_steps),
+            "decode_GBps": dbytes / (ms_d * 1e-3) / 1e9, "total_ms": ms_p + ms_d,
+            "layers": layers, "chunks": chunks, "decode_steps": decode_steps}
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
 
 
 DECODERS = {"0.6B": dict(hs=1024, inter=3072), "1.7B": dict(hs=2048, inter=6144)}
@@ -406,7 +511,7 @@ def cpu_baseline(lengths, budget_s: float = 10.0):
     med = float(np.median(times))
     nbytes = decode_bytes([L + 1 for L in lengths])
     return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "us_per_layer": med * 1e6,
+            "us_per_layer": med * 1e6, "cpu_model": cpu_model(),
             "sample": f"config 3 decode layer-steps (16 slots, lengths as the GPU run), "
                       f"{len(times)} reps over ~{budget_s:.0f} s, median; oracle/oracle.cpp "
                       f"(C++ restatement of cpu_decoder.rs:274-423, f32), {threads} threads"}
@@ -446,6 +551,8 @@ def main():
             "prefill2": lambda: bench_prefill(420, 0, K, W),
             "prefill4": lambda: bench_prefill(512, 7680, K, W),
             "copycal": lambda: copy_calibration(K),
+            "streamread": lambda: stream_read_calibration(decode_bytes([L + 1 for L in lens3]), K, W),
+            "config4_whole": lambda: bench_config4_whole(max(3, K // 10), 1),
             "decoder16": lambda: bench_text_decoder("1.7B", lens3, K, W),
             "decoder1": lambda: bench_text_decoder("0.6B", [511], K, W),
             "decoder16_int8": lambda: bench_text_decoder("1.7B", lens3, K, W, int8=True),
@@ -469,11 +576,16 @@ def main():
         log("[bench] config 4 (last 512-row chunk at kv_start 7680; decode at 8192)")
         extra["config4_prefill_last_chunk"] = bench_prefill(512, 7680, K, W)
         extra["config4_decode"] = bench_decode(1, [8192], K, W)
+        log("[bench] config 4 whole workload (16 chunked prefills + 64 decode steps, 28 layers)")
+        extra["config4_whole_workload"] = bench_config4_whole(max(3, K // 10), 1)
         log("[bench] config 5")
         lens5 = splitmix_lengths(SEED_BASE + 5, 64, 64, 4096)
         extra["config5_decode"] = bench_decode(64, lens5, max(5, K // 5), W)
         log("[bench] 16 slots at a uniform 2048-token context (the target's ~2k context)")
         extra["decode_16slots_2k_context"] = bench_decode(16, [2048] * 16, K, W)
+        log("[bench] streaming-read calibration at config 3's bytes per launch")
+        extra["streamread_config3_bytes"] = stream_read_calibration(
+            decode_bytes([L + 1 for L in lens3]), K, W)
         log("[bench] text decoder steps (whole decoder around the attention path)")
         extra["text_decoder_1p7b_16slots"] = bench_text_decoder("1.7B", lens3, K, W)
         extra["text_decoder_0p6b_1slot"] = bench_text_decoder("0.6B", [511], K, W)

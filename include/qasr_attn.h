@@ -273,6 +273,27 @@ int qasr_decoder_prefill_batch(qasr_decoder* dec, qasr_kv* kv, const qasr_segmen
 int qasr_dequant_i8(qasr_ctx* ctx, const void* q_dev, const float* scale_dev, int64_t rows,
                     int32_t cols, void* out_dev, void* stream);
 
+/* Diagnostic: the attention kernels' softmax weight for scores s_dev[i]
+ * against row maxima m_dev[i] (f32, device, n each; m >= s), in both forms
+ * the kernels use: out_scaled_dev[i] = 2^(f32(s*sl2) - f32(m*sl2)) (decode)
+ * and out_raw_dev[i] = 2^(fma(s, sl2, -f32(m*sl2))) (prefill), where sl2 =
+ * the context's softmax scale times log2(e).  The reference forms
+ * expf(f32(s*scale) - f32(m*scale)) (cpu_decoder.rs:292-365); this entry
+ * exists so tests can measure the difference.  No counterpart in the
+ * reference. */
+int qasr_softmax_weights(qasr_ctx* ctx, const float* s_dev, const float* m_dev, int64_t n,
+                         float* out_scaled_dev, float* out_raw_dev, void* stream);
+
+/* Calibration: a bare streaming read of `bytes` bytes at src_dev (device)
+ * by `wgs` workgroups of `waves` waves, each reading one contiguous share
+ * with the decode kernel's load form (non-temporal dwordx4 buffer loads);
+ * sink_dev receives one word per wave (wgs * waves uint32).  bytes must be a
+ * multiple of 16 * wgs.  Measures what the memory system delivers to one
+ * launch of a given size, against which the decode kernel's bandwidth is
+ * read.  No counterpart in the reference. */
+int qasr_stream_read(qasr_ctx* ctx, const void* src_dev, int64_t bytes, int wgs, int waves,
+                     uint32_t* sink_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -425,6 +425,14 @@ int qo_layer_attn(const qo_shape* sh, int cap, const uint16_t* qkv, int rows, in
 
 // cpu_decoder.rs:228 / decoder.rs:1610: grow-only, KV_STEP (256) granular,
 // clamped to max_seq.
+void qo_softmax_weights(const float* s, const float* m, int64_t n, float scale, float* out) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float st = s[i] * scale;    // s = dot * scale
+        const float best = m[i] * scale;  // the row's largest s
+        out[i] = std::exp(st - best);     // (s - best).exp()
+    }
+}
+
 int qo_kv_target_cap(int need, int cap, int max_seq) {
     const int step = 256;
     int64_t t = ((int64_t)need + step - 1) / step * step;

@@ -99,6 +99,12 @@ int32_t qo_uniform_int(uint64_t* state, int32_t lo, int32_t hi); /* inclusive */
 
 int qo_hardware_threads(void);
 
+/* Softmax weight of the reference attention (cpu_decoder.rs:292-365) for a
+ * raw dot product s against the row's largest dot m: out[i] =
+ * expf(f32(s*scale) - f32(m*scale)), glibc expf, each operation rounded as
+ * the Rust source rounds it. */
+void qo_softmax_weights(const float* s, const float* m, int64_t n, float scale, float* out);
+
 /* ---- the whole text decoder for one sequence (cpu_decoder.rs) -----------
  * CpuTextDecoder restated for the end-to-end greedy check: rms_norm_row
  * 261-272, forward 367-456 (q/k/v/o/gate/up/down with dot_transposed's

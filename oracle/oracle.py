@@ -100,6 +100,8 @@ def lib():
         L.qo_uniform_int.restype = ctypes.c_int32
         L.qo_uniform_int.argtypes = [_u64p, ctypes.c_int32, ctypes.c_int32]
         L.qo_hardware_threads.restype = ctypes.c_int
+        L.qo_softmax_weights.argtypes = [_f32p, _f32p, ctypes.c_int64, ctypes.c_float, _f32p]
+        L.qo_softmax_weights.restype = None
         _lib = L
     return _lib
 
@@ -222,6 +224,17 @@ def attention(shape: Shape, cap: int, q, q0: int, k_cache, v_cache, nthreads: in
                             _p(k_cache, _f32p), _p(v_cache, _f32p), _p(out, _u16p), nthreads)
     if rc != 0:
         raise ValueError("qo_attention rejected its arguments")
+    return out
+
+
+def softmax_weights(s, m, scale: float) -> np.ndarray:
+    """expf(f32(s*scale) - f32(m*scale)) per element (glibc expf), the
+    reference attention's softmax weight (cpu_decoder.rs:292-365)."""
+    s = np.ascontiguousarray(s, dtype=np.float32)
+    m = np.ascontiguousarray(m, dtype=np.float32)
+    assert s.shape == m.shape
+    out = np.empty(s.shape, np.float32)
+    lib().qo_softmax_weights(_p(s, _f32p), _p(m, _f32p), s.size, scale, _p(out, _f32p))
     return out
 
 

@@ -93,6 +93,20 @@ __device__ __forceinline__ void fma_mix_hi(float& acc, float p, uint32_t pk) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Softmax weights in the exp2 domain.  The reference forms
+// e = expf(s*scale - max*scale) (cpu_decoder.rs:292-365); the kernels fold
+// log2(e) into the scale (sl2 = scale*log2(e), rounded once on the host) and
+// exponentiate with v_exp_f32:
+//  - decode keeps scores pre-multiplied (s2 = s*sl2) and its running max in
+//    that domain (m2): w = 2^(s2 - m2);
+//  - prefill keeps raw scores and folds the multiply into one FMA against
+//    the scaled max: w = 2^(fma(s, sl2, -m2)).
+// qasr_softmax_weights evaluates both forms for the tests against glibc expf.
+__device__ __forceinline__ float softmax_w_scaled(float s2, float m2) { return fast_exp2(s2 - m2); }
+__device__ __forceinline__ float softmax_w_raw(float s, float sl2, float m2) {
+    return fast_exp2(fmaf(s, sl2, -m2));
+}
+
 // ---- publishing partial results to other workgroups ---------------------
 // MI355X has one L2 per XCD and they are not coherent with each other inside
 // a kernel.  An agent-scope release/acquire fence would write back and

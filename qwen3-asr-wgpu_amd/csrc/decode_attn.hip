@@ -250,8 +250,8 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
         mt = fmaxf(mt, dpp<kDppRor8>(mt));
         const float mn = fmaxf(m_run, mt);
         const float mu = mn == kNegInf ? 0.0f : mn;
-        const float alpha = fast_exp2(m_run - mu);
-        const float pv = fast_exp2(sv - mu);
+        const float alpha = softmax_w_scaled(m_run, mu);
+        const float pv = softmax_w_scaled(sv, mu);
         m_run = mn;
         float ps = pv + dpp<kDppXor2>(pv);
         ps += dpp<kDppRor4>(ps);

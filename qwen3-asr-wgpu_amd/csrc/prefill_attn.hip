@@ -202,7 +202,7 @@ __device__ __forceinline__ void step_s(Wave& w, const f16* kt, int k0, half8v (&
     for (int w4 = 0; w4 < 4; ++w4)
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-            pb[w4][j] = (f16)fast_exp2(fmaf(s[w4 >> 1][8 * (w4 & 1) + j], w.scale_log2, -mu));
+            pb[w4][j] = (f16)softmax_w_raw(s[w4 >> 1][8 * (w4 & 1) + j], w.scale_log2, mu);
     const half2v ones2 = {(f16)1.0f, (f16)1.0f};
     float ps = 0.0f;
 #pragma unroll

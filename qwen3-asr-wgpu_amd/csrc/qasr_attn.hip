@@ -339,6 +339,7 @@ int qasr_set_rope_tables(qasr_ctx* ctx, const uint16_t* cos_f16, const uint16_t*
     DeviceScope ds(ctx->device);
     if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
     const size_t bytes = (size_t)rows * ctx->cfg.head_dim * sizeof(uint16_t);
+    HIP_TRY(hipDeviceSynchronize(), "rope tables sync");  // no launch in flight reads the old ones
     if (ctx->cos) (void)hipFree(ctx->cos);
     if (ctx->sin) (void)hipFree(ctx->sin);
     ctx->cos = ctx->sin = nullptr;
@@ -423,6 +424,11 @@ int qasr_kv_ensure_capacity(qasr_kv* kv, int need, int keep_rows, int* cap_out) 
     tmp.cap = target;
     const qasr::CacheGeom ng = geom(&tmp);
     const size_t nbytes = (size_t)ng.slot_stride * kv->slots * sizeof(f16);
+    // Work queued on any stream (a step still appending row pos-1 on a
+    // non-blocking stream, say) completes before the rows are copied: the
+    // copy below runs on the null stream, which does not order non-blocking
+    // streams.
+    HIP_TRY(hipDeviceSynchronize(), "KV pool growth sync");
     f16* nb = nullptr;
     HIP_TRY(hipMalloc(&nb, nbytes), "KV pool growth");
     hipError_t e = hipMemset(nb, 0, nbytes);

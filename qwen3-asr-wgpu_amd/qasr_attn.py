@@ -37,6 +37,7 @@ ABI_SYMBOLS = (
     "qasr_decode_attn", "qasr_decode_step", "qasr_prefill_attn", "qasr_prefill_layer",
     "qasr_decoder_create", "qasr_decoder_destroy", "qasr_decoder_step", "qasr_decoder_prefill",
     "qasr_decoder_prefill_batch", "qasr_dequant_i8", "qasr_prefill_attn_batch",
+    "qasr_softmax_weights", "qasr_stream_read",
 )
 MAX_PREFILL_SEGMENTS = 64  # segments per qasr_decoder_prefill_batch call
 
@@ -144,6 +145,8 @@ def load(path: str = LIB_PATH):
     L.qasr_decoder_prefill_batch.argtypes = [_vp, _vp, ctypes.POINTER(Segment), ctypes.c_int, _vp,
                                              _vp, _vp, _vp]
     L.qasr_dequant_i8.argtypes = [_vp, _vp, _vp, ctypes.c_int64, ctypes.c_int32, _vp, _vp]
+    L.qasr_softmax_weights.argtypes = [_vp, _vp, _vp, ctypes.c_int64, _vp, _vp, _vp]
+    L.qasr_stream_read.argtypes = [_vp, _vp, ctypes.c_int64, ctypes.c_int, ctypes.c_int, _vp, _vp]
     _lib = L
     return L
 
@@ -196,6 +199,20 @@ def _dev(t, name: str, dtype=None) -> int:
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
     return t.data_ptr()
+
+
+def _need(t, elems: int, name: str, exact: bool = False):
+    """The C ABI receives raw device pointers: a tensor smaller than the rows
+    the call implies would be read or written out of bounds, so it is refused
+    here, before any launch, with the library's EINVAL."""
+    n = int(t.numel())
+    if n < elems or (exact and n != elems):
+        raise QasrError(QASR_EINVAL, f"{name} holds {n} elements, the call needs "
+                                     f"{'exactly ' if exact else ''}{elems}")
+
+
+def _rows_of(segments) -> int:
+    return sum(int(r) for _, _, r in segments)
 
 
 class Context:
@@ -307,8 +324,24 @@ class _DeviceView:
 
 # ---- stage entry points (thin wrappers over the C ABI) --------------------
 
+def _widths(ctx: Context):
+    """(fused qkv row, q/out row) widths in elements for this context."""
+    hd = ctx.cfg.head_dim
+    return (ctx.nqh + 2 * ctx.nkvh) * hd, ctx.nqh * hd
+
+
+def _gains(ctx: Context, q_gain, k_gain):
+    _need(q_gain, ctx.cfg.head_dim, "q_gain", exact=True)
+    _need(k_gain, ctx.cfg.head_dim, "k_gain", exact=True)
+
+
 def qk_norm_rope_append(ctx: Context, kv: KVPool, layer: int, segments, qkv, q_gain, k_gain,
                         q_out, stream=None):
+    tot, qd = _widths(ctx)
+    rows = _rows_of(segments)
+    _need(qkv, rows * tot, "qkv")
+    _need(q_out, rows * qd, "q_out")
+    _gains(ctx, q_gain, k_gain)
     segs = (Segment * len(segments))(*[Segment(int(s), int(p), int(r)) for s, p, r in segments])
     _check(load().qasr_qk_norm_rope_append(
         ctx.handle, kv.handle, layer, segs, len(segments), _dev(qkv, "qkv"),
@@ -317,6 +350,11 @@ def qk_norm_rope_append(ctx: Context, kv: KVPool, layer: int, segments, qkv, q_g
 
 def decode_attn(ctx: Context, kv: KVPool, layer: int, cur_len, q, out, slots=None, stream=None):
     b = len(cur_len)
+    _, qd = _widths(ctx)
+    _need(q, b * qd, "q")
+    _need(out, b * qd, "out")
+    if slots is not None and len(slots) != b:
+        raise QasrError(QASR_EINVAL, f"{len(slots)} slots for {b} entries")
     _check(load().qasr_decode_attn(ctx.handle, kv.handle, layer, b,
                                    _i32(slots) if slots is not None else None, _i32(cur_len),
                                    _dev(q, "q"), _dev(out, "out"), _stream(stream)))
@@ -325,6 +363,12 @@ def decode_attn(ctx: Context, kv: KVPool, layer: int, cur_len, q, out, slots=Non
 def decode_step(ctx: Context, kv: KVPool, layer: int, pos, qkv, q_gain, k_gain, out, slots=None,
                 stream=None):
     b = len(pos)
+    tot, qd = _widths(ctx)
+    _need(qkv, b * tot, "qkv")
+    _need(out, b * qd, "out")
+    _gains(ctx, q_gain, k_gain)
+    if slots is not None and len(slots) != b:
+        raise QasrError(QASR_EINVAL, f"{len(slots)} slots for {b} entries")
     _check(load().qasr_decode_step(ctx.handle, kv.handle, layer, b,
                                    _i32(slots) if slots is not None else None, _i32(pos),
                                    _dev(qkv, "qkv"), _dev(q_gain, "q_gain"),
@@ -333,6 +377,9 @@ def decode_step(ctx: Context, kv: KVPool, layer: int, pos, qkv, q_gain, k_gain, 
 
 def prefill_attn(ctx: Context, kv: KVPool, layer: int, slot: int, kv_start: int, s: int, q, out,
                  stream=None):
+    _, qd = _widths(ctx)
+    _need(q, max(s, 0) * qd, "q")
+    _need(out, max(s, 0) * qd, "out")
     _check(load().qasr_prefill_attn(ctx.handle, kv.handle, layer, slot, kv_start, s,
                                     _dev(q, "q"), _dev(out, "out"), _stream(stream)))
 
@@ -341,6 +388,10 @@ def prefill_attn_batch(ctx: Context, kv: KVPool, layer: int, segments, q, out, s
     """Stage (c) for segments [(slot, kv_start, rows)] whose q rows (and
     output rows) are concatenated in order; one launch where the key ranges
     are short."""
+    _, qd = _widths(ctx)
+    rows = _rows_of(segments)
+    _need(q, rows * qd, "q")
+    _need(out, rows * qd, "out")
     segs = (Segment * len(segments))(*[Segment(int(s), int(p), int(r)) for s, p, r in segments])
     _check(load().qasr_prefill_attn_batch(ctx.handle, kv.handle, layer, segs, len(segments),
                                           _dev(q, "q"), _dev(out, "out"), _stream(stream)))
@@ -348,6 +399,11 @@ def prefill_attn_batch(ctx: Context, kv: KVPool, layer: int, segments, q, out, s
 
 def prefill_layer(ctx: Context, kv: KVPool, layer: int, slot: int, kv_start: int, s: int, qkv,
                   q_gain, k_gain, q_work, out, stream=None):
+    tot, qd = _widths(ctx)
+    _need(qkv, max(s, 0) * tot, "qkv")
+    _need(q_work, max(s, 0) * qd, "q_work")
+    _need(out, max(s, 0) * qd, "out")
+    _gains(ctx, q_gain, k_gain)
     _check(load().qasr_prefill_layer(ctx.handle, kv.handle, layer, slot, kv_start, s,
                                      _dev(qkv, "qkv"), _dev(q_gain, "q_gain"),
                                      _dev(k_gain, "k_gain"), _dev(q_work, "q_work"),
@@ -410,13 +466,46 @@ def dequant_i8(ctx: Context, q, scale, out=None):
     reference's dequant_i8, weights.rs:366-385), on the GPU."""
     import torch
 
+    if q.dim() != 2:
+        raise QasrError(QASR_EINVAL, "q must be a [rows][cols] int8 matrix")
     rows, cols = int(q.shape[0]), int(q.shape[1])
+    _need(scale, rows, "scale", exact=True)
     if out is None:
         out = torch.empty((rows, cols), dtype=torch.float16, device=q.device)
+    _need(out, rows * cols, "out", exact=True)
     _check(load().qasr_dequant_i8(ctx.handle, _dev(q, "q", torch.int8),
                                   _dev(scale, "scale", torch.float32), rows, cols,
                                   _dev(out, "out"), _stream(None)))
     return out
+
+
+def softmax_weights(ctx: Context, s, m):
+    """The attention kernels' softmax weights for scores s against maxima m
+    (f32 CUDA tensors of one size): (decode form, prefill form), each
+    2^(s*scale*log2(e) - m*scale*log2(e)) as that kernel rounds it."""
+    import torch
+
+    n = int(s.numel())
+    _need(m, n, "m", exact=True)
+    a = torch.empty_like(s)
+    b = torch.empty_like(s)
+    _check(load().qasr_softmax_weights(ctx.handle, _dev(s, "s", torch.float32),
+                                       _dev(m, "m", torch.float32), n,
+                                       _dev(a, "out_scaled", torch.float32),
+                                       _dev(b, "out_raw", torch.float32), _stream(None)))
+    return a, b
+
+
+def stream_read(ctx: Context, src, wgs: int, waves: int, sink, stream=None):
+    """Bare streaming read of a whole CUDA tensor (calibration, see
+    qasr_stream_read); sink: int32 CUDA tensor of >= wgs * waves entries."""
+    import torch
+
+    if not src.is_cuda or not src.is_contiguous():
+        raise ValueError("src must be a contiguous CUDA tensor")
+    _need(sink, wgs * waves, "sink")
+    _check(load().qasr_stream_read(ctx.handle, src.data_ptr(), src.numel() * src.element_size(),
+                                   wgs, waves, _dev(sink, "sink", torch.int32), _stream(stream)))
 
 
 LAYER_WEIGHT_NAMES = ("input_layernorm", "q_proj", "k_proj", "v_proj", "q_norm", "k_norm",
@@ -519,6 +608,11 @@ class TextDecoder:
     def set_rope_tables(self, cos_u16, sin_u16):
         self.ctx.set_rope_tables(cos_u16, sin_u16)
 
+    def _check_hidden(self, hidden):
+        if hidden.dim() != 2 or int(hidden.shape[1]) != self.hs:
+            raise QasrError(QASR_EINVAL, f"hidden must be [rows][{self.hs}], got "
+                                         f"{list(hidden.shape)}")
+
     @property
     def slots(self) -> int:
         return len(self.pos)
@@ -546,6 +640,9 @@ class TextDecoder:
         """hidden: [s][hs] f16 CUDA tensor; prefilled in chunks of max_rows
         rows.  Returns the argmax token after the last row (and fills
         `logits`, a [vocab] f32 CUDA tensor, if given)."""
+        self._check_hidden(hidden)
+        if logits is not None:
+            _need(logits, self.vocab, "logits")
         s = int(hidden.shape[0])
         if kv_start + s > self.max_seq:
             raise QasrError(QASR_ERANGE, f"prefill needs {kv_start + s} positions, "
@@ -574,6 +671,10 @@ class TextDecoder:
         Returns the greedy token after each segment (and fills row i of
         `logits`, [len(items)][vocab] f32, if given)."""
         items = [(int(it[0]), it[1], int(it[2]) if len(it) > 2 else 0) for it in items]
+        for _, hidden, _ in items:
+            self._check_hidden(hidden)
+        if logits is not None:
+            _need(logits, len(items) * self.vocab, "logits")
         if len({slot for slot, _, _ in items}) != len(items):
             raise QasrError(QASR_EINVAL, "prefill_batch: two segments share a slot")
         for slot, hidden, start in items:
@@ -639,6 +740,13 @@ class TextDecoder:
                     logits=None, stream=None):
         """Asynchronous step: tokens_dev / next_dev are int32 CUDA tensors of
         len(slots) entries (they may be the same tensor)."""
+        b = len(slots)
+        if len(pos) != b:
+            raise QasrError(QASR_EINVAL, f"{len(pos)} positions for {b} slots")
+        _need(tokens_dev, b, "tokens")
+        _need(next_dev, b, "next")
+        if logits is not None:
+            _need(logits, b * self.vocab, "logits")
         lg = _dev(logits, "logits", self.t.float32) if logits is not None else None
         _check(load().qasr_decoder_step(self.handle, self.kv.handle, len(slots), _i32(slots),
                                         _i32(pos), _dev(tokens_dev, "tokens", self.t.int32),

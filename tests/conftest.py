@@ -22,6 +22,21 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X GPU (runs the HIP kernels)")
 
 
+def pytest_sessionfinish(session, exitstatus):
+    """Write every parity check's figures (workloads.REPORT) to
+    $QASR_PARITY_REPORT, if set."""
+    path = os.environ.get("QASR_PARITY_REPORT")
+    if not path:
+        return
+    import json
+
+    import workloads
+
+    os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+    with open(path, "w") as f:
+        json.dump(workloads.REPORT, f, indent=1)
+
+
 def _ensure_oracle():
     import oracle
 

@@ -71,6 +71,11 @@ class Gpu:
         t = self.kv.tensor()
         return host(t[slot, layer, 0, :, :rows].contiguous()), host(t[slot, layer, 1, :, :rows].contiguous())
 
+    def cache_row(self, slot: int, layer: int, pos: int):
+        """(K, V) row `pos` of (slot, layer) as u16 [nkvh][hd]."""
+        t = self.kv.tensor()
+        return host(t[slot, layer, 0, :, pos].contiguous()), host(t[slot, layer, 1, :, pos].contiguous())
+
     def close(self):
         self.kv.close()
         self.ctx.close()

@@ -54,10 +54,10 @@ def _decode_step_check(O, rng, lay, g, refs, lengths, layer=0, slots=None):
         ma, mr = assert_parity(got[i:i + 1], want, f"entry {i} slot {sl} L={lengths[i] + 1}")
         worst = (max(worst[0], ma), max(worst[1], mr))
         # the appended row is bit-exact
-        k_gpu, v_gpu = g.cache(sl, layer, lengths[i] + 1)
-        k_ref, v_ref = refs[sl].cache_f16()
-        assert np.array_equal(k_gpu[:, -1], k_ref[:, lengths[i]])
-        assert np.array_equal(v_gpu[:, -1], v_ref[:, lengths[i]])
+        k_gpu, v_gpu = g.cache_row(sl, layer, lengths[i])
+        k_ref, v_ref = refs[sl].row_f16(lengths[i])
+        assert np.array_equal(k_gpu, k_ref)
+        assert np.array_equal(v_gpu, v_ref)
     return got, rows, worst
 
 
@@ -160,29 +160,41 @@ def test_decode_cap_length_and_permuted_slots(O, gpu):
     g.close()
 
 
-def test_config5_64_slots_two_layers(O, gpu):
-    """Config 5's shape (64 slots, ragged [64, 4096]) on two layers."""
-    from gpu_helpers import Gpu
+def test_config5_64_slots_all_layers(O, gpu):
+    """Config 5: 64 slots, ragged [64, 4096], the fused step of all 28 layers.
+    Layer 0's caches are filled through stage (a) on both sides; every other
+    layer's caches are device copies of them (the oracle reuses its arrays),
+    and each layer then steps with its own gains and raw qkv rows, so each of
+    the 28 launches reads its own cache region and appends its own row."""
+    from gpu_helpers import Gpu, say
 
     from oracle import Rng
 
     rng = Rng(SEED_BASE + 5)
     lengths = decode_lengths(rng, 64, 64, 4096)
     cap = cap_for(max(lengths) + 1)
-    g = Gpu(slots=64, cap=cap, layers=2)
+    layers = 28
+    g = Gpu(slots=64, cap=cap, layers=layers)
+    lay0 = Layer(rng)
+    refs = _setup(O, rng, lay0, lengths, cap, g, layer=0)
+    pool = g.kv.tensor()
+    for layer in range(1, layers):
+        pool[:, layer].copy_(pool[:, 0])
     worst = (0.0, 0.0)
-    for layer in (0, 1):
-        lay = Layer(rng)
-        refs = _setup(O, rng, lay, lengths, cap, g, layer=layer)
+    for layer in range(layers):
+        lay = lay0 if layer == 0 else Layer(rng)
+        for ref in refs:
+            ref.layer = lay
+        say(f"config5 layer {layer}")
         _, _, w = _decode_step_check(O, rng, lay, g, refs, lengths, layer=layer)
         worst = (max(worst[0], w[0]), max(worst[1], w[1]))
-        del refs
     print("config5 max_abs/max_rel", worst)
     g.close()
 
 
 def test_decode_long_context_split(O, gpu):
-    """Config 4's decode side: one slot at 8192+ keys, 3 consecutive steps."""
+    """Config 4's decode side: one slot at 8192 cached keys, the workload's
+    64 consecutive steps (positions 8192..8255)."""
     from gpu_helpers import Gpu
 
     from oracle import Rng
@@ -193,6 +205,6 @@ def test_decode_long_context_split(O, gpu):
     cap = cap_for(L0 + 64)
     g = Gpu(slots=1, cap=cap)
     refs = _setup(O, rng, lay, [L0], cap, g)
-    for step in range(3):
+    for step in range(64):
         _decode_step_check(O, rng, lay, g, refs, [L0 + step])
     g.close()

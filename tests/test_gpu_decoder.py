@@ -5,15 +5,16 @@ oracle's TextDecoder), on seeded random weights of the Qwen3-ASR decoder
 shapes (no checkpoint exists offline).
 
 The two sides differ by rounding (GEMM summation order, tree sums in the
-norms), so the greedy streams may part only at a near-tie; logits must agree
-to 2% of their spread at every compared step (decoder_model.compare_greedy).
+norms): logits must agree to 2% of their spread at every step, and the greedy
+token streams must be identical at every step on these seeds
+(decoder_model.compare_greedy), at both decoder shapes.
 """
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
-from decoder_model import CFG_0P6B, compare_greedy, host_bits, synth_weights
+from decoder_model import CFG_0P6B, CFG_1P7B, compare_greedy, host_bits, synth_weights
 from workloads import SEED_BASE
 
 pytestmark = pytest.mark.gpu
@@ -70,8 +71,86 @@ def test_native_decoder_greedy_0p6b_single_slot(O, gpu):
     dec.close()
     say(f"cpu tokens {[t for t, _ in cpu_out]}")
     say(f"gpu tokens {[t for t, _ in gpu_out]}")
-    n = compare_greedy(cpu_out, gpu_out, "native 0.6B")
-    assert n >= steps // 2, f"streams parted after {n} steps"
+    compare_greedy(cpu_out, gpu_out, "native 0.6B")
+
+
+def test_native_decoder_greedy_1p7b_single_slot(O, gpu):
+    """1.7B shape, 28 layers, full vocabulary: a 40-row prompt, 16 steps;
+    identical token streams against the oracle's CPU decoder."""
+    from gpu_helpers import say
+
+    cfg = dict(CFG_1P7B)
+    s, steps = 40, 16
+    W = synth_weights(cfg, SEED_BASE + 1300, device="cuda")
+    Wh = host_bits(W)
+    hidden = _prompt(SEED_BASE + 1301, s, cfg["hs"])
+    cos, sin = O.text_rope_tables_f16(cfg["max_seq"])
+    say("native decoder 1.7B: CPU reference decoder")
+    cpu = O.TextDecoder(cfg, Wh, 1024, cos, sin)
+    cpu_out = [cpu.prefill(hidden.cpu().numpy().view(np.uint16), 0)]
+    for _ in range(steps):
+        cpu_out.append(cpu.step())
+    cpu.close()
+    del Wh
+
+    say("native decoder 1.7B: GPU")
+    dec = _native(cfg, W, 1, 1024)
+    lg = _logits(cfg["vocab"])
+    tok = dec.prefill(hidden, 0, logits=lg)
+    gpu_out = [(tok, lg.cpu().numpy())]
+    lgb = lg.view(1, -1)
+    for _ in range(steps):
+        t = dec.step(logits=lgb)[0]
+        gpu_out.append((t, lgb[0].cpu().numpy()))
+    dec.close()
+    say(f"cpu tokens {[t for t, _ in cpu_out]}")
+    say(f"gpu tokens {[t for t, _ in gpu_out]}")
+    compare_greedy(cpu_out, gpu_out, "native 1.7B")
+
+
+def test_native_decoder_1p7b_16_slot_batched_steps(O, gpu):
+    """1.7B shape, 28 layers, full vocabulary, 16 slots (--batch 16): each
+    slot's prompt (3-18 rows) is prefilled, then two steps run all 16 slots
+    in one batch (the skinny GEMM's 16-row case and 16-entry decode
+    attention).  Every slot's tokens equal its own CPU reference decoder's."""
+    import torch
+
+    from gpu_helpers import say
+
+    cfg = dict(CFG_1P7B)
+    nslot, steps = 16, 2
+    lens = [3 + i for i in range(nslot)]
+    W = synth_weights(cfg, SEED_BASE + 1310, device="cuda")
+    Wh = host_bits(W)
+    cos, sin = O.text_rope_tables_f16(cfg["max_seq"])
+    prompts = [_prompt(SEED_BASE + 1311 + i, L, cfg["hs"]) for i, L in enumerate(lens)]
+    cpu_out = []
+    for i in range(nslot):
+        say(f"native decoder 1.7B x16: CPU reference, slot {i}")
+        cpu = O.TextDecoder(cfg, Wh, 1024, cos, sin)
+        seq = [cpu.prefill(prompts[i].cpu().numpy().view(np.uint16), 0)]
+        for _ in range(steps):
+            seq.append(cpu.step())
+        cpu_out.append(seq)
+        cpu.close()
+    del Wh
+
+    say("native decoder 1.7B x16: GPU")
+    dec = _native(cfg, W, nslot, 1024)
+    lg = _logits(cfg["vocab"])
+    gpu_out = []
+    for i in range(nslot):
+        tok = dec.prefill(prompts[i], 0, slot=i, logits=lg)
+        gpu_out.append([(tok, lg.cpu().numpy())])
+    lgb = torch.empty((nslot, cfg["vocab"]), dtype=torch.float32, device="cuda")
+    for _ in range(steps):
+        toks = dec.step(list(range(nslot)), logits=lgb)
+        host = lgb.cpu().numpy()
+        for i in range(nslot):
+            gpu_out[i].append((toks[i], host[i]))
+    dec.close()
+    for i in range(nslot):
+        compare_greedy(cpu_out[i], gpu_out[i], f"native 1.7B slot {i}")
 
 
 def test_native_decoder_two_slots_chunked_prefill(O, gpu):
@@ -117,8 +196,7 @@ def test_native_decoder_two_slots_chunked_prefill(O, gpu):
     assert dec.kv.cap >= max(lens) + steps
     dec.close()
     for i in range(2):
-        n = compare_greedy(cpu_out[i], gpu_out[i], f"native slot {i}")
-        assert n >= steps // 2, f"slot {i}: streams parted after {n} steps"
+        compare_greedy(cpu_out[i], gpu_out[i], f"native slot {i}")
 
 
 def test_native_decoder_step_graph_replays_equal_eager(O, gpu):

@@ -8,10 +8,11 @@ oracle's TextDecoder) on identical seeded weights and inputs.
 
 Everything outside the attention path runs in torch on the GPU (test
 plumbing, f32 math with the reference's f16 rounding points); the two sides
-therefore differ by rounding: the streams may part only at a near-tie, a step
-whose CPU top-2 logit margin is within twice the measured logit difference
-(decoder_model.compare_greedy).  No checkpoint exists offline, so the weights
-are seeded random weights of the Qwen3-ASR decoder shapes.
+differ by rounding, so the logits agree to a small fraction of their spread,
+and the token streams must be identical at every step on these seeds
+(decoder_model.compare_greedy: a difference fails, its message says whether
+it fell on a near-tie).  No checkpoint exists offline, so the weights are
+seeded random weights of the Qwen3-ASR decoder shapes.
 """
 from __future__ import annotations
 
@@ -70,8 +71,7 @@ def test_e2e_greedy_0p6b_shape_single_slot(O, gpu):
     dec.close()
     say(f"cpu tokens {[t for t, _ in cpu_out]}")
     say(f"gpu tokens {[t for t, _ in gpu_out]}")
-    n = compare_greedy(cpu_out, gpu_out, "0.6B")
-    assert n >= steps // 2, f"streams parted after {n} steps"
+    compare_greedy(cpu_out, gpu_out, "0.6B")
 
 
 def test_e2e_greedy_two_slots_chunked_prefill_split_decode(O, gpu):
@@ -120,5 +120,4 @@ def test_e2e_greedy_two_slots_chunked_prefill_split_decode(O, gpu):
     for i in range(2):
         say(f"slot {i}: cpu {[t for t, _ in cpu_out[i]]}")
         say(f"slot {i}: gpu {[t for t, _ in gpu_out[i]]}")
-        n = compare_greedy(cpu_out[i], gpu_out[i], f"slot {i}")
-        assert n >= steps // 2, f"slot {i}: streams parted after {n} steps"
+        compare_greedy(cpu_out[i], gpu_out[i], f"slot {i}")

@@ -51,6 +51,11 @@ def test_errors_before_launch(O, gpu):
     q = empty(2, QDIM)
     out = empty(2, QDIM)
     row = dev(rng.normal_f16((2, TOT)))
+    # buffers sized for the refused calls' rows: the binding refuses an
+    # undersized tensor itself (EINVAL), and these checks are about the
+    # library's own range checks
+    q40, out40 = empty(40, QDIM), empty(40, QDIM)
+    row40 = dev(rng.normal_f16((40, TOT)))
     E = qasr_attn.QasrError
 
     def code(fn):
@@ -64,15 +69,17 @@ def test_errors_before_launch(O, gpu):
     assert code(lambda: qasr_attn.decode_attn(g.ctx, g.kv, 1, [4, 3], q, out)) == qasr_attn.QASR_EINVAL
     assert code(lambda: qasr_attn.decode_step(g.ctx, g.kv, 0, [1024, 3], row, qg, kg, out)) == qasr_attn.QASR_ERANGE
     assert code(lambda: qasr_attn.decode_step(g.ctx, g.kv, 0, [4, 3], row, qg, kg, out, slots=[1, 1])) == qasr_attn.QASR_EINVAL
-    assert code(lambda: qasr_attn.prefill_attn(g.ctx, g.kv, 0, 0, 1000, 30, q, out)) == qasr_attn.QASR_ERANGE
+    assert code(lambda: qasr_attn.prefill_attn(g.ctx, g.kv, 0, 0, 1000, 30, q40, out40)) == qasr_attn.QASR_ERANGE
     assert code(lambda: qasr_attn.prefill_attn(g.ctx, g.kv, 0, 5, 0, 1, q, out)) == qasr_attn.QASR_EINVAL
-    assert code(lambda: qasr_attn.qk_norm_rope_append(g.ctx, g.kv, 0, [(0, 1020, 10)], row, qg, kg, q)) == qasr_attn.QASR_ERANGE
+    assert code(lambda: qasr_attn.qk_norm_rope_append(g.ctx, g.kv, 0, [(0, 1020, 10)], row40, qg, kg, q40)) == qasr_attn.QASR_ERANGE
     # beyond max_seq after growth
     assert g.kv.ensure_capacity(5000, 0) == 2000
     assert code(lambda: qasr_attn.decode_step(g.ctx, g.kv, 0, [2000, 3], row, qg, kg, out)) == qasr_attn.QASR_ERANGE
-    assert code(lambda: qasr_attn.prefill_attn(g.ctx, g.kv, 0, 0, 1990, 11, q, out)) == qasr_attn.QASR_ERANGE
-    # wrong dtype / host tensor never reaches the library
+    assert code(lambda: qasr_attn.prefill_attn(g.ctx, g.kv, 0, 0, 1990, 11, q40, out40)) == qasr_attn.QASR_ERANGE
+    # undersized, wrong dtype or host tensors never reach the library
     import torch
+
+    assert code(lambda: qasr_attn.prefill_attn(g.ctx, g.kv, 0, 0, 0, 30, q, out)) == qasr_attn.QASR_EINVAL
 
     with pytest.raises(ValueError):
         qasr_attn.decode_attn(g.ctx, g.kv, 0, [4, 3], q.float(), out)
@@ -109,7 +116,7 @@ def test_backend_mirror_prefill_then_steps(O, gpu):
     out = host(be.prefill(0, dev(prompt), 900, 0, qg, kg, slot=1))
     ref = OracleSeq(O, 1536, lay, tables(O))
     _, want = ref.step(prompt, 0)
-    assert_parity(out, want, "backend prefill")
+    assert_parity(out, want, "backend prefill", p_f16=True)
     for _ in range(2):
         row = rng.normal_f16((1, TOT))
         p = be.pos[1]
@@ -117,3 +124,47 @@ def test_backend_mirror_prefill_then_steps(O, gpu):
         _, want = ref.step(row, p)
         assert_parity(got, want, "backend step")
     assert be.pos == [0, 902]
+
+
+def test_growth_during_pipelined_steps_on_a_side_stream(O, gpu):
+    """The pool grows (1024 -> 1280 rows) from step_async while the previous
+    step, queued on a non-default torch stream, may still be appending row
+    pos-1: every row written before and after the growth equals, bit for
+    bit, the same steps run on a pool that never grows."""
+    import torch
+
+    import qasr_attn
+    from decoder_model import CFG_0P6B, synth_weights
+    from gpu_helpers import say
+
+    cfg = dict(CFG_0P6B, layers=2, vocab=4096)
+    W = synth_weights(cfg, SEED_BASE + 710, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(SEED_BASE + 711)
+    prompt = torch.randn((1016, cfg["hs"]), device="cuda", generator=g).half()
+    steps = 20  # positions 1016 .. 1035: crosses the 1024-row capacity
+    runs = []
+    for cap in (1024, 2048):
+        dec = qasr_attn.TextDecoder(W, cfg["nqh"], cfg["nkvh"], cfg["hd"], cfg["layers"],
+                                    cfg["eps"], cfg["max_seq"], slots=1, max_rows=1024, cap=cap)
+        dec.prefill(prompt, 0)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        toks = []
+        say(f"pipelined steps from cap {cap}")
+        with torch.cuda.stream(side):
+            h = dec.step_async([0])
+            for _ in range(steps - 1):
+                h_next = dec.step_async([0])  # may grow the pool: h is in flight
+                toks += dec.step_result(h)
+                h = h_next
+            toks += dec.step_result(h)
+        torch.cuda.synchronize()
+        end = 1016 + steps
+        kv = dec.kv.tensor()[0, :, :, :, :end].clone()
+        runs.append((dec.kv.cap, toks, kv))
+        dec.close()
+    (cap_a, toks_a, kv_a), (cap_b, toks_b, kv_b) = runs
+    assert cap_a == 1280 and cap_b == 2048
+    assert toks_a == toks_b
+    assert torch.equal(kv_a, kv_b), "rows differ after growth during a pipelined step"

@@ -352,3 +352,25 @@ def test_kv_target_cap(O):
     assert O.kv_target_cap(20000, 1024, 16384) == 16384
     assert O.kv_target_cap(100, 2048, 16384) == 2048
     assert O.kv_target_cap(16385, 1024, 16000) == 16000
+
+
+def test_softmax_weights_are_expf_of_the_rounded_difference(O):
+    """qo_softmax_weights = expf(f32(s*scale) - f32(m*scale)): against float64
+    exp of the same f32 argument (glibc expf is within one ulp), exactly 1 at
+    s == m, and a planted mistake (the difference taken before scaling, a
+    different rounding of the argument) is told apart on integer dots."""
+    rng = np.random.default_rng(11)
+    scale = np.float32(1.0 / np.sqrt(np.float32(128.0)))
+    m = rng.uniform(-300, 300, 200000).astype(np.float32)
+    s = (m - rng.uniform(0, 80 / float(scale), m.size)).astype(np.float32)
+    got = O.softmax_weights(s, m, float(scale)).astype(np.float64)
+    arg = (s * scale).astype(np.float32) - (m * scale).astype(np.float32)  # f32 ops
+    want = np.exp(arg.astype(np.float64))
+    ulp = np.spacing(want.astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got - want) <= ulp)
+    assert np.all(O.softmax_weights(m, m, float(scale)) == 1.0)
+    si = np.arange(-200, 0, dtype=np.float32)
+    mi = np.zeros_like(si) + 7.0
+    planted = np.exp(((si - mi) * scale).astype(np.float32).astype(np.float64))
+    real = O.softmax_weights(si, mi, float(scale)).astype(np.float64)
+    assert np.any(real != planted.astype(np.float32))

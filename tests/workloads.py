@@ -6,12 +6,21 @@ f16 RNE), seeded 0x51A50000 + config id.  Raw qkv rows are N(0,1); q/k RMSNorm
 gains are N(1, 0.1).  Cached positions are produced by running stage (a) on
 raw rows (the oracle for the reference cache, the HIP kernel for the GPU one).
 
-Parity metric (stated once, used everywhere): over all output elements,
-  max_abs = max |got - ref|
-  max_rel = max |got - ref| / max(|ref|, REL_FLOOR),  REL_FLOOR = ATOL / RTOL = 0.2
-with ATOL = 2e-3 and RTOL = 1e-2 from the north-star tolerance.  The floor
-keeps the relative figure meaningful where the reference is near zero (there
-an f16 output's own spacing dwarfs any relative bound).
+Parity metrics (stated once, used everywhere), with ATOL = 2e-3 and
+RTOL = 1e-2 from the north-star tolerance:
+  max_abs       = max |got - ref| over all output elements            <= ATOL
+  max_rel       = max |got - ref| / max(|ref|, ATOL / RTOL)           <= RTOL
+                  (the allclose-style reading: |d| <= max(ATOL, RTOL |ref|))
+  max_rel_small = max |got - ref| / max(|ref|, 1e-3)                  <= RTOL
+                  where the kernel keeps softmax weights in f32 (decode);
+                  recorded, not asserted, where they are rounded to f16 for
+                  the P.V MFMA (prefill: each weight carries up to 2^-11
+                  relative rounding, so outputs near zero carry ~1e-4 absolute
+                  noise; the reference's own GPU path rounds P to f16 too)
+  max_rel_vec   = max over (row, head) output vectors of
+                  ||got - ref||_2 / ||ref||_2                          <= RTOL
+Every check is recorded in REPORT (per call: label and the four figures);
+conftest writes REPORT to $QASR_PARITY_REPORT at the end of a session.
 """
 from __future__ import annotations
 
@@ -27,6 +36,9 @@ EPS = 1e-6
 ATOL = 2e-3
 RTOL = 1e-2
 REL_FLOOR = ATOL / RTOL
+REL_FLOOR_SMALL = 1e-3
+
+REPORT = []
 
 
 def errors(got_u16: np.ndarray, ref_u16: np.ndarray):
@@ -43,10 +55,40 @@ def errors(got_u16: np.ndarray, ref_u16: np.ndarray):
     return float(d.max()), float((d / np.maximum(np.abs(r), REL_FLOOR)).max())
 
 
-def assert_parity(got_u16, ref_u16, what: str = ""):
-    ma, mr = errors(got_u16, ref_u16)
-    assert ma <= ATOL and mr <= RTOL, f"{what}: max_abs {ma:.3e} (<= {ATOL}), max_rel {mr:.3e} (<= {RTOL})"
-    return ma, mr
+def error_report(got_u16, ref_u16, vec: int = HD) -> dict:
+    """All four parity figures of f16 outputs (uint16 bit patterns); `vec`
+    is the length of the vectors max_rel_vec is taken over (a head)."""
+    g = np.asarray(got_u16, dtype=np.uint16).view(np.float16).astype(np.float64)
+    r = np.asarray(ref_u16, dtype=np.uint16).view(np.float16).astype(np.float64)
+    assert g.shape == r.shape
+    if g.size == 0:
+        return dict(max_abs=0.0, max_rel=0.0, max_rel_small=0.0, max_rel_vec=0.0)
+    assert np.all(np.isfinite(r)), "reference has non-finite values"
+    if not np.all(np.isfinite(g)):
+        inf = float("inf")
+        return dict(max_abs=inf, max_rel=inf, max_rel_small=inf, max_rel_vec=inf)
+    d = np.abs(g - r)
+    ar = np.abs(r)
+    dv, rv = d.reshape(-1, vec), r.reshape(-1, vec)
+    vn = np.sqrt((dv * dv).sum(1)) / np.maximum(np.sqrt((rv * rv).sum(1)), 1e-30)
+    return dict(max_abs=float(d.max()), max_rel=float((d / np.maximum(ar, REL_FLOOR)).max()),
+                max_rel_small=float((d / np.maximum(ar, REL_FLOOR_SMALL)).max()),
+                max_rel_vec=float(vn.max()))
+
+
+def assert_parity(got_u16, ref_u16, what: str = "", p_f16: bool = False):
+    """The north-star bound.  p_f16: the kernel rounds softmax weights to f16
+    (prefill), so max_rel_small is recorded but not asserted.  Returns
+    (max_abs, max_rel)."""
+    e = error_report(got_u16, ref_u16)
+    REPORT.append(dict(what=what, p_f16=p_f16, **e))
+    msg = (f"{what}: max_abs {e['max_abs']:.3e} (<= {ATOL}), max_rel {e['max_rel']:.3e}, "
+           f"max_rel_small {e['max_rel_small']:.3e}, max_rel_vec {e['max_rel_vec']:.3e} "
+           f"(<= {RTOL})")
+    assert e["max_abs"] <= ATOL and e["max_rel"] <= RTOL and e["max_rel_vec"] <= RTOL, msg
+    if not p_f16:
+        assert e["max_rel_small"] <= RTOL, msg
+    return e["max_abs"], e["max_rel"]
 
 
 class Tables:
@@ -100,6 +142,11 @@ class OracleSeq:
         """Stage (a) + attention (cpu_decoder.rs:398-427).  Returns (q, out)."""
         return self.O.layer_attn(self.shape, self.cap, qkv_rows, q0, self.layer.q_gain,
                                  self.layer.k_gain, self.tab.cos, self.tab.sin, self.k, self.v)
+
+    def row_f16(self, pos: int):
+        """K and V row `pos` of every kv head as f16 bit patterns ([nkvh][hd])."""
+        return (self.O.f16_from_f32(np.ascontiguousarray(self.k[:, pos])),
+                self.O.f16_from_f32(np.ascontiguousarray(self.v[:, pos])))
 
     def cache_f16(self):
         """The caches as f16 bit patterns (exact: they hold f16 values)."""
