@@ -20,11 +20,16 @@ __global__ void softmax_weights_kernel(const float* __restrict__ s, const float*
                                        float* __restrict__ out_raw) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    // The products are rounded on their own (no contraction into the
-    // subtraction), as in the decode kernel, where the scaled score also
-    // feeds the row maximum.
-    const float si = s[i], m2 = __fmul_rn(m[i], sl2);
-    out_scaled[i] = qasr::softmax_w_scaled(__fmul_rn(si, sl2), m2);
+    // The products are rounded on their own, as in the kernels (decode keeps
+    // s*sl2 because it also feeds the row maximum, prefill scales the
+    // maximum): written as one v_mul_f32 each so the compiler cannot contract
+    // them into the subtraction, which would turn the decode form into the
+    // prefill form.
+    const float si = s[i];
+    float m2, s2;
+    asm volatile("v_mul_f32 %0, %1, %2" : "=v"(m2) : "v"(m[i]), "v"(sl2));
+    asm volatile("v_mul_f32 %0, %1, %2" : "=v"(s2) : "v"(si), "v"(sl2));
+    out_scaled[i] = qasr::softmax_w_scaled(s2, m2);
     out_raw[i] = qasr::softmax_w_raw(si, sl2, m2);
 }
 
