@@ -163,6 +163,20 @@ int qasr_decode_step(qasr_ctx* ctx, qasr_kv* kv, int layer, int batch, const int
 int qasr_prefill_attn(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, int s,
                       const void* q_dev, void* out_dev, void* stream);
 
+/* Stage (c) exactly as qasr_prefill_attn, with no allocation of any kind
+ * (no hipMalloc / hipFree, nothing a library allocates), for callers that
+ * cannot allocate: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid it.  No counterpart in the reference.  The split-K
+ * partials live in a static device array of the library (17.3 MB per GPU,
+ * held until the process ends) instead of the KV pool's workspace, which
+ * qasr_prefill_attn grows on demand.  Limits: s <= 64 * min(64, 256 / nkvh)
+ * rows per call (2048 for 8 kv heads; longer prompts go in chunks with
+ * kv_start > 0), nkvh <= 16; beyond them QASR_EINVAL.  Every call on one GPU
+ * shares that array: calls that overlap on one GPU (different streams or
+ * threads) race and must be serialised by the caller. */
+int qasr_prefill_attn_noalloc(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start,
+                              int s, const void* q_dev, void* out_dev, void* stream);
+
 /* Stage (c) for several segments in one call (the attention loop of
  * prefill_multi, decoder.rs:3642-3700, one dispatch per segment there):
  * segment i's roped q rows are rows row_i .. of q_dev (segments concatenated

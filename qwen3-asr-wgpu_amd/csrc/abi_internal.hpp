@@ -59,7 +59,8 @@ struct qasr_ctx {
     qasr::f16* sin = nullptr;
     int rope_rows = 0;
     float scale_log2;
-    int cus = 256;  // compute units of the device (decode plans two workgroups per CU)
+    int cus = 256;  // compute units of the device (the decode planner's workgroup budget)
+    float* scratch = nullptr;  // device address of the no-allocation prefill scratch on `device`
 };
 
 struct qasr_kv {

@@ -18,6 +18,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -233,6 +234,149 @@ int run_decode(bool fused, qasr_ctx* ctx, qasr_kv* kv, int layer, int batch, con
     return QASR_OK;
 }
 
+// ---- prefill: planning shared by the allocating and the no-allocation entry
+
+// Split workspace of qasr_prefill_attn_noalloc, for callers that cannot
+// allocate (HIP graph capture, serving loops, harnesses that forbid it): a
+// file-scope device array, one copy per GPU, alive until the process ends.
+// Partials of at most kScratchItems work items (17.3 MB) plus the arrival
+// counters.  Host code reaches it only through the address resolved per
+// device by hipGetSymbolAddress (scratch_ptr); the array's name is a host
+// stand-in, not a device address.
+constexpr int64_t kScratchItems = 256;
+constexpr int kScratchMaxKvHeads = 16;  // nkvh <= 16 (qasr_ctx_create's head limit)
+constexpr int64_t kScratchO = kScratchItems * qasr::kPrefillItemFloats;
+constexpr int64_t kScratchMl = kScratchItems * qasr::kPrefillItemMl;
+constexpr int64_t kScratchCounters = (int64_t)kScratchMaxKvHeads * qasr::kMaxRowBlocks;
+static __device__ __align__(256) float scratch[kScratchO + kScratchMl + kScratchCounters];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of `scratch` on `device` (resolved once per device, with
+// that device current).
+int scratch_ptr(int device, float** out) {
+    if (device < 0 || device >= kMaxDevices) return fail(QASR_EINVAL, "device %d beyond %d", device, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[device]) {
+        DeviceScope ds(device);
+        if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+        void* p = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (!p) return fail(QASR_EDEVICE, "no device address for the prefill scratch array");
+        g_scratch_dev[device] = (float*)p;
+    }
+    *out = g_scratch_dev[device];
+    return QASR_OK;
+}
+
+__global__ void zero_u32_kernel(uint32_t* p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// Longest prefill one qasr_prefill_attn_noalloc call takes: every row block
+// of the launch must have at least one work item in the scratch array.
+int noalloc_max_rows(int nkvh) {
+    return qasr::kPrefillRows * (int)std::min<int64_t>(qasr::kMaxRowBlocks, kScratchItems / nkvh);
+}
+
+int run_prefill(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, int s,
+                const void* q_dev, void* out_dev, void* stream, bool noalloc) {
+    int rc = check_common(ctx, kv, layer);
+    if (rc) return rc;
+    if (slot < 0 || slot >= kv->slots)
+        return fail(QASR_EINVAL, "slot %d outside [0, %d)", slot, kv->slots);
+    if (kv_start < 0 || s < 0) return fail(QASR_EINVAL, "negative kv_start / s");
+    if (s == 0) return QASR_OK;
+    if (!q_dev || !out_dev) return fail(QASR_EINVAL, "null device pointer");
+    const int64_t end = (int64_t)kv_start + s;
+    if (end > ctx->cfg.max_seq)
+        return fail(QASR_ERANGE, "prefill needs %lld positions, max_seq is %d", (long long)end,
+                    ctx->cfg.max_seq);
+    if (end > kv->cap)
+        return fail(QASR_ERANGE, "prefill needs %lld positions, KV capacity is %d",
+                    (long long)end, kv->cap);
+    const qasr_attn_cfg& c = ctx->cfg;
+    const int nqh = c.num_attention_heads, nkvh = c.num_key_value_heads;
+    if (noalloc) {
+        if (nkvh > kScratchMaxKvHeads)
+            return fail(QASR_EINVAL, "%d kv heads: the no-allocation prefill takes at most %d",
+                        nkvh, kScratchMaxKvHeads);
+        if (s > noalloc_max_rows(nkvh))
+            return fail(QASR_EINVAL, "%d rows: the no-allocation prefill takes at most %d rows per "
+                        "call (prefill longer prompts in chunks, kv_start > 0)", s,
+                        noalloc_max_rows(nkvh));
+        if (!ctx->scratch) return fail(QASR_ESTATE, "context has no prefill scratch address");
+    }
+    DeviceScope ds(ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    const qasr::CacheGeom g = geom(kv);
+    const int64_t ld = (int64_t)nqh * qasr::kHeadDim;
+    const int rows_per_launch = qasr::kMaxRowBlocks * qasr::kPrefillRows;
+    const int tps_forced = env_int("QASR_PREFILL_TPS", 0);
+    qasr::PrefillWs fixed{};
+    if (noalloc) {
+        fixed.o = ctx->scratch;
+        fixed.ml = ctx->scratch + kScratchO;
+        fixed.counters = reinterpret_cast<uint32_t*>(ctx->scratch + kScratchO + kScratchMl);
+        fixed.items = kScratchItems;
+        // The array keeps the last call's contents: the arrival counters
+        // start this call at zero.
+        const int n = nkvh * qasr::kMaxRowBlocks;
+        hipLaunchKernelGGL(zero_u32_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                           fixed.counters, n);
+        HIP_TRY(hipGetLastError(), "scratch counter clear");
+    }
+    for (int r0 = 0; r0 < s; r0 += rows_per_launch) {
+        const int rows = std::min(rows_per_launch, s - r0);
+        const int ks = kv_start + r0;
+        const int nrb = (rows + qasr::kPrefillRows - 1) / qasr::kPrefillRows;
+        const int max_tiles = (ks + rows + qasr::kPrefillTileKeys - 1) / qasr::kPrefillTileKeys;
+        // Tiles per split: about one workgroup per CU (256), without
+        // splitting row blocks whose key range is short.
+        int tps = tps_forced;
+        if (tps <= 0) {
+            const int64_t tiles_all = (int64_t)nrb * max_tiles;
+            const int64_t want = std::max<int64_t>(1, 256 / nkvh);
+            tps = (int)std::max<int64_t>(2, (tiles_all + want - 1) / want);
+        }
+        qasr::PrefillPlan P = qasr::plan_prefill(rows, ks, nkvh, tps);
+        if (noalloc) {
+            // Coarser splits until the partials fit the scratch array; at
+            // tps = max_tiles every row block is one item (s is bounded so
+            // that this fits).
+            while ((int64_t)P.items_per_kvh * nkvh > kScratchItems && tps < max_tiles) {
+                tps = std::min(max_tiles, tps * 2);
+                P = qasr::plan_prefill(rows, ks, nkvh, tps);
+            }
+            if ((int64_t)P.items_per_kvh * nkvh > kScratchItems)
+                return fail(QASR_EINVAL, "prefill plan of %lld items exceeds the scratch's %lld",
+                            (long long)P.items_per_kvh * nkvh, (long long)kScratchItems);
+        } else {
+            rc = ensure_prefill_ws(kv, (int64_t)P.items_per_kvh * nkvh);
+            if (rc) return rc;
+        }
+        qasr::PrefillArgs a;
+        a.q = (const f16*)q_dev + r0 * ld;
+        a.out = (f16*)out_dev + r0 * ld;
+        a.k = g.base + slot * g.slot_stride + layer * g.layer_stride;
+        a.v = a.k + g.kv_stride;
+        a.head_stride = g.head_stride;
+        a.nqh = nqh;
+        a.nkvh = nkvh;
+        a.s = rows;
+        a.kv_start = ks;
+        a.scale_log2 = ctx->scale_log2;
+        const qasr::PrefillWs ws =
+            noalloc ? fixed : qasr::PrefillWs{kv->pws_o, kv->pws_ml, kv->pws_ctr, kv->pws_items};
+        hipError_t e = qasr::launch_prefill_attn(a, P, ws, (hipStream_t)stream);
+        if (e != hipSuccess) return hip_fail(e, "prefill attention launch");
+    }
+    return QASR_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -265,9 +409,13 @@ int qasr_ctx_create(const qasr_attn_cfg* cfg, int device, qasr_ctx** out) {
     int cus = 0;
     HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
             "hipDeviceGetAttribute");
+    float* scratch_dev = nullptr;
+    int src = scratch_ptr(device, &scratch_dev);
+    if (src != QASR_OK) return src;
     qasr_ctx* ctx = new qasr_ctx();
     ctx->cfg = c;
     ctx->device = device;
+    ctx->scratch = scratch_dev;
     ctx->cus = std::max(1, cus);
     // scale = 1/sqrt(hd) in f32 (decoder.rs:204-206), folded with log2(e) so the
     // kernels exponentiate with exp2.
@@ -589,60 +737,12 @@ int qasr_decode_step(qasr_ctx* ctx, qasr_kv* kv, int layer, int batch, const int
 
 int qasr_prefill_attn(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, int s,
                       const void* q_dev, void* out_dev, void* stream) {
-    int rc = check_common(ctx, kv, layer);
-    if (rc) return rc;
-    if (slot < 0 || slot >= kv->slots)
-        return fail(QASR_EINVAL, "slot %d outside [0, %d)", slot, kv->slots);
-    if (kv_start < 0 || s < 0) return fail(QASR_EINVAL, "negative kv_start / s");
-    if (s == 0) return QASR_OK;
-    if (!q_dev || !out_dev) return fail(QASR_EINVAL, "null device pointer");
-    const int64_t end = (int64_t)kv_start + s;
-    if (end > ctx->cfg.max_seq)
-        return fail(QASR_ERANGE, "prefill needs %lld positions, max_seq is %d", (long long)end,
-                    ctx->cfg.max_seq);
-    if (end > kv->cap)
-        return fail(QASR_ERANGE, "prefill needs %lld positions, KV capacity is %d",
-                    (long long)end, kv->cap);
-    DeviceScope ds(ctx->device);
-    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
-    const qasr_attn_cfg& c = ctx->cfg;
-    const int nqh = c.num_attention_heads, nkvh = c.num_key_value_heads;
-    const qasr::CacheGeom g = geom(kv);
-    const int64_t ld = (int64_t)nqh * qasr::kHeadDim;
-    const int rows_per_launch = qasr::kMaxRowBlocks * qasr::kPrefillRows;
-    const int tps_forced = env_int("QASR_PREFILL_TPS", 0);
-    for (int r0 = 0; r0 < s; r0 += rows_per_launch) {
-        const int rows = std::min(rows_per_launch, s - r0);
-        const int ks = kv_start + r0;
-        // Tiles per split: about one workgroup per CU (256), without
-        // splitting row blocks whose key range is short.
-        int tps = tps_forced;
-        if (tps <= 0) {
-            const int nrb = (rows + qasr::kPrefillRows - 1) / qasr::kPrefillRows;
-            const int64_t tiles_all =
-                (int64_t)nrb * ((ks + rows + qasr::kPrefillTileKeys - 1) / qasr::kPrefillTileKeys);
-            const int64_t want = std::max<int64_t>(1, 256 / nkvh);
-            tps = (int)std::max<int64_t>(2, (tiles_all + want - 1) / want);
-        }
-        qasr::PrefillPlan P = qasr::plan_prefill(rows, ks, nkvh, tps);
-        rc = ensure_prefill_ws(kv, (int64_t)P.items_per_kvh * nkvh);
-        if (rc) return rc;
-        qasr::PrefillArgs a;
-        a.q = (const f16*)q_dev + r0 * ld;
-        a.out = (f16*)out_dev + r0 * ld;
-        a.k = g.base + slot * g.slot_stride + layer * g.layer_stride;
-        a.v = a.k + g.kv_stride;
-        a.head_stride = g.head_stride;
-        a.nqh = nqh;
-        a.nkvh = nkvh;
-        a.s = rows;
-        a.kv_start = ks;
-        a.scale_log2 = ctx->scale_log2;
-        qasr::PrefillWs ws{kv->pws_o, kv->pws_ml, kv->pws_ctr, kv->pws_items};
-        hipError_t e = qasr::launch_prefill_attn(a, P, ws, (hipStream_t)stream);
-        if (e != hipSuccess) return hip_fail(e, "prefill attention launch");
-    }
-    return QASR_OK;
+    return run_prefill(ctx, kv, layer, slot, kv_start, s, q_dev, out_dev, stream, false);
+}
+
+int qasr_prefill_attn_noalloc(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start,
+                              int s, const void* q_dev, void* out_dev, void* stream) {
+    return run_prefill(ctx, kv, layer, slot, kv_start, s, q_dev, out_dev, stream, true);
 }
 
 // Longest key range (kv_start + rows) of a segment that a one-launch batched

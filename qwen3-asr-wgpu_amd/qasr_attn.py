@@ -37,7 +37,7 @@ ABI_SYMBOLS = (
     "qasr_decode_attn", "qasr_decode_step", "qasr_prefill_attn", "qasr_prefill_layer",
     "qasr_decoder_create", "qasr_decoder_destroy", "qasr_decoder_step", "qasr_decoder_prefill",
     "qasr_decoder_prefill_batch", "qasr_dequant_i8", "qasr_prefill_attn_batch",
-    "qasr_softmax_weights", "qasr_stream_read",
+    "qasr_softmax_weights", "qasr_stream_read", "qasr_prefill_attn_noalloc",
 )
 MAX_PREFILL_SEGMENTS = 64  # segments per qasr_decoder_prefill_batch call
 
@@ -131,6 +131,8 @@ def load(path: str = LIB_PATH):
                                    _vp, _vp, _vp]
     L.qasr_prefill_attn.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_int, _vp, _vp, _vp]
+    L.qasr_prefill_attn_noalloc.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_int, _vp, _vp, _vp]
     L.qasr_prefill_layer.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                      ctypes.c_int, _vp, _vp, _vp, _vp, _vp, _vp]
     L.qasr_prefill_attn_batch.argtypes = [_vp, _vp, ctypes.c_int, ctypes.POINTER(Segment),
@@ -382,6 +384,18 @@ def prefill_attn(ctx: Context, kv: KVPool, layer: int, slot: int, kv_start: int,
     _need(out, max(s, 0) * qd, "out")
     _check(load().qasr_prefill_attn(ctx.handle, kv.handle, layer, slot, kv_start, s,
                                     _dev(q, "q"), _dev(out, "out"), _stream(stream)))
+
+
+def prefill_attn_noalloc(ctx: Context, kv: KVPool, layer: int, slot: int, kv_start: int, s: int,
+                         q, out, stream=None):
+    """qasr_prefill_attn_noalloc: prefill_attn without any allocation (split
+    partials in the library's static per-GPU scratch; at most 2048 rows per
+    call with 8 kv heads; calls overlapping on one GPU race)."""
+    _, qd = _widths(ctx)
+    _need(q, max(s, 0) * qd, "q")
+    _need(out, max(s, 0) * qd, "out")
+    _check(load().qasr_prefill_attn_noalloc(ctx.handle, kv.handle, layer, slot, kv_start, s,
+                                            _dev(q, "q"), _dev(out, "out"), _stream(stream)))
 
 
 def prefill_attn_batch(ctx: Context, kv: KVPool, layer: int, segments, q, out, stream=None):
