@@ -37,6 +37,8 @@
 // and substitutes them for the cache load of that key.  The first K/V pass is
 // issued before this prologue so its latency overlaps it.
 
+#include <type_traits>
+
 #include "kernels.hpp"
 #include "norm_rope.hpp"
 
@@ -97,7 +99,6 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     __shared__ float s_wm[4 * W][2];
     __shared__ float s_wl[4 * W][2];
     __shared__ float s_wa[4 * W][2][kHeadDim];
-    __shared__ __attribute__((aligned(16))) float s_ml[16][4];  // one merge batch
     __shared__ int s_last;
 
     const int wg = blockIdx.x;
@@ -339,43 +340,77 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     __syncthreads();
     if (!s_last) return;
 
-    // Last arrival: merge the nch partials of (b, kv head), online (running
-    // max, rescaled sums) in chunk order.  Per batch of 16 chunks the (m, l)
-    // of each (one 16-byte load per chunk, to LDS) and this thread's element
-    // of each are requested together as plain device-coherent (sc1) loads, so
-    // a batch costs one memory round trip.
+    // Last arrival: merge the nch partials of (b, kv head) in chunk order:
+    // M = max of the chunk maxima, then sum_i 2^(m_i - M) * (l_i, acc_i).
+    // Every chunk holds at least one real key, so every m_i is finite.  Each
+    // thread requests the (m, l) of its head and its element of every chunk
+    // of a batch of 32 at once, as plain device-coherent (sc1) loads: a batch
+    // costs one memory round trip and the arithmetic has no branches.
     const int64_t it0 = P.wg_base[b] + kvh * nch;
     const __amdgpu_buffer_rsrc_t acc_res = make_rsrc(ws_acc + it0 * (2 * kHeadDim), nch * (2 * kHeadDim) * 4);
     const __amdgpu_buffer_rsrc_t ml_res = make_rsrc(ws_ml + it0 * 4, nch * 16);
-    constexpr int kBatch = 16;
-    float Mh = kNegInf, lsum = 0.0f, acc = 0.0f;
-    for (int i0 = 0; i0 < nch; i0 += kBatch) {
-        const int nb = min(kBatch, nch - i0);
-        if (i0 > 0) __syncthreads();  // s_ml of the previous batch is consumed
-        if (tid < nb) {
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(ml_res, (i0 + tid) * 16, 0, kSc1);
-            *(u32x4*)&s_ml[tid][0] = v;
-        }
-        float x[kBatch];
+    constexpr int kBatch = kDecodeMergeBatch;
+    auto ld_ml = [&](int i, int k) {  // k: 0 = m, 2 = l
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ml_res, (i * 4 + k + h) * 4, 0, kSc1));
+    };
+    auto ld_acc = [&](int i) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             acc_res, (i * (2 * kHeadDim) + h * kHeadDim + j) * 4, 0, kSc1));
+    };
+    float lsum = 0.0f, acc = 0.0f;
+    // One round trip for N >= nch chunks (N a compile-time batch, so only
+    // about as many loads are issued as there are chunks).
+    auto merge_one_batch = [&](auto n_tag) {
+        constexpr int N = decltype(n_tag)::value;
+        float mv[N], lv[N], xv[N];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int i = i0 + (u < nb ? u : 0);
-            x[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                  acc_res, (i * (2 * kHeadDim) + h * kHeadDim + j) * 4, 0, kSc1));
+        for (int u = 0; u < N; ++u) {
+            const int i = u < nch ? u : 0;
+            mv[u] = ld_ml(i, 0);
+            lv[u] = ld_ml(i, 2);
+            xv[u] = ld_acc(i);
         }
-        __syncthreads();
+        float M = mv[0];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            if (u < nb) {
-                const float mi = s_ml[u][h];
-                if (mi != kNegInf) {
-                    const float mn = fmaxf(Mh, mi);
-                    const float fo = Mh == kNegInf ? 0.0f : fast_exp2(Mh - mn);
-                    const float fi = fast_exp2(mi - mn);
-                    lsum = fmaf(s_ml[u][2 + h], fi, lsum * fo);
-                    acc = fmaf(x[u], fi, acc * fo);
-                    Mh = mn;
-                }
+        for (int u = 1; u < N; ++u) M = fmaxf(M, mv[u]);  // repeats of chunk 0 change nothing
+#pragma unroll
+        for (int u = 0; u < N; ++u) {
+            const float wgt = u < nch ? fast_exp2(mv[u] - M) : 0.0f;
+            lsum = fmaf(lv[u], wgt, lsum);
+            acc = fmaf(xv[u], wgt, acc);
+        }
+    };
+    if (nch <= 4) {
+        merge_one_batch(std::integral_constant<int, 4>{});
+    } else if (nch <= 8) {
+        merge_one_batch(std::integral_constant<int, 8>{});
+    } else if (nch <= 16) {
+        merge_one_batch(std::integral_constant<int, 16>{});
+    } else if (nch <= kBatch) {
+        merge_one_batch(std::integral_constant<int, kBatch>{});
+    } else {
+        float M = kNegInf;
+        for (int i0 = 0; i0 < nch; i0 += kBatch) {
+            float mv[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) mv[u] = ld_ml(i0 + u < nch ? i0 + u : i0, 0);
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) M = fmaxf(M, mv[u]);
+        }
+        for (int i0 = 0; i0 < nch; i0 += kBatch) {
+            float mv[kBatch], lv[kBatch], xv[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const int i = i0 + u < nch ? i0 + u : i0;
+                mv[u] = ld_ml(i, 0);
+                lv[u] = ld_ml(i, 2);
+                xv[u] = ld_acc(i);
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const float wgt = i0 + u < nch ? fast_exp2(mv[u] - M) : 0.0f;
+                lsum = fmaf(lv[u], wgt, lsum);
+                acc = fmaf(xv[u], wgt, acc);
             }
         }
     }

@@ -47,7 +47,8 @@ constexpr int kDecodeWavesPerEU = 2;  // occupancy target: <= 256 VGPRs (two pas
 constexpr int kDecodeTileKeys = 32;   // keys per wave pass
 constexpr int kDecodeMaxChunksPerEntry = 256;
 constexpr int kDecodeMinChunk = 128;   // keys (256: config 1 2.7% slower, others equal)
-constexpr int kDecodeMaxSplit = 16;    // chunks per entry by default (one merge batch)
+constexpr int kDecodeMergeBatch = 32;  // partials the merging workgroup requests per round trip
+constexpr int kDecodeMaxSplit = kDecodeMergeBatch;  // chunks per entry by default (one merge batch)
 constexpr int kDecodeMaxItems = 8192;   // >= 4096 target + kMaxBatch * nkvh rounding slack
 
 // Split-K workspace of one launch: per workgroup the unnormalised partial

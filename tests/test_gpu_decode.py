@@ -130,7 +130,7 @@ def test_decode_chunk_sizes_and_unfused_equal_fused(O, gpu, min_chunk, wgs, wave
 
 def test_decode_merge_past_16_chunks(O, gpu, monkeypatch):
     """Up to 64 chunks per entry (QASR_DECODE_MAX_SPLIT=64, 32-key chunks):
-    the last arrival merges the partials in batches of 16, one round trip
+    the last arrival merges the partials in batches of 32, one round trip
     each, in chunk order -- the same oracle bound and fused/unfused equality."""
     monkeypatch.setenv("QASR_DECODE_MAX_SPLIT", "64")
     test_decode_chunk_sizes_and_unfused_equal_fused(O, gpu, "32", "4096", "4", monkeypatch)

@@ -170,13 +170,16 @@ def _segments_setup(O, rng, lay, segments, cap):
     return g, refs, qkv, q
 
 
-def test_prefill_attn_batch_equals_per_segment_launches(O, gpu):
-    """Key ranges of at most 256 (no split either way): one launch for all
-    segments gives the per-segment launches' output bit for bit."""
+def test_prefill_attn_batch_equals_per_segment_launches(O, gpu, monkeypatch):
+    """With the per-segment launches held to one split per row block
+    (QASR_PREFILL_TPS large; the one-launch path never splits), one launch
+    for all segments gives the per-segment launches' output bit for bit."""
     import qasr_attn
     from gpu_helpers import dev, empty, host, say
 
     from oracle import Rng
+
+    monkeypatch.setenv("QASR_PREFILL_TPS", "100000")
 
     rng = Rng(SEED_BASE + 480)
     lay = Layer(rng)
