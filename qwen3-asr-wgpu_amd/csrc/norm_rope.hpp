@@ -44,6 +44,24 @@ __device__ __forceinline__ float head_inv_rms_squares(const float* sq, float eps
     return 1.0f / sqrtf(sum2 / (float)kHeadDim + eps);
 }
 
+// The same chain with all 32 four-square reads issued before the adds (one
+// LDS latency instead of one per pair of reads); same adds, same order.
+__device__ __forceinline__ float head_inv_rms_squares_all(const float* sq, float eps) {
+#pragma clang fp contract(off)
+    float4 v[kHeadDim / 4];
+#pragma unroll
+    for (int i = 0; i < kHeadDim / 4; ++i) v[i] = *(const float4*)(sq + 4 * i);
+    float sum2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kHeadDim / 4; ++i) {
+        sum2 += v[i].x;
+        sum2 += v[i].y;
+        sum2 += v[i].z;
+        sum2 += v[i].w;
+    }
+    return 1.0f / sqrtf(sum2 / (float)kHeadDim + eps);
+}
+
 // One roped element j of a head whose raw values, gains and cos/sin rows are
 // given (all f16).  `inv` is the head's inverse RMS.
 __device__ __forceinline__ f16 rope_elem(const f16* raw, const f16* gain, const f16* cos_row,
@@ -57,6 +75,33 @@ __device__ __forceinline__ f16 rope_elem(const f16* raw, const f16* gain, const 
     const float b = xp * h2f(sin_row[j]);
     // sign * xp * s with sign = -1 for j < half: (-xp)*s == -(xp*s) exactly.
     return f2h(j < half ? a - b : a + b);
+}
+
+// Elements j0 .. j0+7 (j0 a multiple of 8) of the same, each operand read as
+// one 16-byte vector (the rotation partners j0 +- half are 8 aligned too);
+// per element the arithmetic of rope_elem.
+__device__ __forceinline__ uint4 rope8(const f16* raw, const f16* gain, const f16* cos_row,
+                                       const f16* sin_row, float inv, int j0) {
+#pragma clang fp contract(off)
+    constexpr int half = kHeadDim / 2;
+    const bool lo = j0 < half;
+    const int p0 = lo ? j0 + half : j0 - half;
+    H8 x, xp, g, gp, c, sn, o;
+    x.u = *(const uint4*)(raw + j0);
+    xp.u = *(const uint4*)(raw + p0);
+    g.u = *(const uint4*)(gain + j0);
+    gp.u = *(const uint4*)(gain + p0);
+    c.u = *(const uint4*)(cos_row + j0);
+    sn.u = *(const uint4*)(sin_row + j0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float xj = (h2f(x.e[e]) * inv) * h2f(g.e[e]);
+        const float xq = (h2f(xp.e[e]) * inv) * h2f(gp.e[e]);
+        const float a = xj * h2f(c.e[e]);
+        const float b = xq * h2f(sn.e[e]);
+        o.e[e] = f2h(lo ? a - b : a + b);
+    }
+    return o.u;
 }
 
 }  // namespace qasr

@@ -27,9 +27,13 @@
 // more than 2^8, so p <= 256 and the rescale branch is rarely taken; the
 // result is the same softmax.  Only key halves that straddle the diagonal are
 // masked, and halves wholly past it are skipped.
-// K/V tiles are copied global -> LDS directly (buffer_load ... lds, rows past
-// the row block's last key clamped to it), double buffered: the copy of tile
-// t+1 is in flight while tile t is consumed.
+// K/V tiles and the Q block are copied global -> LDS directly (buffer_load ...
+// lds, rows past the last key or query clamped to it), the K/V tiles double
+// buffered: the first two tiles and Q are requested together at the start,
+// and the copy of tile t+2 goes into tile t's buffers as soon as every wave is
+// done with them, so one tile is always in flight while another is consumed.
+// Every copy is inline asm waited for by count, so nothing the compiler
+// inserts waits for a copy issued later.
 // When the key range of a row block is split, each item publishes its partial
 // (max, sum, unnormalised O) with device-scope stores and the last to arrive
 // merges (ticket), as in the decode kernel.
@@ -129,6 +133,23 @@ __device__ __forceinline__ void dma_tile(u32x4v kr, u32x4v vr, int t0, int kend,
     for (int j = 0; j < 4; ++j) dma16(vr, rv * 256 + vchunk + j * 64, lds_addr(vdst + (8 * j + wave) * 512));
 }
 static_assert(kAllWaves == 8 && kTileKeys == 128, "copy pattern: 32 one-KB blocks per tile over 8 waves");
+
+// Q block: 64 rows x the kv head's 2 q heads (512 contiguous bytes per row),
+// copied like the tiles (instruction j of wave w: LDS KB 8j + w, lane l at
+// +16 l, i.e. row 2(8j + w) + l/32, slot l%32).  Slot c of row r holds
+// 16-byte chunk c ^ (r & 15), so the operand read (16 consecutive rows, one
+// chunk each) hits 16 different slots.  Rows past the block's last row are
+// read from row s-1 (finite values; their outputs are not written).
+constexpr int kQBlockHalves = kRowsPerBlock * kRep * kHeadDim;  // 32 KB
+__device__ __forceinline__ void dma_q(u32x4v qr, int row0, int last_row, int ldq_bytes, const f16* qdst,
+                                      int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = 2 * (8 * j + wave) + (lane >> 5);
+        const int c = (lane & 31) ^ (r & 15);
+        dma16(qr, min(row0 + r, last_row) * ldq_bytes + c * 16, lds_addr(qdst + (8 * j + wave) * 512));
+    }
+}
 
 // 4 halves of V^T: ds_read_b64_tr_b16 transposes 16-bit elements within each
 // 16-lane group (result lane 4m+e, element k <- source lane 4k+m, element e).
@@ -417,11 +438,12 @@ template <bool MULTI>
 __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     PrefillArgs a, PrefillPlan P, PrefillSegs S, float* __restrict__ ws_o,
     float* __restrict__ ws_ml, uint32_t* __restrict__ counters) {
-    // 128 KB: K and V tiles, double buffered.
+    // 160 KB: K and V tiles, double buffered, and the Q block.
     __shared__ __attribute__((aligned(16))) f16 K0[kTileHalves];
     __shared__ __attribute__((aligned(16))) f16 K1[kTileHalves];
     __shared__ __attribute__((aligned(16))) f16 V0[kTileHalves];
     __shared__ __attribute__((aligned(16))) f16 V1[kTileHalves];
+    __shared__ __attribute__((aligned(16))) f16 Qs[kQBlockHalves];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -489,21 +511,19 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     const int vrow = 16 * wave + (lane >> 2);
     const int vchunk = (lane & 3) * 16;
 
+    // Every copy is issued here in this order and waited for by count:
+    // tile t_begin (8 per thread), the Q block (4), tile t_begin + 1 (8).
+    const u32x4v qres = make_rsrc_words(a.q + kvh * kRep * kHeadDim,
+                                        (a.s - 1) * ldq * 2 + kRep * kHeadDim * 2);
     dma_tile(kres, vres, t_begin * kTileKeys, kend, krow, kchunk, vrow, vchunk, K0, V0, wave);
+    dma_q(qres, row0, a.s - 1, ldq * 2, Qs, wave, lane);
+    const bool two = t_begin + 1 < t_end;
+    if (two) dma_tile(kres, vres, (t_begin + 1) * kTileKeys, kend, krow, kchunk, vrow, vchunk, K1, V1, wave);
 
     Wave w;
     w.g = g;
     w.qpos = a.kv_start + r;
     w.scale_log2 = a.scale_log2;
-    {
-        const f16* qrow = a.q + (int64_t)(row_ok ? r : 0) * ldq + head * kHeadDim + g * 8;
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            H8 t;
-            t.u = row_ok ? *(const uint4*)(qrow + ks * 16) : make_uint4(0, 0, 0, 0);
-            w.qb[ks] = t.h;
-        }
-    }
 #pragma unroll
     for (int db = 0; db < 4; ++db) w.o[db] = (float16v){};
     w.m = kNegInf;
@@ -517,17 +537,17 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
         w.vbase = (4 * (q4 >> 1) + ((lane >> 2) & 3)) * 32 + 16 * (q4 & 1) + 4 * (lane & 3);
     }
 
-    // This thread's tile copies have landed, then every wave's have.
+    // This thread's copies of the next tile have landed (the only ones
+    // outstanding), then every wave's have.
     auto tile_sync = [&]() {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
     };
-    // Tile t: start the copy of tile t+1 into the other buffers, then this
-    // wave's half of tile t.  Two tiles per iteration, so every LDS address
-    // is a per-lane base plus a constant.
-    auto run = [&](const f16* kt, const f16* vt, const f16* kn, const f16* vn, int t) {
-        if (t + 1 < t_end)
-            dma_tile(kres, vres, (t + 1) * kTileKeys, kend, krow, kchunk, vrow, vchunk, kn, vn, wave);
+    // Tile t: this wave's half of it (tile t+1 is in flight meanwhile), then
+    // once every wave is done with its buffers and tile t+1 has landed, the
+    // copy of tile t+2 into them.  Two tiles per iteration, so every LDS
+    // address is a per-lane base plus a constant.
+    auto run = [&](const f16* kt, const f16* vt, int t) {
         const int k0 = t * kTileKeys + kg * kGroupKeys;
         if (k0 <= last_pos) {  // some key visible to some row
             const f16* kh = kt + kg * kGroupKeys * kHeadDim;
@@ -540,12 +560,29 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
             step_pv(w, vh, pb);
         }
         tile_sync();
+        if (t + 2 < t_end)
+            dma_tile(kres, vres, (t + 2) * kTileKeys, kend, krow, kchunk, vrow, vchunk, kt, vt, wave);
     };
-    tile_sync();  // tile t_begin and Q
+    // Tile t_begin and Q have landed (tile t_begin + 1 may be in flight).
+    if (two)
+        __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+    else
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    {
+        // Q^T operand, k-step ks: chunk 16*(head&1) + 2*ks + g of row n.
+        const int qr = (rw >> 1) * 32 + n;
+        const f16* qrow = Qs + qr * (kRep * kHeadDim);
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const int c = (((rw & 1) * 16 + 2 * ks + g) ^ (qr & 15));
+            w.qb[ks] = *(const half8v*)(qrow + c * 8);
+        }
+    }
     for (int t = t_begin;;) {
-        run(K0, V0, K1, V1, t);
+        run(K0, V0, t);
         if (++t >= t_end) break;
-        run(K1, V1, K0, V0, t);
+        run(K1, V1, t);
         if (++t >= t_end) break;
     }
 

@@ -251,6 +251,7 @@ constexpr int64_t kScratchCounters = (int64_t)kScratchMaxKvHeads * qasr::kMaxRow
 static __device__ __align__(256) float scratch[kScratchO + kScratchMl + kScratchCounters];
 
 constexpr int kMaxDevices = 64;
+constexpr int kPrefillNoSplitTiles = 4;  // key ranges of up to 512 keys run unsplit
 std::mutex g_scratch_mu;
 float* g_scratch_dev[kMaxDevices] = {};
 
@@ -335,12 +336,17 @@ int run_prefill(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, i
         const int nrb = (rows + qasr::kPrefillRows - 1) / qasr::kPrefillRows;
         const int max_tiles = (ks + rows + qasr::kPrefillTileKeys - 1) / qasr::kPrefillTileKeys;
         // Tiles per split: about one workgroup per CU (256), without
-        // splitting row blocks whose key range is short.
+        // splitting row blocks whose key range is short.  A split's merge
+        // (publish, ticket, read back) is about three memory round trips, as
+        // long as several latency-bound tiles: key ranges of up to
+        // kPrefillNoSplitTiles tiles are never split.
         int tps = tps_forced;
         if (tps <= 0) {
             const int64_t tiles_all = (int64_t)nrb * max_tiles;
             const int64_t want = std::max<int64_t>(1, 256 / nkvh);
-            tps = (int)std::max<int64_t>(2, (tiles_all + want - 1) / want);
+            tps = max_tiles <= kPrefillNoSplitTiles
+                      ? max_tiles
+                      : (int)std::max<int64_t>(2, (tiles_all + want - 1) / want);
         }
         qasr::PrefillPlan P = qasr::plan_prefill(rows, ks, nkvh, tps);
         if (noalloc) {
