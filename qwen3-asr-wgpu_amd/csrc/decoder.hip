@@ -57,6 +57,21 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// N independent wave_sums, each step's N exchanges issued together (one LDS
+// latency per step instead of one per value).  Each lane adds the same pairs
+// as wave_sum, so every result is bit-identical to wave_sum's.
+template <int N>
+__device__ __forceinline__ void wave_sums(float (&v)[N]) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        float o[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) o[i] = __shfl_xor(v[i], m);
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] += o[i];
+    }
+}
+
 // (value, index) pair order for the argmax: larger value, then smaller index
 // (the reference keeps the first maximal index: `if v > logits[best]`).
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
@@ -79,15 +94,32 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
 
 // Embedding rows of the batch's tokens (embed_row, cpu_decoder.rs:255-258).
 // An id outside [0, vocab) reads row 0 (the caller's contract says in range).
+// With ss set (hs <= 2048, one 8-element chunk per thread), also each chunk's
+// sum of squares, fmaf from 0 in element order: the chunk sums a fused
+// RMSNorm of the first projection starts from (ss[r][c], 256 per row).
 __global__ __launch_bounds__(256) void embed_rows_kernel(const f16* __restrict__ embed,
                                                          const int32_t* __restrict__ tokens,
-                                                         int vocab, int hs, f16* __restrict__ x) {
+                                                         int vocab, int hs, f16* __restrict__ x,
+                                                         float* __restrict__ ss) {
     const int r = blockIdx.x;
     int t = tokens[r];
     if (t < 0 || t >= vocab) t = 0;
     const uint4* src = (const uint4*)(embed + (int64_t)t * hs);
     uint4* dst = (uint4*)(x + (int64_t)r * hs);
-    for (int c = threadIdx.x; c < hs / 8; c += blockDim.x) dst[c] = src[c];
+    for (int c = threadIdx.x; c < hs / 8; c += blockDim.x) {
+        H8 v;
+        v.u = src[c];
+        dst[c] = v.u;
+        if (ss) {
+            float a = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float f = (float)v.e[e];
+                a = fmaf(f, f, a);
+            }
+            ss[r * 256 + c] = a;
+        }
+    }
 }
 
 // The last row of every segment of a batched prefill, packed: dst[r] =
@@ -252,6 +284,10 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
 // gate|up rows.
 constexpr int kOutF16 = 0, kOutAcc = 1, kOutF32 = 2, kOutGlu = 3;
 constexpr int kSkinnyRows = 16;
+// Fused RMSNorm in front of a skinny projection: hidden sizes up to 8 x this
+// (one 8-element chunk per thread of rms_norm_kernel's 256).
+constexpr int kNormMaxChunks = 256;
+constexpr int kNormMaxK = 8 * kNormMaxChunks;
 constexpr int kSkinnyUnroll = 4;                     // k-steps per stage (8 measured no faster)
 constexpr int kSkinnyPair = 2 * 32 * kSkinnyUnroll;  // K per wave: a multiple (even stage count)
 
@@ -309,11 +345,69 @@ struct SkinnyArgs {
     int M, N, K, groups;
     float* ws;           // split partials
     uint32_t* counters;  // split tickets
+    const f16* nw;       // fused RMSNorm: gain [K] (X is the raw residual stream)
+    float eps;
+    const float* ss_in;  // fused RMSNorm: X's chunk sums of squares [kSkinnyRows][kNormMaxChunks]
+    float* ss_out;       // kOutAcc: write the result rows' chunk sums there (or null)
 };
 
-template <int KS, int U, bool W8, int OUT>
+// Fused RMSNorm prologue, in two halves so that its loads are issued ahead
+// of the weight stream and are not queued behind it: issue() loads this
+// thread's gain chunk and its share of the rows' chunk sums of squares
+// ss[row][c] (the squares of elements 8c..8c+7 summed with fmaf from 0 in
+// element order, written by the producer of X); finish() stages the gains as
+// f32 in LDS and returns the inverse RMS of activation row r (this lane's
+// row): 64 chunks at a time through the same wave64 butterfly, then the four
+// partials added in order, as rms_norm_kernel does -- its thread t sums
+// exactly chunk t when K <= 8 * 256 -- so the normed values match that
+// kernel's bit for bit.  Rows >= M get 0 (their activations read as zeros).
+template <int KS>
+struct NormPrologue {
+    static constexpr int kPairs = kSkinnyRows * 4;  // (row, group of 64 chunks): q = 4 row + group
+    static constexpr int kPer = (kPairs + KS - 1) / KS;  // wave w takes q = w, w + KS, ..
+    static_assert(KS * 64 >= kNormMaxChunks, "one gain chunk per thread");
+    H8 gain;
+    float v[kPer];
+
+    __device__ void issue(const SkinnyArgs& p, int wave, int lane) {
+        const int nch = p.K / 8;
+        const int c = threadIdx.x;
+        gain.u = c < nch ? *(const uint4*)(p.nw + 8 * c) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int q = wave + i * KS, row = q >> 2, ch = 64 * (q & 3) + lane;
+            v[i] = (q < kPairs && row < p.M && ch < nch) ? p.ss_in[row * kNormMaxChunks + ch] : 0.0f;
+        }
+    }
+
+    __device__ float finish(const SkinnyArgs& p, float* s_gain, float* s_part, int wave, int lane,
+                            int r) {
+        const int c = threadIdx.x;
+        if (c < p.K / 8) {
+            *(float4*)&s_gain[8 * c] =
+                make_float4((float)gain.e[0], (float)gain.e[1], (float)gain.e[2], (float)gain.e[3]);
+            *(float4*)&s_gain[8 * c + 4] =
+                make_float4((float)gain.e[4], (float)gain.e[5], (float)gain.e[6], (float)gain.e[7]);
+        }
+        wave_sums(v);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int q = wave + i * KS;
+            if (lane == 0 && q < kPairs) s_part[q] = v[i];
+        }
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tot += s_part[r * 4 + i];
+        return r < p.M ? 1.0f / sqrtf(tot / (float)p.K + p.eps) : 0.0f;
+    }
+};
+
+template <int KS, int U, bool W8, int OUT, bool NORM>
 __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
     __shared__ qasr::float4v s_red[KS][64];
+    __shared__ __attribute__((aligned(16))) float s_gain[NORM ? kNormMaxK : 1];
+    __shared__ float s_part[NORM ? kSkinnyRows * 4 : 1];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int M = p.M, N = p.N, K = p.K, groups = p.groups;
@@ -360,37 +454,61 @@ __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
         }
     };
     qasr::float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto mma_stage = [&](const Stage& S) {
+    float inv = 0.0f;  // NORM: inverse RMS of activation row r
+    // NORM: the activations are normed on the way into the MFMA, as
+    // rms_norm_kernel rounds them: f16((x * inv) * gain).
+    auto act = [&](const qasr::half8v& x, int kk) {
+        if constexpr (NORM) {
+            const float4 g0 = *(const float4*)&s_gain[kk + 8 * g];
+            const float4 g1 = *(const float4*)&s_gain[kk + 8 * g + 4];
+            const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+            qasr::half8v n;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) n[e] = f16_of_f32(((float)x[e] * inv) * gv[e]);
+            return n;
+        } else {
+            return x;
+        }
+    };
+    auto mma_stage = [&](const Stage& S, int st) {
+        const int k0 = kbeg + st * 32 * U;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
+            const qasr::half8v xa = act(S.x[u], k0 + 32 * u);
             if constexpr (W8) {
                 const qasr::half8v b = dequant8(S.q[u].x, S.q[u].y, ws);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(S.x[u], b, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, b, acc, 0, 0, 0);
             } else {
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(S.x[u], S.b[u], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, S.b[u], acc, 0, 0, 0);
             }
         }
     };
-    // nst is even (the wave's K slice is a multiple of 64 U): no conditional load,
-    // so every wait leaves the other buffer's loads in flight.
+    // nst is even (the wave's K slice is a multiple of 64 U): stages 0 and 1
+    // are requested first (after the fused norm's own loads), then each
+    // stage's buffer is refilled two stages ahead as soon as its MFMAs are
+    // issued, so two stages are always in flight -- the norm prologue too
+    // runs under them.
     Stage s0, s1;
+    NormPrologue<KS> np;
+    if constexpr (NORM) np.issue(p, wave, lane);
     load_stage(0, s0);
+    load_stage(1, s1);
+    if constexpr (NORM) inv = np.finish(p, s_gain, s_part, wave, lane, r);
     int st = 0;
     for (; st + 2 < nst; st += 2) {
-        load_stage(st + 1, s1);
         __builtin_amdgcn_sched_barrier(0);
-        mma_stage(s0);
+        mma_stage(s0, st);
         __builtin_amdgcn_sched_barrier(0);
         load_stage(st + 2, s0);
         __builtin_amdgcn_sched_barrier(0);
-        mma_stage(s1);
+        mma_stage(s1, st + 1);
         __builtin_amdgcn_sched_barrier(0);
+        load_stage(st + 3, s1);
     }
-    load_stage(st + 1, s1);
     __builtin_amdgcn_sched_barrier(0);
-    mma_stage(s0);
+    mma_stage(s0, st);
     __builtin_amdgcn_sched_barrier(0);
-    mma_stage(s1);
+    mma_stage(s1, st + 1);
     s_red[wave][lane] = acc;
     __syncthreads();
     if (wave != 0) return;
@@ -437,7 +555,32 @@ __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
             ((float*)p.Y)[idx] = sum[i];
         } else {
             f16* y = (f16*)p.Y;
-            y[idx] = (f16)(OUT == kOutAcc ? (float)y[idx] + sum[i] : sum[i]);
+            const f16 out = (f16)(OUT == kOutAcc ? (float)y[idx] + sum[i] : sum[i]);
+            y[idx] = out;
+            if constexpr (OUT == kOutAcc) sum[i] = (float)out;  // for the chunk sums below
+        }
+    }
+    if constexpr (OUT == kOutAcc) {
+        if (p.ss_out) {
+            // The next projection's half of a fused RMSNorm: this tile's two
+            // 8-column chunks of every result row, squares summed with fmaf
+            // in column order (rms_norm_kernel's per-thread sum), via LDS
+            // (only this wave is left; s_red is free).
+            float* s_y = reinterpret_cast<float*>(&s_red[0][0]);  // [16 rows][16 columns]
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s_y[(4 * g + i) * 16 + r] = sum[i];
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            __builtin_amdgcn_wave_barrier();
+            const int row = lane >> 1, ch = lane & 1;
+            if (lane < 32 && row < M) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float f = s_y[row * 16 + 8 * ch + e];
+                    ss = fmaf(f, f, ss);
+                }
+                p.ss_out[row * kNormMaxChunks + 2 * tile + ch] = ss;
+            }
         }
     }
 }
@@ -474,6 +617,11 @@ struct qasr_decoder {
     uint32_t* sk_ctr = nullptr;
     f16* wdq = nullptr;      // int8 projections of prefill calls: one dequantised matrix
     int64_t wdq_elems = 0;
+    // Chunk sums of squares of the residual rows [kSkinnyRows][kNormMaxChunks],
+    // written by the launch that last wrote x when ss_valid (embedding or a
+    // skinny residual projection): a fused RMSNorm's starting point.
+    float* ss = nullptr;
+    bool ss_valid = false;
 };
 
 namespace {
@@ -482,7 +630,7 @@ void free_decoder(qasr_decoder* d) {
     if (d->blas) (void)rocblas_destroy_handle(d->blas);
     for (void* p : {(void*)d->blas_ws, (void*)d->x, (void*)d->n, (void*)d->qkv, (void*)d->qw,
                     (void*)d->attn, (void*)d->gu, (void*)d->h, (void*)d->logits, (void*)d->am_v,
-                    (void*)d->am_i, (void*)d->sk_ws, (void*)d->sk_ctr, (void*)d->wdq})
+                    (void*)d->am_i, (void*)d->sk_ws, (void*)d->sk_ctr, (void*)d->wdq, (void*)d->ss})
         if (p) (void)hipFree(p);
     delete d;
 }
@@ -515,21 +663,21 @@ SkinnyShape skinny_shape(qasr_decoder* d, int rows, int n_out, int k) {
     return SkinnyShape{};
 }
 
-template <bool W8, int OUT>
+template <bool W8, int OUT, bool NORM>
 int launch_skinny_w(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
     const dim3 grid(a.N / 16, sh.groups);
     constexpr int U = kSkinnyUnroll;
     switch (sh.ks) {
         case 4:
-            hipLaunchKernelGGL((skinny_gemm_kernel<4, U, W8, OUT>), grid, dim3(4 * 64), 0,
+            hipLaunchKernelGGL((skinny_gemm_kernel<4, U, W8, OUT, NORM>), grid, dim3(4 * 64), 0,
                                d->stream, a);
             break;
         case 8:
-            hipLaunchKernelGGL((skinny_gemm_kernel<8, U, W8, OUT>), grid, dim3(8 * 64), 0,
+            hipLaunchKernelGGL((skinny_gemm_kernel<8, U, W8, OUT, NORM>), grid, dim3(8 * 64), 0,
                                d->stream, a);
             break;
         case 12:
-            hipLaunchKernelGGL((skinny_gemm_kernel<12, U, W8, OUT>), grid, dim3(12 * 64),
+            hipLaunchKernelGGL((skinny_gemm_kernel<12, U, W8, OUT, NORM>), grid, dim3(12 * 64),
                                0, d->stream, a);
             break;
         default:
@@ -539,9 +687,10 @@ int launch_skinny_w(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
     return QASR_OK;
 }
 
-template <int OUT>
+template <int OUT, bool NORM = false>
 int launch_skinny(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
-    return a.scale ? launch_skinny_w<true, OUT>(d, sh, a) : launch_skinny_w<false, OUT>(d, sh, a);
+    return a.scale ? launch_skinny_w<true, OUT, NORM>(d, sh, a)
+                   : launch_skinny_w<false, OUT, NORM>(d, sh, a);
 }
 
 SkinnyArgs skinny_args(qasr_decoder* d, SkinnyShape sh, int rows, int n_out, int k, const void* W,
@@ -566,8 +715,13 @@ SkinnyArgs skinny_args(qasr_decoder* d, SkinnyShape sh, int rows, int n_out, int
 int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f16* x, f16* y,
              bool accumulate, const float* scale = nullptr) {
     const SkinnyShape sh = skinny_shape(d, rows, n_out, k);
+    if (y == d->x) d->ss_valid = false;  // unless the launch below writes the chunk sums
     if (sh.ks) {
-        const SkinnyArgs a = skinny_args(d, sh, rows, n_out, k, W, x, y, scale);
+        SkinnyArgs a = skinny_args(d, sh, rows, n_out, k, W, x, y, scale);
+        if (accumulate && y == d->x && d->fuse && n_out <= kNormMaxK) {
+            a.ss_out = d->ss;  // the residual rows' chunk sums, for the next fused norm
+            d->ss_valid = true;
+        }
         return accumulate ? launch_skinny<kOutAcc>(d, sh, a) : launch_skinny<kOutF16>(d, sh, a);
     }
     if (scale) {
@@ -589,24 +743,67 @@ int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f
     return QASR_OK;
 }
 
+int launch_rms_norm(const f16* x, int64_t x_stride, const void* w, f16* out, int rows, int hs,
+                    float eps, hipStream_t st);
+
+// Whether a projection of the residual rows x (k = hidden size) can take
+// its RMSNorm in the skinny kernel's prologue: a skinny shape, and chunk sums
+// of x written by the launch that wrote x.
+bool norm_fusable(qasr_decoder* d, SkinnyShape sh, int k, const f16* x) {
+    return d->fuse && sh.ks && k <= kNormMaxK && x == d->x && d->ss_valid;
+}
+
+SkinnyArgs with_norm(qasr_decoder* d, SkinnyArgs a, const void* nw) {
+    a.nw = (const f16*)nw;
+    a.eps = d->ctx->cfg.rms_norm_eps;
+    a.ss_in = d->ss;
+    return a;
+}
+
 // h[rows][inter] = SiLU(x . Wg^T) * (x . Wu^T) for the fused gate|up W in
-// one skinny launch (kOutGlu); *fused = false (nothing launched) when the
-// shape takes the library GEMM instead.
+// one skinny launch (kOutGlu), with x first normed by gain nw when nw is
+// set; *fused = false (nothing launched) when the shape or the options rule
+// that out.
 int glu_skinny(qasr_decoder* d, int rows, int inter, int k, const void* W, const f16* x, f16* h,
-               const float* scale, bool* fused) {
+               const float* scale, const void* nw, bool* fused) {
     *fused = false;
     if (!d->fuse) return QASR_OK;
     const SkinnyShape sh = skinny_shape(d, rows, 2 * inter, k);
     const int64_t span = (int64_t)(inter + 8) * k * (scale ? 1 : 2);
     if (!sh.ks || span >= (int64_t(1) << 31)) return QASR_OK;
+    if (nw && !norm_fusable(d, sh, k, x)) return QASR_OK;
     *fused = true;
-    return launch_skinny<kOutGlu>(d, sh, skinny_args(d, sh, rows, 2 * inter, k, W, x, h, scale));
+    const SkinnyArgs a = skinny_args(d, sh, rows, 2 * inter, k, W, x, h, scale);
+    return nw ? launch_skinny<kOutGlu, true>(d, sh, with_norm(d, a, nw))
+              : launch_skinny<kOutGlu>(d, sh, a);
 }
 
-// logits[rows][vocab] (f32) = n[rows][hs] . E[vocab][hs]^T.
-int gemm_logits(qasr_decoder* d, int rows, const f16* nrows, float* out) {
+// y = f16(rms_norm(x; nw) . W^T): in one skinny launch when the shape
+// allows, else rms_norm_kernel into the normed-rows buffer and the
+// projection (bit-identical either way).
+int normed_proj(qasr_decoder* d, int rows, int n_out, const void* W, const f16* x, const void* nw,
+                f16* y, const float* scale) {
+    const int hs = d->cfg.hidden_size;
+    const SkinnyShape sh = skinny_shape(d, rows, n_out, hs);
+    if (norm_fusable(d, sh, hs, x))
+        return launch_skinny<kOutF16, true>(
+            d, sh, with_norm(d, skinny_args(d, sh, rows, n_out, hs, W, x, y, scale), nw));
+    int rc = launch_rms_norm(x, hs, nw, d->n, rows, hs, d->ctx->cfg.rms_norm_eps, d->stream);
+    if (rc) return rc;
+    return gemm_f16(d, rows, n_out, hs, W, d->n, y, false, scale);
+}
+
+// logits[rows][vocab] (f32) = n[rows][hs] . E[vocab][hs]^T; with nw set,
+// `nrows` are raw rows normed by gain nw first (in the kernel's prologue).
+int gemm_logits(qasr_decoder* d, int rows, const f16* nrows, float* out, const void* nw = nullptr) {
     const int hs = d->cfg.hidden_size, vocab = d->cfg.vocab_size;
     const SkinnyShape sh = skinny_shape(d, rows, vocab, hs);
+    if (nw) {
+        if (!norm_fusable(d, sh, hs, nrows))
+            return fail(QASR_EINVAL, "logits with a fused norm: not a skinny shape");
+        return launch_skinny<kOutF32, true>(
+            d, sh, with_norm(d, skinny_args(d, sh, rows, vocab, hs, d->embed, nrows, out), nw));
+    }
     if (sh.ks)
         return launch_skinny<kOutF32>(
             d, sh, skinny_args(d, sh, rows, vocab, hs, d->embed, nrows, out));
@@ -636,11 +833,18 @@ int layer_tail(qasr_decoder* d, const qasr_layer_weights& L, int rows, hipStream
     const int qdim = a.num_attention_heads * a.head_dim;
     int rc = gemm_f16(d, rows, hs, qdim, L.o_proj, d->attn, d->x, true, L.o_scale);
     if (rc) return rc;
-    rc = launch_rms_norm(d->x, hs, L.post_norm, d->n, rows, hs, a.rms_norm_eps, st);
-    if (rc) return rc;
+    // Post-attention norm folded into gate|up when it can be, else its own launch.
     bool fused = false;
-    rc = glu_skinny(d, rows, inter, hs, L.gate_up_proj, d->n, d->h, L.gate_up_scale, &fused);
+    rc = glu_skinny(d, rows, inter, hs, L.gate_up_proj, d->x, d->h, L.gate_up_scale, L.post_norm,
+                    &fused);
     if (rc) return rc;
+    if (!fused) {
+        rc = launch_rms_norm(d->x, hs, L.post_norm, d->n, rows, hs, a.rms_norm_eps, st);
+        if (rc) return rc;
+        rc = glu_skinny(d, rows, inter, hs, L.gate_up_proj, d->n, d->h, L.gate_up_scale, nullptr,
+                        &fused);
+        if (rc) return rc;
+    }
     if (!fused) {
         rc = gemm_f16(d, rows, 2 * inter, hs, L.gate_up_proj, d->n, d->gu, false, L.gate_up_scale);
         if (rc) return rc;
@@ -659,11 +863,16 @@ int head(qasr_decoder* d, const f16* x_rows, int rows, int32_t* next_dev, float*
     const int hs = d->cfg.hidden_size, vocab = d->cfg.vocab_size;
     for (int r0 = 0; r0 < rows; r0 += kHeadRows) {
         const int nr = std::min(kHeadRows, rows - r0);
-        int rc = launch_rms_norm(x_rows + (int64_t)r0 * hs, hs, d->final_norm, d->n, nr, hs,
-                                 d->ctx->cfg.rms_norm_eps, st);
-        if (rc) return rc;
         float* lg = logits_dev ? logits_dev + (int64_t)r0 * vocab : d->logits;
-        rc = gemm_logits(d, nr, d->n, lg);
+        int rc;
+        if (r0 == 0 && norm_fusable(d, skinny_shape(d, nr, vocab, hs), hs, x_rows)) {
+            rc = gemm_logits(d, nr, x_rows + (int64_t)r0 * hs, lg, d->final_norm);  // norm folded
+        } else {
+            rc = launch_rms_norm(x_rows + (int64_t)r0 * hs, hs, d->final_norm, d->n, nr, hs,
+                                 d->ctx->cfg.rms_norm_eps, st);
+            if (rc) return rc;
+            rc = gemm_logits(d, nr, d->n, lg);
+        }
         if (rc) return rc;
         hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxChunks, nr), dim3(kArgmaxThreads), 0,
                            st, lg, vocab, d->am_v, d->am_i);
@@ -736,11 +945,10 @@ int prefill_segments(qasr_decoder* dec, qasr_kv* kv, const qasr_segment* segs, i
     const int qkvdim = (a.num_attention_heads + 2 * a.num_key_value_heads) * a.head_dim;
     HIP_TRY(hipMemcpyAsync(dec->x, hidden_dev, (size_t)rows * hs * 2, hipMemcpyDeviceToDevice, st),
             "prefill input copy");
+    dec->ss_valid = false;
     for (int l = 0; l < a.num_hidden_layers; ++l) {
         const qasr_layer_weights& L = dec->layers[l];
-        rc = launch_rms_norm(dec->x, hs, L.input_norm, dec->n, rows, hs, a.rms_norm_eps, st);
-        if (rc) return rc;
-        rc = gemm_f16(dec, rows, qkvdim, hs, L.qkv_proj, dec->n, dec->qkv, false, L.qkv_scale);
+        rc = normed_proj(dec, rows, qkvdim, L.qkv_proj, dec->x, L.input_norm, dec->qkv, L.qkv_scale);
         if (rc) return rc;
         rc = qasr_qk_norm_rope_append(dec->ctx, kv, l, segs, nseg, dec->qkv, L.q_norm, L.k_norm,
                                       dec->qw, stream);
@@ -816,6 +1024,7 @@ int qasr_decoder_create(qasr_ctx* ctx, const qasr_decoder_cfg* cfg, const void* 
         {&d->blas_ws, kBlasWorkspace},
         {(void**)&d->sk_ws, (size_t)kSkinnyMaxTiles * kSkinnyMaxGroups * 1024},
         {(void**)&d->sk_ctr, (size_t)kSkinnyMaxTiles * 4},
+        {(void**)&d->ss, (size_t)kSkinnyRows * kNormMaxChunks * 4},
     };
     // The largest int8 projection sets the prefill dequantisation scratch.
     int64_t wdq = 0;
@@ -881,14 +1090,15 @@ int qasr_decoder_step(qasr_decoder* dec, qasr_kv* kv, int batch, const int32_t* 
     const qasr_attn_cfg& a = dec->ctx->cfg;
     const int hs = dec->cfg.hidden_size;
     const int qkvdim = (a.num_attention_heads + 2 * a.num_key_value_heads) * a.head_dim;
+    // Chunk sums for a fused first norm when a skinny batch can use them.
+    dec->ss_valid = dec->fuse && batch <= kSkinnyRows && hs <= kNormMaxK;
     hipLaunchKernelGGL(embed_rows_kernel, dim3(batch), dim3(256), 0, st, dec->embed, tokens_dev,
-                       dec->cfg.vocab_size, hs, dec->x);
+                       dec->cfg.vocab_size, hs, dec->x, dec->ss_valid ? dec->ss : nullptr);
     HIP_TRY(hipGetLastError(), "embedding launch");
     for (int l = 0; l < a.num_hidden_layers; ++l) {
         const qasr_layer_weights& L = dec->layers[l];
-        rc = launch_rms_norm(dec->x, hs, L.input_norm, dec->n, batch, hs, a.rms_norm_eps, st);
-        if (rc) return rc;
-        rc = gemm_f16(dec, batch, qkvdim, hs, L.qkv_proj, dec->n, dec->qkv, false, L.qkv_scale);
+        rc = normed_proj(dec, batch, qkvdim, L.qkv_proj, dec->x, L.input_norm, dec->qkv,
+                         L.qkv_scale);
         if (rc) return rc;
         rc = qasr_decode_step(dec->ctx, kv, l, batch, slots, pos, dec->qkv, L.q_norm, L.k_norm,
                               dec->attn, stream);

@@ -402,10 +402,12 @@ def test_int8_projections_equal_dequantized_f16(gpu, model, batch, blas, monkeyp
                                               ("1.7B", 16, True), ("0.6B", 5, True),
                                               ("0.6B", 4, True)])
 def test_fused_epilogues_equal_unfused(gpu, model, batch, int8, monkeypatch):
-    """The decode step's fused epilogues (gate|up with SiLU * up in one skinny
-    launch) against the same step with them off (QASR_DECODER_FUSE=0:
-    gate|up, then silu_mul_kernel): identical logits and tokens, bitwise --
-    the fusion moves where values are rounded to f16, not how."""
+    """The decode step's fusions -- the input, post-attention and final
+    RMSNorms folded into the qkv, gate|up and logits projections, and gate|up
+    with SiLU * up in one skinny launch -- against the same step with them off
+    (QASR_DECODER_FUSE=0: rms_norm_kernel launches, gate|up, then
+    silu_mul_kernel): identical logits and tokens, bitwise -- the fusion moves
+    where values are rounded to f16, not how."""
     import torch
 
     from decoder_model import CFG_1P7B
