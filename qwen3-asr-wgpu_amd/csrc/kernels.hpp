@@ -87,12 +87,13 @@ struct PrefillArgs {
     float scale_log2;
 };
 
-// Stage (c) plan: row blocks of 64 rows; row block rb's key tiles (128 keys)
-// are split into ceil(tiles / tps) pieces.  Items of a kv head are laid out
+// Stage (c) plan: row blocks of 64 rows (32 for unsplit short key ranges);
+// row block rb's key tiles (128 keys) are split into ceil(tiles / tps) pieces.  Items of a kv head are laid out
 // rb-major: item = kvh*items_per_kvh + sp_base[rb] + split.
 constexpr int kMaxRowBlocks = 64;  // 4096 rows per launch
 constexpr int kPrefillRows = 64;
 struct PrefillPlan {
+    int32_t rows_per_block;  // kPrefillRows, or kPrefillRows / 2 for unsplit short key ranges
     int32_t nrb;
     int32_t tps;
     int32_t items_per_kvh;
@@ -130,7 +131,8 @@ struct PrefillSegs {
     int64_t kv_off[kMaxPrefillSegs];
 };
 
-PrefillPlan plan_prefill(int s, int kv_start, int nkvh, int tiles_per_split);
+PrefillPlan plan_prefill(int s, int kv_start, int nkvh, int tiles_per_split,
+                         int rows_per_block = kPrefillRows);
 hipError_t launch_prefill_attn_segs(const PrefillArgs& a, const PrefillSegs& S, hipStream_t stream);
 hipError_t launch_prefill_attn(const PrefillArgs& a, const PrefillPlan& P, const PrefillWs& ws,
                                hipStream_t stream);

@@ -141,10 +141,11 @@ static_assert(kAllWaves == 8 && kTileKeys == 128, "copy pattern: 32 one-KB block
 // chunk each) hits 16 different slots.  Rows past the block's last row are
 // read from row s-1 (finite values; their outputs are not written).
 constexpr int kQBlockHalves = kRowsPerBlock * kRep * kHeadDim;  // 32 KB
+template <int RB>  // rows of the block: RB / 16 instructions per wave
 __device__ __forceinline__ void dma_q(u32x4v qr, int row0, int last_row, int ldq_bytes, const f16* qdst,
                                       int wave, int lane) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < RB / 16; ++j) {
         const int r = 2 * (8 * j + wave) + (lane >> 5);
         const int c = (lane & 31) ^ (r & 15);
         dma16(qr, min(row0 + r, last_row) * ldq_bytes + c * 16, lds_addr(qdst + (8 * j + wave) * 512));
@@ -169,32 +170,34 @@ struct Wave {
     float scale_log2;
 };
 
-// First half of a 64-key step: S^T from K rows kt[0..63] (first key k0),
-// row max, the running-max update, P^T (f16, B-operand layout) and its row
-// sum.  MASK: some key is past some row's position.
-template <bool MASK>
-__device__ __forceinline__ void step_s(Wave& w, const f16* kt, int k0, half8v (&pb)[4]) {
+// First half of a step over NB * 32 keys: S^T from K rows kt[0..32 NB - 1]
+// (first key k0), row max, the running-max update, P^T (f16, B-operand
+// layout) and its row sum.  MASK: some key is past some row's position.
+template <bool MASK, int NB>
+__device__ __forceinline__ void step_s(Wave& w, const f16* kt, int k0, half8v (&pb)[2 * NB]) {
     // S^T: keys kb*32 + (8*(i/4) + 4*g + i%4) x query n, accumulated over dims.
-    float16v s[2] = {(float16v){}, (float16v){}};
+    float16v s[NB];
+#pragma unroll
+    for (int kb = 0; kb < NB; ++kb) s[kb] = (float16v){};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
+        for (int kb = 0; kb < NB; ++kb) {
             const half8v ka = *(const half8v*)&kt[kb * 32 * kHeadDim + w.kaddr[ks]];
             s[kb] = mfma32(ka, w.qb[ks], s[kb]);
         }
     // Operand reads run at most two k-steps ahead of the MFMAs (bounded
-    // register lifetime; 16 reads + 16 MFMAs).
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    // register lifetime; 8 NB reads + 8 NB MFMAs).
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * NB, 0);
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, NB, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, NB, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 2 * NB, 0);
     float mx = kNegInf;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < NB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             if (MASK) {
@@ -220,14 +223,14 @@ __device__ __forceinline__ void step_s(Wave& w, const f16* kt, int k0, half8v (&
     // P^T = 2^(s*scale_log2 - m), k-step w4 covering keys 16*w4 + 4*g +
     // {0..3, 8..11}; the row sum from the same f16 values (v_dot2, f32 sum).
 #pragma unroll
-    for (int w4 = 0; w4 < 4; ++w4)
+    for (int w4 = 0; w4 < 2 * NB; ++w4)
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             pb[w4][j] = (f16)softmax_w_raw(s[w4 >> 1][8 * (w4 & 1) + j], w.scale_log2, mu);
     const half2v ones2 = {(f16)1.0f, (f16)1.0f};
     float ps = 0.0f;
 #pragma unroll
-    for (int w4 = 0; w4 < 4; ++w4)
+    for (int w4 = 0; w4 < 2 * NB; ++w4)
 #pragma unroll
         for (int q2 = 0; q2 < 4; ++q2) {
             const half2v pr = {pb[w4][2 * q2], pb[w4][2 * q2 + 1]};
@@ -236,11 +239,12 @@ __device__ __forceinline__ void step_s(Wave& w, const f16* kt, int k0, half8v (&
     w.l += halves_sum(ps);
 }
 
-// Second half: O^T += V^T P^T with V rows vt[0..63] (slab stride
+// Second half: O^T += V^T P^T with V rows vt[0..32 NB - 1] (slab stride
 // kTileKeys*32 halves).
-__device__ __forceinline__ void step_pv(Wave& w, const f16* vt, const half8v (&pb)[4]) {
+template <int NB>
+__device__ __forceinline__ void step_pv(Wave& w, const f16* vt, const half8v (&pb)[2 * NB]) {
 #pragma unroll
-    for (int w4 = 0; w4 < 4; ++w4)
+    for (int w4 = 0; w4 < 2 * NB; ++w4)
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
             const f16* vp = vt + w.vbase + db * (kTileKeys * 32) + w4 * 16 * 32;
@@ -252,7 +256,7 @@ __device__ __forceinline__ void step_pv(Wave& w, const f16* vt, const half8v (&p
     // Two transposing reads per MFMA, at most two MFMAs ahead.
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-    for (int i = 0; i < 14; ++i) {
+    for (int i = 0; i < 8 * NB - 2; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
@@ -339,10 +343,65 @@ struct EpiArgs {
     f16* K1;
     f16* V0;
     f16* V1;
+    f16* Q;
     int item, kvh, rb, nsp, rw, r, head;
     bool row_ok;
     int g, lane, tid;
 };
+
+// Epilogue of a 32-row block (four key groups of 32 keys per row wave, no
+// split): wave (rw, KG) finishes dim block KG.  Each wave leaves its other
+// three blocks (16 accumulator elements x 64 lanes, element-major) and its
+// (m, l) in LDS -- the tile buffers and the free half of the Q block -- and
+// combines the four partials of its block in key-group order.
+template <int KG>
+__device__ __forceinline__ void epilogue4(Wave& w, const EpiArgs& e) {
+    const int lane = e.lane, rw = e.rw;
+    // Partials of row wave rw, key group src: 16 KB at (rw ? V : K)(src >> 1)
+    // + (src & 1) * 16 KB, dim block db at + db * 4 KB.
+    auto blk = [&](int src, int db) {
+        f16* b = rw ? (src < 2 ? e.V0 : e.V1) : (src < 2 ? e.K0 : e.K1);
+        return reinterpret_cast<float*>(b) + (src & 1) * 4096 + db * 1024;
+    };
+    float* ml = reinterpret_cast<float*>(e.Q + kQBlockHalves / 2) + rw * 4 * 128;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+        if (db == KG) continue;
+        float* dst = blk(KG, db);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dst[i * 64 + lane] = w.o[db][i];
+    }
+    ml[KG * 128 + lane] = w.m;
+    ml[KG * 128 + 64 + lane] = w.l;
+    __syncthreads();
+    float mj[4], lj[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        mj[j] = j == KG ? w.m : ml[j * 128 + lane];
+        lj[j] = j == KG ? w.l : ml[j * 128 + 64 + lane];
+    }
+    const float M = fmaxf(fmaxf(mj[0], mj[1]), fmaxf(mj[2], mj[3]));
+    float L = 0.0f;
+    float16v o = (float16v){};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float aj = mj[j] == kNegInf ? 0.0f : fast_exp2(mj[j] - M);
+        L = fmaf(lj[j], aj, L);
+        const float* src = blk(j, KG);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[i] = fmaf(j == KG ? w.o[KG][i] : src[i * 64 + lane], aj, o[i]);
+    }
+    if (!e.row_ok) return;
+    const float inv = 1.0f / L;
+    f16* orow = e.a.out + (int64_t)e.r * (e.a.nqh * kHeadDim) + e.head * kHeadDim;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+        half4v h4;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) h4[x] = (f16)(o[q4 * 4 + x] * inv);
+        *(half4v*)(orow + KG * 32 + 8 * q4 + 4 * e.g) = h4;
+    }
+}
 
 // Epilogue of the wave of key group KG: wave (rw, KG) keeps dim blocks 2*KG
 // and 2*KG+1 of the output and hands the other two blocks, with its (m, l),
@@ -434,7 +493,12 @@ __device__ __forceinline__ void epilogue(Wave& w, const EpiArgs& e) {
     if (e.tid == 0) ticket_reset(ctr);
 }
 
-template <bool MULTI>
+// NKG = 2: 64-row blocks, row wave rw = wave & 3 (2 q heads x 2 x 32 rows),
+// key group kg = wave >> 2 taking keys 64 kg .. +64 of every tile.  NKG = 4
+// (unsplit short key ranges): 32-row blocks, rw = wave & 1 (the 2 q heads),
+// kg = wave >> 1 taking keys 32 kg .. +32 -- half the work per workgroup and
+// twice the workgroups.
+template <bool MULTI, int NKG>
 __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     PrefillArgs a, PrefillPlan P, PrefillSegs S, float* __restrict__ ws_o,
     float* __restrict__ ws_ml, uint32_t* __restrict__ counters) {
@@ -447,9 +511,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
+    constexpr int kRowWaves = kAllWaves / NKG;
+    constexpr int RB = 16 * kRowWaves;        // rows per block: 64 or 32
+    constexpr int GK = kTileKeys / NKG;       // keys per key group and tile: 64 or 32
+    constexpr int NB = GK / 32;               // 32-key MFMA blocks per step
+    static_assert(!MULTI || NKG == 2, "segment launches use 64-row blocks");
     const int wave = tid >> 6;       // 0..7: copy slot
-    const int rw = wave & 3;         // row wave
-    const int kg = wave >> 2;        // key group
+    const int rw = wave % kRowWaves; // row wave
+    const int kg = wave / kRowWaves; // key group
     const int n = lane & 31;  // query column within the wave's 32 rows
     const int g = lane >> 5;  // k-slot group of the MFMA operands
 
@@ -487,8 +556,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
         nsp = P.sp_base[rb + 1] - P.sp_base[rb];
         tps = P.tps;
     }
-    const int row0 = rb * kRowsPerBlock;
-    const int kend = a.kv_start + min(row0 + kRowsPerBlock, a.s);  // keys < kend
+    const int row0 = rb * RB;
+    const int kend = a.kv_start + min(row0 + RB, a.s);  // keys < kend
     const int ntiles = (kend + kTileKeys - 1) / kTileKeys;
     const int t_begin = sp * tps;
     const int t_end = min(t_begin + tps, ntiles);
@@ -516,7 +585,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     const u32x4v qres = make_rsrc_words(a.q + kvh * kRep * kHeadDim,
                                         (a.s - 1) * ldq * 2 + kRep * kHeadDim * 2);
     dma_tile(kres, vres, t_begin * kTileKeys, kend, krow, kchunk, vrow, vchunk, K0, V0, wave);
-    dma_q(qres, row0, a.s - 1, ldq * 2, Qs, wave, lane);
+    dma_q<RB>(qres, row0, a.s - 1, ldq * 2, Qs, wave, lane);
     const bool two = t_begin + 1 < t_end;
     if (two) dma_tile(kres, vres, (t_begin + 1) * kTileKeys, kend, krow, kchunk, vrow, vchunk, K1, V1, wave);
 
@@ -548,16 +617,16 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     // copy of tile t+2 into them.  Two tiles per iteration, so every LDS
     // address is a per-lane base plus a constant.
     auto run = [&](const f16* kt, const f16* vt, int t) {
-        const int k0 = t * kTileKeys + kg * kGroupKeys;
+        const int k0 = t * kTileKeys + kg * GK;
         if (k0 <= last_pos) {  // some key visible to some row
-            const f16* kh = kt + kg * kGroupKeys * kHeadDim;
-            const f16* vh = vt + kg * kGroupKeys * 32;
-            half8v pb[4];
-            if (k0 + kGroupKeys - 1 <= first_pos)  // no key masked
-                step_s<false>(w, kh, k0, pb);
+            const f16* kh = kt + kg * GK * kHeadDim;
+            const f16* vh = vt + kg * GK * 32;
+            half8v pb[2 * NB];
+            if (k0 + GK - 1 <= first_pos)  // no key masked
+                step_s<false, NB>(w, kh, k0, pb);
             else
-                step_s<true>(w, kh, k0, pb);
-            step_pv(w, vh, pb);
+                step_s<true, NB>(w, kh, k0, pb);
+            step_pv<NB>(w, vh, pb);
         }
         tile_sync();
         if (t + 2 < t_end)
@@ -589,22 +658,32 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     // The two key groups of a row wave combine through LDS (the tile buffers
     // are free now); from here on both waves of a pair share the epilogue
     // work half and half.
-    EpiArgs e{a, P, ws_o, ws_ml, counters, K0, K1, V0, V1, item, kvh, rb, nsp, rw, r, head, row_ok, g, lane, tid};
-    if (kg == 0)
-        epilogue<0>(w, e);
-    else
-        epilogue<1>(w, e);
+    EpiArgs e{a, P, ws_o, ws_ml, counters, K0, K1, V0, V1, Qs, item, kvh, rb, nsp, rw, r, head, row_ok, g, lane, tid};
+    if constexpr (NKG == 2) {
+        if (kg == 0)
+            epilogue<0>(w, e);
+        else
+            epilogue<1>(w, e);
+    } else {
+        switch (kg) {
+            case 0: epilogue4<0>(w, e); break;
+            case 1: epilogue4<1>(w, e); break;
+            case 2: epilogue4<2>(w, e); break;
+            default: epilogue4<3>(w, e); break;
+        }
+    }
 }
 
 }  // namespace
 
-PrefillPlan plan_prefill(int s, int kv_start, int nkvh, int tiles_per_split) {
+PrefillPlan plan_prefill(int s, int kv_start, int nkvh, int tiles_per_split, int rows_per_block) {
     PrefillPlan P{};
-    P.nrb = (s + kRowsPerBlock - 1) / kRowsPerBlock;
+    P.rows_per_block = rows_per_block;
+    P.nrb = (s + rows_per_block - 1) / rows_per_block;
     P.tps = tiles_per_split;
     P.sp_base[0] = 0;
     for (int rb = 0; rb < P.nrb; ++rb) {
-        const int kend = kv_start + std::min((rb + 1) * kRowsPerBlock, s);
+        const int kend = kv_start + std::min((rb + 1) * rows_per_block, s);
         const int ntiles = (kend + kTileKeys - 1) / kTileKeys;
         P.sp_base[rb + 1] = P.sp_base[rb] + (ntiles + P.tps - 1) / P.tps;
     }
@@ -618,8 +697,17 @@ hipError_t launch_prefill_attn(const PrefillArgs& a, const PrefillPlan& P, const
     const int items = P.items_per_kvh * a.nkvh;
     if (items <= 0) return hipSuccess;
     if (items > ws.items || P.nrb > kMaxRowBlocks) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(prefill_attn_kernel<false>, dim3(items), dim3(kThreads), 0, stream, a, P,
-                       PrefillSegs{}, ws.o, ws.ml, ws.counters);
+    if (P.rows_per_block == kRowsPerBlock / 2) {
+        // 32-row blocks: unsplit items only (their epilogue has no merge).
+        if (P.items_per_kvh != P.nrb) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((prefill_attn_kernel<false, 4>), dim3(items), dim3(kThreads), 0, stream,
+                           a, P, PrefillSegs{}, ws.o, ws.ml, ws.counters);
+    } else if (P.rows_per_block == kRowsPerBlock) {
+        hipLaunchKernelGGL((prefill_attn_kernel<false, 2>), dim3(items), dim3(kThreads), 0, stream,
+                           a, P, PrefillSegs{}, ws.o, ws.ml, ws.counters);
+    } else {
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
@@ -627,7 +715,7 @@ hipError_t launch_prefill_attn_segs(const PrefillArgs& a, const PrefillSegs& S, 
     if (S.n <= 0 || S.n > kMaxPrefillSegs) return hipErrorInvalidValue;
     const int items = S.item_base[S.n];
     if (items <= 0) return hipSuccess;
-    hipLaunchKernelGGL(prefill_attn_kernel<true>, dim3(items), dim3(kThreads), 0, stream, a,
+    hipLaunchKernelGGL((prefill_attn_kernel<true, 2>), dim3(items), dim3(kThreads), 0, stream, a,
                        PrefillPlan{}, S, nullptr, nullptr, nullptr);
     return hipGetLastError();
 }

@@ -340,22 +340,29 @@ int run_prefill(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, i
         // (publish, ticket, read back) is about three memory round trips, as
         // long as several latency-bound tiles: key ranges of up to
         // kPrefillNoSplitTiles tiles are never split.
+        // Unsplit short ranges also take 32-row blocks: twice the workgroups,
+        // half the work on the longest one (a forced split count keeps
+        // 64-row blocks).
         int tps = tps_forced;
+        int rb_rows = qasr::kPrefillRows;
         if (tps <= 0) {
             const int64_t tiles_all = (int64_t)nrb * max_tiles;
             const int64_t want = std::max<int64_t>(1, 256 / nkvh);
-            tps = max_tiles <= kPrefillNoSplitTiles
-                      ? max_tiles
-                      : (int)std::max<int64_t>(2, (tiles_all + want - 1) / want);
+            if (max_tiles <= kPrefillNoSplitTiles) {
+                tps = max_tiles;
+                rb_rows = qasr::kPrefillRows / 2;
+            } else {
+                tps = (int)std::max<int64_t>(2, (tiles_all + want - 1) / want);
+            }
         }
-        qasr::PrefillPlan P = qasr::plan_prefill(rows, ks, nkvh, tps);
+        qasr::PrefillPlan P = qasr::plan_prefill(rows, ks, nkvh, tps, rb_rows);
         if (noalloc) {
             // Coarser splits until the partials fit the scratch array; at
             // tps = max_tiles every row block is one item (s is bounded so
             // that this fits).
             while ((int64_t)P.items_per_kvh * nkvh > kScratchItems && tps < max_tiles) {
                 tps = std::min(max_tiles, tps * 2);
-                P = qasr::plan_prefill(rows, ks, nkvh, tps);
+                P = qasr::plan_prefill(rows, ks, nkvh, tps, rb_rows);
             }
             if ((int64_t)P.items_per_kvh * nkvh > kScratchItems)
                 return fail(QASR_EINVAL, "prefill plan of %lld items exceeds the scratch's %lld",

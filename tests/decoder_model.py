@@ -280,4 +280,7 @@ def compare_greedy(cpu, gpu, label: str, rel_logit_tol: float = 0.02):
                                  f"{tg} (CPU top-2 gap {gap:.4g}, logit diff {d:.4g})")
     print(f"{label}: {len(cpu)} steps identical; min top-2 gap {min_gap:.4g}, "
           f"max logit diff {worst_diff:.4g}", flush=True)
+    from workloads import REPORT
+    REPORT.append({"label": f"greedy {label}", "steps": len(cpu), "min_top2_gap": min_gap,
+                   "max_logit_diff": worst_diff})
     return len(cpu)

@@ -84,10 +84,10 @@ def test_e2e_greedy_two_slots_chunked_prefill_split_decode(O, gpu):
     cfg = dict(CFG_0P6B, layers=2)
     lens, steps, chunk = [1100, 700], 12, 512
     cap = _cap(max(lens) + steps + 1)
-    W = synth_weights(cfg, SEED_BASE + 910, device="cuda")
+    W = synth_weights(cfg, SEED_BASE + 930, device="cuda")
     Wh = host_bits(W)
     cos, sin = O.text_rope_tables_f16(cfg["max_seq"])
-    prompts = [_prompt(SEED_BASE + 911 + i, L, cfg["hs"]) for i, L in enumerate(lens)]
+    prompts = [_prompt(SEED_BASE + 931 + i, L, cfg["hs"]) for i, L in enumerate(lens)]
 
     cpu_out = []
     for i, L in enumerate(lens):
