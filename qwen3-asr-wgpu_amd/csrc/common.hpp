@@ -30,6 +30,25 @@ union H8 {
     f16 e[8];
 };
 
+// ---- direct global -> LDS copies ---------------------------------------
+// A buffer resource as four dwords (for inline asm), `bytes` the range past
+// which loads return zeros (and copies write nothing).
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4v make_rsrc_words(const void* p, int bytes) {
+    const uint64_t a = (uint64_t)p;
+    return (u32x4v){(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)bytes, 0x00020000u};
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// One `buffer_load_dwordx4 ... lds`: lane l's 16 bytes from byte offset voff
+// of the resource land at LDS address lds + 16 l (M0 = lds).  Issued as
+// inline asm, so the compiler does not wait for it before unrelated LDS
+// reads; the caller waits for it itself (vmcnt) before reading its bytes.
+__device__ __forceinline__ void dma16(u32x4v rsrc, int voff, uint32_t lds) {
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
+}
+
 // ---- DPP cross-lane moves inside a 16-lane row (no LDS traffic) ----------
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {

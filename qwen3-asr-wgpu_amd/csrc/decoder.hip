@@ -403,6 +403,88 @@ struct NormPrologue {
     }
 };
 
+// A finished 16 x 16 output tile (column tile `tile`): lane l holds
+// D[4(l/16) + i][l%16], i < 4, in `sum`, summed over this workgroup's K range.
+// With K groups, the group partials are published and the last of the tile's
+// workgroups to arrive (ticket) sums them in group order.  Then the outputs
+// per OUT (see skinny_gemm_kernel), and for kOutAcc with ss_out the result
+// rows' chunk sums of squares.  s_y: 256 floats of this wave's LDS.
+template <int OUT>
+__device__ __forceinline__ void skinny_tile_out(const SkinnyArgs& p, qasr::float4v sum, int tile,
+                                                int group, int lane, float* s_y) {
+    const int r = lane & 15, g = lane >> 4;
+    const int M = p.M, N = p.N, groups = p.groups;
+    const int n0 = tile * 16;
+    constexpr bool kGlu = OUT == kOutGlu;
+    if (groups > 1) {
+        // This wave's stores complete (vmcnt(0)) before the ticket, and the
+        // last arrival reads every group's partial with device-coherent
+        // loads.
+        float* mine = p.ws + ((int64_t)tile * groups + group) * 256 + lane * 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qasr::store_dev(&mine[i], sum[i]);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        uint32_t old = 0;
+        if (lane == 0) old = qasr::ticket_add(&p.counters[tile]);
+        old = __builtin_amdgcn_readfirstlane(old);
+        if (old != (uint32_t)(groups - 1)) return;
+        const __amdgpu_buffer_rsrc_t pres = rsrc(p.ws + (int64_t)tile * groups * 256, (int64_t)groups * 1024);
+        sum = qasr::float4v{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int grp = 0; grp < groups; ++grp)
+            sum += __builtin_bit_cast(qasr::float4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         pres, (grp * 64 + lane) * 16, 0, kSc1));
+        if (lane == 0) qasr::ticket_reset(&p.counters[tile]);
+    }
+    const int n = n0 + r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * g + i;
+        if constexpr (kGlu) {
+            // Lanes r and r^8 (same rows) exchange gate and up; every lane of
+            // the wave takes part in the shuffle.
+            const float v = (float)(f16)sum[i];
+            const float up = __shfl_xor(v, 8);
+            if (r < 8 && m < M)
+                ((f16*)p.Y)[(int64_t)m * (N / 2) + 8 * tile + r] = f16_of_f32(silu_times(v, up));
+            continue;
+        }
+        if (m >= M) continue;
+        const int64_t idx = (int64_t)m * N + n;
+        if constexpr (OUT == kOutF32) {
+            ((float*)p.Y)[idx] = sum[i];
+        } else {
+            f16* y = (f16*)p.Y;
+            const f16 out = (f16)(OUT == kOutAcc ? (float)y[idx] + sum[i] : sum[i]);
+            y[idx] = out;
+            if constexpr (OUT == kOutAcc) sum[i] = (float)out;  // for the chunk sums below
+        }
+    }
+    if constexpr (OUT == kOutAcc) {
+        if (p.ss_out) {
+            // The next projection's half of a fused RMSNorm: this tile's two
+            // 8-column chunks of every result row, squares summed with fmaf
+            // in column order (rms_norm_kernel's per-thread sum), via this
+            // wave's LDS scratch s_y ([16 rows][16 columns]).
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s_y[(4 * g + i) * 16 + r] = sum[i];
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            __builtin_amdgcn_wave_barrier();
+            const int row = lane >> 1, ch = lane & 1;
+            if (lane < 32 && row < M) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float f = s_y[row * 16 + 8 * ch + e];
+                    ss = fmaf(f, f, ss);
+                }
+                p.ss_out[row * kNormMaxChunks + 2 * tile + ch] = ss;
+            }
+        }
+    }
+}
+
 template <int KS, int U, bool W8, int OUT, bool NORM>
 __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
     __shared__ qasr::float4v s_red[KS][64];
@@ -515,73 +597,132 @@ __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
     qasr::float4v sum = s_red[0][lane];
 #pragma unroll
     for (int w = 1; w < KS; ++w) sum += s_red[w][lane];
-    if (groups > 1) {
-        // Only wave 0 is left: its stores complete (vmcnt(0)) before the
-        // ticket, and the last arrival reads every group's partial with
-        // device-coherent loads.
-        float* mine = p.ws + ((int64_t)tile * groups + blockIdx.y) * 256 + lane * 4;
+    skinny_tile_out<OUT>(p, sum, tile, blockIdx.y, lane, reinterpret_cast<float*>(&s_red[0][0]));
+}
+
+// ---- skinny GEMM with the weight rows staged in LDS ------------------------
+// The same product as skinny_gemm_kernel, for very wide outputs: a workgroup
+// is 4 waves over `tpw` consecutive column tiles of one K group, and wave w
+// takes K range [(group*4 + w) kw, +kw), kw = 32 NKS.  The wave loads its
+// activation slice once, into registers (normed there once when NORM), and
+// uses it for all its tiles -- skinny_gemm_kernel reloads it with every
+// k-step of every tile, as many bytes as the weights at 16 rows.  Each tile's
+// 16 row slices stream by direct global->LDS copies (1024 / RB rows per copy
+// instruction, every row slice one contiguous run) into the wave's own LDS
+// buffer -- NBUF of them, so tile t+2 streams while t+1 is next -- and the
+// MFMA B operand is read back from LDS.  No wave reads another's buffer, so
+// the stream needs no barrier; each wave leaves its per-tile partial in LDS,
+// and after the last tile wave w finishes tiles w, w+4, .. (the four partials
+// summed in wave order, then skinny_tile_out).  Copies are waited for by
+// count (they are inline asm); the epilogues' stores come after the last
+// copy.  LDS row slice layout: 16-byte chunk c of row n at slot c ^ n, so
+// the operand read (16 rows at one k) is conflict-free.
+constexpr int kLdsWaves = 4;
+constexpr int kLdsMaxTiles = 4;     // column tiles per workgroup
+constexpr int kLdsMinTiles = 2048;  // outputs at least this wide ..
+constexpr int kLdsMinRows = 8;      // .. of at least this many rows take the kernel
+
+template <int NKS, bool W8, int OUT, bool NORM, int NBUF>
+__global__ __launch_bounds__(kLdsWaves * 64) void skinny_lds_kernel(SkinnyArgs p, int tpw) {
+    constexpr int wbytes = W8 ? 1 : 2;
+    constexpr int KW = 32 * NKS;     // K per wave
+    constexpr int RB = KW * wbytes;  // bytes of one row slice
+    static_assert(RB >= 256 && RB <= 1024, "row slices of 256..1024 bytes");
+    constexpr int LPR = RB / 16;   // copy lanes per row, 16..64
+    constexpr int RPI = 64 / LPR;  // rows per copy instruction, 1..4
+    constexpr int NCP = 16 / RPI;  // copy instructions per tile and wave
+    constexpr int TB = 16 * RB;    // one wave's tile buffer
+    __shared__ __attribute__((aligned(16))) char s_w[NBUF][kLdsWaves][TB];
+    __shared__ qasr::float4v s_acc[NBUF > 1 ? kLdsMaxTiles : 1][kLdsWaves][64];
+    __shared__ float s_y[OUT == kOutAcc ? kLdsWaves : 1][256];
+    __shared__ __attribute__((aligned(16))) float s_gain[NORM ? kNormMaxK : 1];
+    __shared__ float s_part[NORM ? kSkinnyRows * 4 : 1];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int M = p.M, N = p.N, K = p.K;
+    const int t0 = blockIdx.x * tpw;
+    const int nt = min(tpw, N / 16 - t0);
+    const int kbeg = (blockIdx.y * kLdsWaves + wave) * KW;
+    constexpr bool kGlu = OUT == kOutGlu;
+    // W row of row i (0..15) of column tile t: 16t + i, or for kOutGlu gate
+    // rows 8t..8t+7 then up rows N/2 + 8t..
+    auto wrow = [&](int t, int i) { return kGlu ? (i < 8 ? 8 * t + i : N / 2 + 8 * t + i - 8) : 16 * t + i; };
+    const qasr::u32x4v wres = qasr::make_rsrc_words(p.W, N * K * wbytes);  // < 2^31 (host-checked)
+    auto copy_tile = [&](int t, int b) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qasr::store_dev(&mine[i], sum[i]);
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        uint32_t old = 0;
-        if (lane == 0) old = qasr::ticket_add(&p.counters[tile]);
-        old = __builtin_amdgcn_readfirstlane(old);
-        if (old != (uint32_t)(groups - 1)) return;
-        const __amdgpu_buffer_rsrc_t pres = rsrc(p.ws + (int64_t)tile * groups * 256, (int64_t)groups * 1024);
-        sum = qasr::float4v{0.0f, 0.0f, 0.0f, 0.0f};
-        for (int grp = 0; grp < groups; ++grp)
-            sum += __builtin_bit_cast(qasr::float4v, __builtin_amdgcn_raw_buffer_load_b128(
-                                                         pres, (grp * 64 + lane) * 16, 0, kSc1));
-        if (lane == 0) qasr::ticket_reset(&p.counters[tile]);
-    }
-    const int n = n0 + r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = 4 * g + i;
-        if constexpr (kGlu) {
-            // Lanes r and r^8 (same rows) exchange gate and up; every lane of
-            // the wave takes part in the shuffle.
-            const float v = (float)(f16)sum[i];
-            const float up = __shfl_xor(v, 8);
-            if (r < 8 && m < M)
-                ((f16*)p.Y)[(int64_t)m * (N / 2) + 8 * tile + r] = f16_of_f32(silu_times(v, up));
-            continue;
+        for (int i = 0; i < NCP; ++i) {
+            const int row = i * RPI + lane / LPR;
+            const int chunk = (lane % LPR) ^ row;
+            qasr::dma16(wres, wrow(t, row) * K * wbytes + kbeg * wbytes + chunk * 16,
+                        qasr::lds_addr(&s_w[b][wave][i * 1024]));
         }
-        if (m >= M) continue;
-        const int64_t idx = (int64_t)m * N + n;
-        if constexpr (OUT == kOutF32) {
-            ((float*)p.Y)[idx] = sum[i];
-        } else {
-            f16* y = (f16*)p.Y;
-            const f16 out = (f16)(OUT == kOutAcc ? (float)y[idx] + sum[i] : sum[i]);
-            y[idx] = out;
-            if constexpr (OUT == kOutAcc) sum[i] = (float)out;  // for the chunk sums below
+    };
+
+    // The fused norm's loads, the activation slice and (int8) this lane's
+    // row scales first, then the first tiles' copies.
+    NormPrologue<kLdsWaves> np;
+    if constexpr (NORM) np.issue(p, wave, lane);
+    const __amdgpu_buffer_rsrc_t xres = rsrc(p.X, (int64_t)M * K * 2);
+    qasr::half8v xr[NKS];
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) xr[s] = load8(xres, (r * K + kbeg + 32 * s + 8 * g) * 2);
+    float wsc[kLdsMaxTiles] = {};
+    if constexpr (W8) {
+#pragma unroll
+        for (int t = 0; t < kLdsMaxTiles; ++t)
+            if (t < nt) wsc[t] = p.scale[wrow(t0 + t, r)];
+    }
+    copy_tile(t0, 0);
+    if (NBUF > 1 && nt > 1) copy_tile(t0 + 1, 1);
+    if constexpr (NORM) {
+        const float inv = np.finish(p, s_gain, s_part, wave, lane, r);
+#pragma unroll
+        for (int s = 0; s < NKS; ++s) {
+            const int k = kbeg + 32 * s + 8 * g;
+            const float4 g0 = *(const float4*)&s_gain[k];
+            const float4 g1 = *(const float4*)&s_gain[k + 4];
+            const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xr[s][e] = f16_of_f32(((float)xr[s][e] * inv) * gv[e]);
         }
     }
-    if constexpr (OUT == kOutAcc) {
-        if (p.ss_out) {
-            // The next projection's half of a fused RMSNorm: this tile's two
-            // 8-column chunks of every result row, squares summed with fmaf
-            // in column order (rms_norm_kernel's per-thread sum), via LDS
-            // (only this wave is left; s_red is free).
-            float* s_y = reinterpret_cast<float*>(&s_red[0][0]);  // [16 rows][16 columns]
+
+    for (int t = 0; t < nt; ++t) {
+        const int b = NBUF > 1 ? (t & 1) : 0;
+        // This wave's copies of tile t have landed (tile t+1's may not).
+        if (NBUF > 1 && t + 1 < nt)
+            __builtin_amdgcn_s_waitcnt(0x0F70 | (NCP & 15) | ((NCP >> 4) << 14));  // vmcnt(NCP)
+        else
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        const char* buf = &s_w[b][wave][0];
+        const float ws = t == 0 ? wsc[0] : t == 1 ? wsc[1] : t == 2 ? wsc[2] : wsc[3];
+        qasr::float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s_y[(4 * g + i) * 16 + r] = sum[i];
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-            __builtin_amdgcn_wave_barrier();
-            const int row = lane >> 1, ch = lane & 1;
-            if (lane < 32 && row < M) {
-                float ss = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float f = s_y[row * 16 + 8 * ch + e];
-                    ss = fmaf(f, f, ss);
-                }
-                p.ss_out[row * kNormMaxChunks + 2 * tile + ch] = ss;
+        for (int s = 0; s < NKS; ++s) {
+            const int c = 4 * s + g;  // this k-step's 8 weights: bytes [c * 8 wbytes, +8 wbytes)
+            qasr::half8v bw;
+            if constexpr (W8) {
+                const uint2 q = *(const uint2*)(buf + r * RB + (((c >> 1) ^ r) * 16) + (c & 1) * 8);
+                bw = dequant8(q.x, q.y, ws);
+            } else {
+                bw = *(const qasr::half8v*)(buf + r * RB + ((c ^ r) * 16));
             }
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xr[s], bw, acc, 0, 0, 0);
         }
+        s_acc[t][wave][lane] = acc;
+        if (t + NBUF < nt) {
+            // Refill this buffer once this wave's reads of it have returned.
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            copy_tile(t0 + t + NBUF, b);
+        }
+    }
+    __syncthreads();
+    for (int t = wave; t < nt; t += kLdsWaves) {
+        qasr::float4v sum = s_acc[t][0][lane];
+#pragma unroll
+        for (int w = 1; w < kLdsWaves; ++w) sum += s_acc[t][w][lane];
+        skinny_tile_out<OUT>(p, sum, t0 + t, blockIdx.y, lane, s_y[OUT == kOutAcc ? wave : 0]);
     }
 }
 
@@ -600,6 +741,8 @@ struct qasr_decoder {
     hipStream_t stream = nullptr;  // of the call in progress
     bool force_blas = false;       // QASR_DECODER_BLAS=1: every projection through rocBLAS
     bool fuse = true;              // QASR_DECODER_FUSE=0: no fused epilogues (same results)
+    int lds_gemm = 1;              // QASR_SKINNY_LDS: 0 older kernel only, 2 LDS kernel wherever it fits
+    int lds_tpw = 0, lds_groups = 0;  // QASR_SKINNY_TPW / _GROUPS: shape overrides (0 = planner)
     // activations, max_rows rows each
     f16* x = nullptr;     // residual stream [rows][hs]
     f16* n = nullptr;     // normed rows [rows][hs]
@@ -646,12 +789,51 @@ void free_decoder(qasr_decoder* d) {
 // partial merge costs ~2 us, repaid only by a long stream; at 2048 x 6144,
 // 2 groups beat 1, 3 and 6 by 20-65 us per 28-layer step, f16 and int8
 // alike).  ks = 0: not a skinny shape (rocBLAS then).
+// The LDS-staged kernel (nks > 0) takes very wide outputs (at least
+// kLdsMinTiles column tiles: the logits' 9,496) of at least kLdsMinRows
+// activation rows whose K splits into 4 waves x `groups` slices of 512 or 256
+// weights, 4 column tiles per workgroup: there one activation slice in
+// registers serves four tiles, and the lm_head step measured 135 us against
+// 161 us (1.7B, 16 rows; the whole step 1.976 against 2.003 ms).  With one
+// row there are no activation bytes to save and it lost (0.6B step 0.989
+// against 0.974 ms).  At the projections' widths
+// (128-768 tiles) it measured no faster than skinny_gemm_kernel (qkv 8.7
+// against 8.4 us, gate|up 18.4 against 17.5 us), so those keep it.
+// QASR_SKINNY_LDS=0 / =2 select the older kernel everywhere / the LDS kernel
+// at every shape it takes; QASR_SKINNY_TPW / QASR_SKINNY_GROUPS override its
+// tiles per workgroup and K groups (sweeps).
 struct SkinnyShape {
     int ks = 0, groups = 1;
+    int nks = 0, tpw = 1, nbuf = 1;  // nks > 0: skinny_lds_kernel
 };
 
-SkinnyShape skinny_shape(qasr_decoder* d, int rows, int n_out, int k) {
+SkinnyShape lds_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8) {
+    SkinnyShape sh{};
+    const int tiles = n_out / 16;
+    if ((int64_t)n_out * k * (w8 ? 1 : 2) >= (int64_t(1) << 31)) return sh;
+    if ((tiles < kLdsMinTiles || rows < kLdsMinRows) && d->lds_gemm < 2) return sh;
+    for (int g = 1; g <= kSkinnyMaxGroups && !sh.nks; ++g) {
+        if (d->lds_groups > 0 && g != d->lds_groups) continue;
+        if (k % (4 * g)) continue;
+        const int kw = k / (4 * g);
+        if ((kw == 512 || kw == 256) && (g == 1 || tiles <= kSkinnyMaxTiles)) {
+            sh.nks = kw / 32;
+            sh.groups = g;
+        }
+    }
+    if (!sh.nks) return sh;
+    sh.tpw = d->lds_tpw > 0 ? std::min(d->lds_tpw, kLdsMaxTiles) : (tiles >= kLdsMinTiles ? 4 : 1);
+    if (sh.groups > 1) sh.tpw = 1;
+    sh.nbuf = sh.tpw > 1 ? 2 : 1;  // tpw == 1 <=> one buffer (s_acc holds one tile then)
+    return sh;
+}
+
+SkinnyShape skinny_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8 = false) {
     if (d->force_blas || rows > kSkinnyRows || n_out % 16) return SkinnyShape{};
+    if (d->lds_gemm) {
+        const SkinnyShape sh = lds_shape(d, rows, n_out, k, w8);
+        if (sh.nks) return sh;
+    }
     const int tiles = n_out / 16;
     if (tiles >= kSkinnyTargetWgs) return SkinnyShape{k % (4 * kSkinnyPair) ? 0 : 4, 1};
     if (k >= 4096)
@@ -687,8 +869,29 @@ int launch_skinny_w(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
     return QASR_OK;
 }
 
+template <bool W8, int OUT, bool NORM>
+int launch_skinny_lds(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
+    const dim3 grid((a.N / 16 + sh.tpw - 1) / sh.tpw, sh.groups);
+    const dim3 block(kLdsWaves * 64);
+    if (sh.nks == 16 && sh.nbuf == 2)
+        hipLaunchKernelGGL((skinny_lds_kernel<16, W8, OUT, NORM, 2>), grid, block, 0, d->stream, a, sh.tpw);
+    else if (sh.nks == 16)
+        hipLaunchKernelGGL((skinny_lds_kernel<16, W8, OUT, NORM, 1>), grid, block, 0, d->stream, a, sh.tpw);
+    else if (sh.nks == 8 && sh.nbuf == 2)
+        hipLaunchKernelGGL((skinny_lds_kernel<8, W8, OUT, NORM, 2>), grid, block, 0, d->stream, a, sh.tpw);
+    else if (sh.nks == 8)
+        hipLaunchKernelGGL((skinny_lds_kernel<8, W8, OUT, NORM, 1>), grid, block, 0, d->stream, a, sh.tpw);
+    else
+        return fail(QASR_EINVAL, "skinny GEMM: %d k-steps per wave", sh.nks);
+    HIP_TRY(hipGetLastError(), "projection launch");
+    return QASR_OK;
+}
+
 template <int OUT, bool NORM = false>
 int launch_skinny(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
+    if (sh.nks)
+        return a.scale ? launch_skinny_lds<true, OUT, NORM>(d, sh, a)
+                       : launch_skinny_lds<false, OUT, NORM>(d, sh, a);
     return a.scale ? launch_skinny_w<true, OUT, NORM>(d, sh, a)
                    : launch_skinny_w<false, OUT, NORM>(d, sh, a);
 }
@@ -714,9 +917,9 @@ SkinnyArgs skinny_args(qasr_decoder* d, SkinnyShape sh, int rows, int n_out, int
 // rocBLAS, an int8 W first dequantised into the scratch matrix.
 int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f16* x, f16* y,
              bool accumulate, const float* scale = nullptr) {
-    const SkinnyShape sh = skinny_shape(d, rows, n_out, k);
+    const SkinnyShape sh = skinny_shape(d, rows, n_out, k, scale != nullptr);
     if (y == d->x) d->ss_valid = false;  // unless the launch below writes the chunk sums
-    if (sh.ks) {
+    if (sh.ks || sh.nks) {
         SkinnyArgs a = skinny_args(d, sh, rows, n_out, k, W, x, y, scale);
         if (accumulate && y == d->x && d->fuse && n_out <= kNormMaxK) {
             a.ss_out = d->ss;  // the residual rows' chunk sums, for the next fused norm
@@ -750,7 +953,7 @@ int launch_rms_norm(const f16* x, int64_t x_stride, const void* w, f16* out, int
 // its RMSNorm in the skinny kernel's prologue: a skinny shape, and chunk sums
 // of x written by the launch that wrote x.
 bool norm_fusable(qasr_decoder* d, SkinnyShape sh, int k, const f16* x) {
-    return d->fuse && sh.ks && k <= kNormMaxK && x == d->x && d->ss_valid;
+    return d->fuse && (sh.ks || sh.nks) && k <= kNormMaxK && x == d->x && d->ss_valid;
 }
 
 SkinnyArgs with_norm(qasr_decoder* d, SkinnyArgs a, const void* nw) {
@@ -768,9 +971,9 @@ int glu_skinny(qasr_decoder* d, int rows, int inter, int k, const void* W, const
                const float* scale, const void* nw, bool* fused) {
     *fused = false;
     if (!d->fuse) return QASR_OK;
-    const SkinnyShape sh = skinny_shape(d, rows, 2 * inter, k);
+    const SkinnyShape sh = skinny_shape(d, rows, 2 * inter, k, scale != nullptr);
     const int64_t span = (int64_t)(inter + 8) * k * (scale ? 1 : 2);
-    if (!sh.ks || span >= (int64_t(1) << 31)) return QASR_OK;
+    if (!(sh.ks || sh.nks) || span >= (int64_t(1) << 31)) return QASR_OK;
     if (nw && !norm_fusable(d, sh, k, x)) return QASR_OK;
     *fused = true;
     const SkinnyArgs a = skinny_args(d, sh, rows, 2 * inter, k, W, x, h, scale);
@@ -784,7 +987,7 @@ int glu_skinny(qasr_decoder* d, int rows, int inter, int k, const void* W, const
 int normed_proj(qasr_decoder* d, int rows, int n_out, const void* W, const f16* x, const void* nw,
                 f16* y, const float* scale) {
     const int hs = d->cfg.hidden_size;
-    const SkinnyShape sh = skinny_shape(d, rows, n_out, hs);
+    const SkinnyShape sh = skinny_shape(d, rows, n_out, hs, scale != nullptr);
     if (norm_fusable(d, sh, hs, x))
         return launch_skinny<kOutF16, true>(
             d, sh, with_norm(d, skinny_args(d, sh, rows, n_out, hs, W, x, y, scale), nw));
@@ -804,7 +1007,7 @@ int gemm_logits(qasr_decoder* d, int rows, const f16* nrows, float* out, const v
         return launch_skinny<kOutF32, true>(
             d, sh, with_norm(d, skinny_args(d, sh, rows, vocab, hs, d->embed, nrows, out), nw));
     }
-    if (sh.ks)
+    if (sh.ks || sh.nks)
         return launch_skinny<kOutF32>(
             d, sh, skinny_args(d, sh, rows, vocab, hs, d->embed, nrows, out));
     const float alpha = 1.0f, beta = 0.0f;
@@ -890,6 +1093,12 @@ int bind_stream(qasr_decoder* d, void* stream) {
     d->force_blas = e && *e == '1';
     const char* f = std::getenv("QASR_DECODER_FUSE");
     d->fuse = !(f && *f == '0');
+    const char* l = std::getenv("QASR_SKINNY_LDS");
+    d->lds_gemm = l ? std::atoi(l) : 1;
+    const char* tp = std::getenv("QASR_SKINNY_TPW");
+    d->lds_tpw = tp ? std::atoi(tp) : 0;
+    const char* gp = std::getenv("QASR_SKINNY_GROUPS");
+    d->lds_groups = gp ? std::atoi(gp) : 0;
     const rocblas_status st = rocblas_set_stream(d->blas, (hipStream_t)stream);
     if (st != rocblas_status_success) return fail(QASR_EDEVICE, "rocblas_set_stream: %s", blas_msg(st));
     return QASR_OK;

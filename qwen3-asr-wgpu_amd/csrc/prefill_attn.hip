@@ -103,17 +103,7 @@ __device__ __forceinline__ int swz16(int r) { return ((r & 3) << 2) | ((r >> 2) 
 // The copies are issued as inline asm (M0 = LDS destination): the compiler
 // then does not wait for them before unrelated LDS reads of the other
 // buffers; the kernel waits for them itself (vmcnt(0)) before each barrier.
-typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ u32x4v make_rsrc_words(const void* p, int bytes) {
-    const uint64_t a = (uint64_t)p;
-    return (u32x4v){(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)bytes, 0x00020000u};
-}
-__device__ __forceinline__ uint32_t lds_addr(const f16* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-__device__ __forceinline__ void dma16(u32x4v rsrc, int voff, uint32_t lds) {
-    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
-}
+// (make_rsrc_words, lds_addr and dma16 are in common.hpp.)
 // Rows past the last key of the row block (only in its last tile) are read
 // from row kend-1 instead: masked keys get p = 0, and 0 * (finite V) = 0,
 // whereas an out-of-range copy would leave whatever the LDS held before.

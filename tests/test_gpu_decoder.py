@@ -245,11 +245,13 @@ def test_native_decoder_step_graph_replays_equal_eager(O, gpu):
     dec.close()
 
 
-@pytest.mark.parametrize("model,batch", [("1.7B", 16), ("0.6B", 1), ("0.6B", 5)])
-def test_skinny_projections_match_rocblas(gpu, model, batch, monkeypatch):
+@pytest.mark.parametrize("model,batch,lds", [("1.7B", 16, "1"), ("0.6B", 1, "1"), ("0.6B", 5, "1"),
+                                             ("1.7B", 16, "2"), ("0.6B", 3, "2")])
+def test_skinny_projections_match_rocblas(gpu, model, batch, lds, monkeypatch):
     """The decode-step projections (at most 16 rows: this library's MFMA
-    skinny GEMM, split across workgroups for a long K) against rocBLAS for
-    the same steps (QASR_DECODER_BLAS=1):
+    skinny GEMMs, split across workgroups for a long K; with
+    QASR_SKINNY_LDS=2 the LDS-staged kernel takes every shape it fits, not
+    just the widest) against rocBLAS for the same steps (QASR_DECODER_BLAS=1):
     logits within rounding of each other, the same tokens wherever the top-2
     margin is clear."""
     import torch
@@ -264,6 +266,7 @@ def test_skinny_projections_match_rocblas(gpu, model, batch, monkeypatch):
         dec.prefill(_prompt(SEED_BASE + 960 + i, 30 + 7 * i, cfg["hs"]), 0, slot=i)
     slots, pos = list(range(batch)), [dec.pos[i] for i in range(batch)]
     tok = torch.tensor([dec.last[i] for i in range(batch)], dtype=torch.int32, device="cuda")
+    monkeypatch.setenv("QASR_SKINNY_LDS", lds)
     out = {}
     for name, blas in (("skinny", "0"), ("rocblas", "1")):
         monkeypatch.setenv("QASR_DECODER_BLAS", blas)
@@ -397,11 +400,12 @@ def test_int8_projections_equal_dequantized_f16(gpu, model, batch, blas, monkeyp
     assert np.array_equal(runs[0][1], runs[1][1])
 
 
-@pytest.mark.parametrize("model,batch,int8", [("1.7B", 16, False), ("0.6B", 1, False),
-                                              ("0.6B", 3, False), ("1.7B", 2, False),
-                                              ("1.7B", 16, True), ("0.6B", 5, True),
-                                              ("0.6B", 4, True)])
-def test_fused_epilogues_equal_unfused(gpu, model, batch, int8, monkeypatch):
+@pytest.mark.parametrize("model,batch,int8,lds", [("1.7B", 16, False, "1"), ("0.6B", 1, False, "1"),
+                                                  ("0.6B", 3, False, "1"), ("1.7B", 2, False, "1"),
+                                                  ("1.7B", 16, True, "1"), ("0.6B", 5, True, "1"),
+                                                  ("0.6B", 4, True, "1"), ("1.7B", 16, False, "2"),
+                                                  ("0.6B", 5, True, "2")])
+def test_fused_epilogues_equal_unfused(gpu, model, batch, int8, lds, monkeypatch):
     """The decode step's fusions -- the input, post-attention and final
     RMSNorms folded into the qkv, gate|up and logits projections, and gate|up
     with SiLU * up in one skinny launch -- against the same step with them off
@@ -425,6 +429,7 @@ def test_fused_epilogues_equal_unfused(gpu, model, batch, int8, monkeypatch):
         dec.prefill(_prompt(SEED_BASE + 1210 + i, 9 + 3 * i, cfg["hs"]), 0, slot=i)
     slots, pos = list(range(batch)), [dec.pos[i] for i in range(batch)]
     tok = torch.tensor([dec.last[i] for i in range(batch)], dtype=torch.int32, device="cuda")
+    monkeypatch.setenv("QASR_SKINNY_LDS", lds)
     out = {}
     for name, fuse in (("fused", "1"), ("unfused", "0")):
         monkeypatch.setenv("QASR_DECODER_FUSE", fuse)
