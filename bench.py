@@ -528,7 +528,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(no multi-GPU path is built; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(no multi-GPU path is built; decode would shard by slot with no exchange, one "
+              "process per GPU)", file=sys.stderr)
         sys.exit(2)
 
     import torch
