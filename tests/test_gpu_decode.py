@@ -136,6 +136,53 @@ def test_decode_merge_past_16_chunks(O, gpu, monkeypatch):
     test_decode_chunk_sizes_and_unfused_equal_fused(O, gpu, "32", "4096", "4", monkeypatch)
 
 
+def test_decode_partials_do_not_leak_between_launches(O, gpu, monkeypatch):
+    """Split-K partial slots are shared by every launch on a pool and handed
+    back unset by each launch's merger.  Steps that alternate planner settings
+    (so a slot serves a different entry, kv head and chunk each time, or no
+    split at all) each match the oracle, and a step repeated after them
+    reproduces its first output bitwise."""
+    import qasr_attn
+    from gpu_helpers import Gpu, dev, empty, host, say
+
+    from oracle import Rng
+
+    rng = Rng(SEED_BASE + 940)
+    lay = Layer(rng)
+    lengths = [1500, 700, 2047, 129, 3000, 900, 2, 1024]
+    n = len(lengths)
+    cap = cap_for(max(lengths) + 1)
+    g = Gpu(slots=n, cap=cap)
+    pos = [L - 1 for L in lengths]
+    refs = _setup(O, rng, lay, pos, cap, g)
+    qg, kg = g.gains(lay)
+
+    def step_rows(rows):
+        out = empty(n, QDIM)
+        qasr_attn.decode_step(g.ctx, g.kv, 0, pos, dev(rows), qg, kg, out)
+        return host(out)
+
+    rows0 = rng.normal_f16((n, TOT))
+    say("decode leak check: first step, default plan")
+    first = step_rows(rows0)
+    for i in range(n):
+        _, want = refs[i].step(rows0[i:i + 1], pos[i])
+        assert_parity(first[i:i + 1], want, f"first step entry {i}")
+    for min_chunk, wgs, split in [("32", "4096", "64"), ("100000", "512", "32"),
+                                  ("64", "97", "32"), ("128", "256", "5")]:
+        monkeypatch.setenv("QASR_DECODE_MIN_CHUNK", min_chunk)
+        monkeypatch.setenv("QASR_DECODE_WGS", wgs)
+        monkeypatch.setenv("QASR_DECODE_MAX_SPLIT", split)
+        say(f"decode leak check: plan {min_chunk}/{wgs}/{split}")
+        _decode_step_check(O, rng, lay, g, refs, pos)
+    for var in ("QASR_DECODE_MIN_CHUNK", "QASR_DECODE_WGS", "QASR_DECODE_MAX_SPLIT"):
+        monkeypatch.delenv(var)
+    say("decode leak check: repeated first step")
+    again = step_rows(rows0)
+    assert np.array_equal(again, first)
+    g.close()
+
+
 def test_decode_cap_length_and_permuted_slots(O, gpu):
     """cur_len == cap; slot order in the batch does not change any slot's output."""
     import qasr_attn
