@@ -287,6 +287,17 @@ int qasr_decoder_prefill_batch(qasr_decoder* dec, qasr_kv* kv, const qasr_segmen
 int qasr_dequant_i8(qasr_ctx* ctx, const void* q_dev, const float* scale_dev, int64_t rows,
                     int32_t cols, void* out_dev, void* stream);
 
+/* c[m][n] = f16(sum_k a[m][k] * b[n][k] (+ c[m][n] when accumulate)), f32
+ * accumulation and one rounding: the prefill projections' GEMM (the
+ * reference's tiled prefill GEMMs, shaders.rs:3033-3105 and 3105-3727,
+ * dispatched by decoder.rs:3580-4162; rounding as batch_dot_acc,
+ * cpu_decoder.rs:45-62).  a [m][k] (activation rows), b [n][k] (weight rows,
+ * checkpoint layout) and c [m][n] are f16 device pointers on ctx's device,
+ * 16-byte aligned; k a multiple of 64, n a multiple of 256, a and b each
+ * under 2 GB. */
+int qasr_gemm_f16(qasr_ctx* ctx, const void* a_dev, const void* b_dev, void* c_dev, int32_t m,
+                  int32_t n, int32_t k, int accumulate, void* stream);
+
 /* Diagnostic: the attention kernels' softmax weight for scores s_dev[i]
  * against row maxima m_dev[i] (f32, device, n each; m >= s), in both forms
  * the kernels use: out_scaled_dev[i] = 2^(f32(s*sl2) - f32(m*sl2)) (decode)

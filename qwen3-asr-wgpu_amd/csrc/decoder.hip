@@ -15,9 +15,12 @@
 // then logits = f32(rms_norm(x_last) * norm . E^T) against the tied embedding
 // and the first maximal index (458-485).
 //
-// The projections are plain GEMMs and go to rocBLAS (f16 operands, f32
+// The projections of a decode step run this file's skinny MFMA kernels; the
+// prefill projections are plain GEMMs and go to rocBLAS (f16 operands, f32
 // accumulation, one f16 rounding of the f32 result; a residual add is the
-// GEMM's beta = 1 term, so x + dot is rounded once as in batch_dot_acc).  The
+// GEMM's beta = 1 term, so x + dot is rounded once as in batch_dot_acc), or
+// with QASR_PREFILL_GEMM=own to gemm.hip's MFMA kernel (same rounding points;
+// it measured 1.4-2.5x slower than the library at these shapes).  The
 // elementwise steps are small HIP kernels below.  Nothing here allocates per
 // call: the activation workspace is sized for max_rows at creation, and
 // rocBLAS gets a fixed workspace so that a step can be captured in a graph.
@@ -27,6 +30,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <string>
 #include <vector>
 
 #include "abi_internal.hpp"
@@ -49,6 +53,9 @@ constexpr int kMaxPrefillSegs = 64;  // segments of one batched prefill call
 // Rows of one call (decode batch or prefill): bounds the activation
 // workspace (about 61 KB per row at the 1.7B shape, 1 GB at the limit).
 constexpr int kMaxDecoderRows = 16384;
+// With QASR_PREFILL_GEMM=own, projections of at least this many rows
+// (prefill) take gemm_f16_kernel (gemm.hip) instead of rocBLAS.
+constexpr int kOwnGemmMinRows = 128;
 
 // ---- block reductions (wave64 shuffles, then one LDS pass) ---------------
 __device__ __forceinline__ float wave_sum(float v) {
@@ -743,6 +750,7 @@ struct qasr_decoder {
     bool fuse = true;              // QASR_DECODER_FUSE=0: no fused epilogues (same results)
     int lds_gemm = 1;              // QASR_SKINNY_LDS: 0 older kernel only, 2 LDS kernel wherever it fits
     int lds_tpw = 0, lds_groups = 0;  // QASR_SKINNY_TPW / _GROUPS: shape overrides (0 = planner)
+    bool own_gemm = false;            // QASR_PREFILL_GEMM=own: gemm_f16_kernel for the prefill projections
     // activations, max_rows rows each
     f16* x = nullptr;     // residual stream [rows][hs]
     f16* n = nullptr;     // normed rows [rows][hs]
@@ -936,6 +944,12 @@ int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f
         HIP_TRY(hipGetLastError(), "dequantisation launch");
         W = d->wdq;
     }
+    if (d->own_gemm && rows >= kOwnGemmMinRows && qasr::gemm_f16_fits(rows, n_out, k)) {
+        HIP_TRY(qasr::launch_gemm_f16(x, (const f16*)W, y, rows, n_out, k, accumulate, d->ctx->cus,
+                                      d->stream),
+                "projection GEMM launch");
+        return QASR_OK;
+    }
     const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
     const rocblas_status st = rocblas_gemm_ex(
         d->blas, rocblas_operation_transpose, rocblas_operation_none, n_out, rows, k, &alpha, W,
@@ -1099,6 +1113,8 @@ int bind_stream(qasr_decoder* d, void* stream) {
     d->lds_tpw = tp ? std::atoi(tp) : 0;
     const char* gp = std::getenv("QASR_SKINNY_GROUPS");
     d->lds_groups = gp ? std::atoi(gp) : 0;
+    const char* pg = std::getenv("QASR_PREFILL_GEMM");
+    d->own_gemm = pg && std::string(pg) == "own";
     const rocblas_status st = rocblas_set_stream(d->blas, (hipStream_t)stream);
     if (st != rocblas_status_success) return fail(QASR_EDEVICE, "rocblas_set_stream: %s", blas_msg(st));
     return QASR_OK;
@@ -1331,6 +1347,25 @@ int qasr_decoder_prefill_batch(qasr_decoder* dec, qasr_kv* kv, const qasr_segmen
     if (nseg < 0 || (nseg > 0 && !segs)) return fail(QASR_EINVAL, "bad segment list");
     if (nseg == 0) return QASR_OK;
     return prefill_segments(dec, kv, segs, nseg, hidden_dev, next_dev, logits_dev, stream);
+}
+
+int qasr_gemm_f16(qasr_ctx* ctx, const void* a_dev, const void* b_dev, void* c_dev, int32_t m,
+                  int32_t n, int32_t k, int accumulate, void* stream) {
+    if (!ctx) return fail(QASR_EINVAL, "null context");
+    if (m < 0 || n < 0 || k < 0) return fail(QASR_EINVAL, "negative GEMM size %d x %d x %d", m, n, k);
+    if (m == 0 || n == 0) return QASR_OK;
+    if (!qasr::gemm_f16_fits(m, n, k))
+        return fail(QASR_EINVAL, "GEMM %d x %d x %d: k must be a positive multiple of 64, n of 256, "
+                    "and each operand under 2 GB", m, n, k);
+    if (!a_dev || !b_dev || !c_dev) return fail(QASR_EINVAL, "null device pointer");
+    if ((uintptr_t)a_dev % 16 || (uintptr_t)b_dev % 16 || (uintptr_t)c_dev % 16)
+        return fail(QASR_EINVAL, "a, b and c must be 16-byte aligned");
+    DeviceScope ds(ctx->device);
+    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
+    HIP_TRY(qasr::launch_gemm_f16((const f16*)a_dev, (const f16*)b_dev, (f16*)c_dev, m, n, k,
+                                  accumulate != 0, ctx->cus, (hipStream_t)stream),
+            "GEMM launch");
+    return QASR_OK;
 }
 
 int qasr_dequant_i8(qasr_ctx* ctx, const void* q_dev, const float* scale_dev, int64_t rows,

@@ -1,0 +1,215 @@
+// gemm.hip -- the prefill projections' GEMM on fp16 MFMA (gfx950):
+//   C[m][n] = f16(sum_k A[m][k] * B[n][k]  (+ C[m][n]))
+// A: activation rows [M][K], B: weight rows [N][K] (checkpoint layout), both
+// K-contiguous; f32 accumulation, one rounding of the f32 result (with the
+// residual added in f32 first when accumulating) -- the rounding points of
+// the reference's batched projections (cpu_decoder.rs:45-62 batch_dot_acc,
+// 398-449; dispatched on the GPU by decoder.rs:3580-4162).
+//
+// Block tile BM x BN (256 x 256, or 256 x 128 / 128 x 128 when the larger
+// grid would leave CUs idle), K steps of 64, four waves in a 2 x 2 grid, each
+// wave (BM/2) x (BN/2) as (BM/64) x (BN/64) tiles of v_mfma_f32_32x32x16_f16;
+// the next 16-k slice's LDS operand reads are interleaved with the current
+// slice's MFMAs.
+// Both operand tiles go global -> LDS by direct copies (buffer_load ... lds,
+// one 1 KB block per wave instruction), double buffered: the copies of K
+// step t+2 are issued as soon as every wave is done with step t's buffers,
+// so one step is in flight while another is consumed.  LDS row layout (both
+// operands): row r is 128 bytes (64 k), its 16-byte chunk c at slot
+// c ^ ((r >> 1) & 7), so an operand read (16 consecutive rows, one chunk)
+// covers 16 distinct 16-byte bank groups.  Rows past M are copied from row
+// M - 1 (finite values; their outputs are not stored).
+// Workgroups are dealt round-robin to the 8 XCDs: when the column blocks
+// divide by 8, XCD x takes a contiguous run of them and walks every row
+// block of one column block before the next, so a weight block is read
+// into that XCD's L2 once while the row blocks stream past it.
+
+#include "kernels.hpp"
+
+namespace qasr {
+
+namespace {
+
+constexpr int kBK = 64;          // k per step
+constexpr int kRowBytes = kBK * 2;  // 128 bytes of one row per step
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float16v mfma32(const half8v& a, const half8v& b, const float16v& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int slot_of(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
+template <int BM, int BN, bool ACC>
+__global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __restrict__ A,
+                                                               const f16* __restrict__ B,
+                                                               f16* __restrict__ C, int M, int N,
+                                                               int K) {
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int MT = WM / 32, NT = WN / 32;
+    constexpr int ACOPY = BM * kRowBytes / 1024 / 4;  // copy instructions per wave and step
+    constexpr int BCOPY = BN * kRowBytes / 1024 / 4;
+    __shared__ __attribute__((aligned(16))) f16 As[2][BM * kBK];
+    __shared__ __attribute__((aligned(16))) f16 Bs[2][BN * kBK];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int g = lane >> 5, l32 = lane & 31;
+
+    // Block coordinates (see the XCD note above).
+    const int nmt = (M + BM - 1) / BM, nnt = N / BN;
+    int mt, nt;
+    {
+        const int bid = blockIdx.x;
+        if (nnt % 8 == 0 && gridDim.x == (unsigned)(nmt * nnt)) {
+            const int x = bid & 7, j = bid >> 3, nper = nnt >> 3;
+            mt = j % nmt;
+            nt = x * nper + j / nmt;
+        } else {
+            mt = bid % nmt;
+            nt = bid / nmt;
+        }
+    }
+    const int m0 = mt * BM, n0 = nt * BN;
+
+    const u32x4v ares = make_rsrc_words(A, M * K * 2);
+    const u32x4v bres = make_rsrc_words(B, N * K * 2);
+    // This thread's copy sources: instruction j of wave w fills LDS bytes
+    // [(4j + w) KB, +1 KB): 16-byte unit p = 64 (4j + w) + lane, row p / 8,
+    // slot p % 8, holding chunk slot ^ ((row >> 1) & 7).
+    int aoff[ACOPY], boff[BCOPY];
+#pragma unroll
+    for (int j = 0; j < ACOPY; ++j) {
+        const int p = 64 * (4 * j + wave) + lane, row = p >> 3;
+        const int src = min(m0 + row, M - 1);
+        aoff[j] = src * K * 2 + slot_of(row, p & 7) * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < BCOPY; ++j) {
+        const int p = 64 * (4 * j + wave) + lane, row = p >> 3;
+        boff[j] = (n0 + row) * K * 2 + slot_of(row, p & 7) * 16;
+    }
+    auto copy_step = [&](int t, int buf) {
+        const int kb = t * kRowBytes;
+#pragma unroll
+        for (int j = 0; j < ACOPY; ++j) dma16(ares, aoff[j] + kb, lds_addr(&As[buf][(4 * j + wave) * 512]));
+#pragma unroll
+        for (int j = 0; j < BCOPY; ++j) dma16(bres, boff[j] + kb, lds_addr(&Bs[buf][(4 * j + wave) * 512]));
+    };
+
+    // Operand reads: A tile i (rows wm WM + 32 i + l32) and B tile i (rows
+    // wn WN + 32 i + l32), k-slice ks: chunk 2 ks + g.
+    int arow[MT], brow[NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) arow[i] = wm * WM + 32 * i + l32;
+#pragma unroll
+    for (int i = 0; i < NT; ++i) brow[i] = wn * WN + 32 * i + l32;
+
+    float16v acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = (float16v){};
+
+    const int nk = K / kBK;
+    constexpr int kStepCopies = ACOPY + BCOPY;
+    copy_step(0, 0);
+    if (nk > 1) copy_step(1, 1);
+    if (nk > 1)
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (kStepCopies & 15) | ((kStepCopies >> 4) << 14));
+    else
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+
+    // Operand registers of two k-slices: slice ks+1's reads are issued
+    // between slice ks's MFMAs (one read per MT*NT/8 MFMAs), so the LDS
+    // latency stays under the matrix core.
+    half8v a[2][MT], b[2][NT];
+    auto read_slice = [&](const f16* as, const f16* bs, int ks, int q) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+            a[q][i] = *(const half8v*)&as[arow[i] * kBK + slot_of(arow[i], 2 * ks + g) * 8];
+#pragma unroll
+        for (int i = 0; i < NT; ++i)
+            b[q][i] = *(const half8v*)&bs[brow[i] * kBK + slot_of(brow[i], 2 * ks + g) * 8];
+    };
+    constexpr int kSlices = kBK / 16;
+    constexpr int kReads = MT + NT, kMfmas = MT * NT;
+    for (int t = 0; t < nk; ++t) {
+        const int buf = t & 1;
+        const f16* as = As[buf];
+        const f16* bs = Bs[buf];
+        read_slice(as, bs, 0, 0);
+#pragma unroll
+        for (int ks = 0; ks < kSlices; ++ks) {
+            const int q = ks & 1;
+            if (ks + 1 < kSlices) read_slice(as, bs, ks + 1, q ^ 1);
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < NT; ++j) acc[i][j] = mfma32(a[q][i], b[q][j], acc[i][j]);
+            if (ks + 1 < kSlices) {
+                // kReads next-slice reads spread over kMfmas MFMAs.
+#pragma unroll
+                for (int r = 0; r < kReads; ++r) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, kMfmas / kReads, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                if constexpr (kMfmas % kReads != 0)
+                    __builtin_amdgcn_sched_group_barrier(0x008, kMfmas % kReads, 0);
+            }
+        }
+        // Step t+1's copies have landed (the only ones outstanding) and every
+        // wave is past step t's buffers: refill them with step t+2.
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+        if (t + 2 < nk) copy_step(t + 2, buf);
+    }
+
+    // acc[i][j][e]: row wm WM + 32 i + 8 (e / 4) + 4 g + e % 4, column
+    // wn WN + 32 j + l32 of the block.
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int m = m0 + wm * WM + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
+            if (m >= M) continue;
+            f16* crow = C + (int64_t)m * N + n0 + wn * WN + l32;
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const float v = acc[i][j][e];
+                crow[32 * j] = (f16)(ACC ? (float)crow[32 * j] + v : v);
+            }
+        }
+}
+
+template <int BM, int BN>
+hipError_t launch_shape(const f16* A, const f16* B, f16* C, int M, int N, int K, bool accumulate,
+                        hipStream_t stream) {
+    const dim3 grid((unsigned)(((M + BM - 1) / BM) * (N / BN)));
+    if (accumulate)
+        hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, true>), grid, dim3(kThreads), 0, stream, A, B, C, M, N, K);
+    else
+        hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, false>), grid, dim3(kThreads), 0, stream, A, B, C, M, N, K);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool gemm_f16_fits(int M, int N, int K) {
+    return M > 0 && N > 0 && K > 0 && K % kBK == 0 && N % 256 == 0 &&
+           (int64_t)M * K * 2 < (int64_t(1) << 31) && (int64_t)N * K * 2 < (int64_t(1) << 31);
+}
+
+hipError_t launch_gemm_f16(const f16* A, const f16* B, f16* C, int M, int N, int K, bool accumulate,
+                           int cus, hipStream_t stream) {
+    if (!gemm_f16_fits(M, N, K)) return hipErrorInvalidValue;
+    // 256 x 256 blocks when they give every CU a block, else 256 x 128, else
+    // 128 x 128.
+    const int64_t mb256 = (M + 255) / 256;
+    if (mb256 * (N / 256) >= cus) return launch_shape<256, 256>(A, B, C, M, N, K, accumulate, stream);
+    if (mb256 * (N / 128) >= cus || M > 128) return launch_shape<256, 128>(A, B, C, M, N, K, accumulate, stream);
+    return launch_shape<128, 128>(A, B, C, M, N, K, accumulate, stream);
+}
+
+}  // namespace qasr

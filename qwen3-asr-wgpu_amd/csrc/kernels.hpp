@@ -137,4 +137,11 @@ hipError_t launch_prefill_attn_segs(const PrefillArgs& a, const PrefillSegs& S, 
 hipError_t launch_prefill_attn(const PrefillArgs& a, const PrefillPlan& P, const PrefillWs& ws,
                                hipStream_t stream);
 
+// Prefill projections (gemm.hip): C[M][N] = f16(A[M][K] . B[N][K]^T (+ C)),
+// f32 accumulation, row-major, leading dimensions K, K and N, 16-byte
+// aligned.  gemm_f16_fits: K % 64 == 0, N % 256 == 0, both operands < 2 GB.
+bool gemm_f16_fits(int M, int N, int K);
+hipError_t launch_gemm_f16(const f16* A, const f16* B, f16* C, int M, int N, int K, bool accumulate,
+                           int cus, hipStream_t stream);
+
 }  // namespace qasr

@@ -37,7 +37,7 @@ ABI_SYMBOLS = (
     "qasr_decode_attn", "qasr_decode_step", "qasr_prefill_attn", "qasr_prefill_layer",
     "qasr_decoder_create", "qasr_decoder_destroy", "qasr_decoder_step", "qasr_decoder_prefill",
     "qasr_decoder_prefill_batch", "qasr_dequant_i8", "qasr_prefill_attn_batch",
-    "qasr_softmax_weights", "qasr_stream_read", "qasr_prefill_attn_noalloc",
+    "qasr_softmax_weights", "qasr_stream_read", "qasr_prefill_attn_noalloc", "qasr_gemm_f16",
 )
 MAX_PREFILL_SEGMENTS = 64  # segments per qasr_decoder_prefill_batch call
 
@@ -147,6 +147,8 @@ def load(path: str = LIB_PATH):
     L.qasr_decoder_prefill_batch.argtypes = [_vp, _vp, ctypes.POINTER(Segment), ctypes.c_int, _vp,
                                              _vp, _vp, _vp]
     L.qasr_dequant_i8.argtypes = [_vp, _vp, _vp, ctypes.c_int64, ctypes.c_int32, _vp, _vp]
+    L.qasr_gemm_f16.argtypes = [_vp, _vp, _vp, _vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                ctypes.c_int, _vp]
     L.qasr_softmax_weights.argtypes = [_vp, _vp, _vp, ctypes.c_int64, _vp, _vp, _vp]
     L.qasr_stream_read.argtypes = [_vp, _vp, ctypes.c_int64, ctypes.c_int, ctypes.c_int, _vp, _vp]
     _lib = L
@@ -491,6 +493,25 @@ def dequant_i8(ctx: Context, q, scale, out=None):
                                   _dev(scale, "scale", torch.float32), rows, cols,
                                   _dev(out, "out"), _stream(None)))
     return out
+
+
+def gemm_f16(ctx: Context, a, b, c=None, accumulate: bool = False):
+    """c = f16(a . b^T (+ c)) for f16 CUDA matrices a [m][k], b [n][k]: the
+    prefill projections' GEMM (f32 accumulation, one rounding).  Returns c."""
+    import torch
+
+    if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[1]:
+        raise QasrError(QASR_EINVAL, "a [m][k] and b [n][k] with the same k")
+    m, k = int(a.shape[0]), int(a.shape[1])
+    n = int(b.shape[0])
+    if c is None:
+        if accumulate:
+            raise QasrError(QASR_EINVAL, "accumulate needs c")
+        c = torch.empty((m, n), dtype=torch.float16, device=a.device)
+    _need(c, m * n, "c", exact=True)
+    _check(load().qasr_gemm_f16(ctx.handle, _dev(a, "a"), _dev(b, "b"), _dev(c, "c"), m, n, k,
+                                1 if accumulate else 0, _stream(None)))
+    return c
 
 
 def softmax_weights(ctx: Context, s, m):
