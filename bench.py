@@ -18,7 +18,7 @@ timed on a bounded sample of config 3 on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
                        [--only decode3|decode1|decode4|decode5|decode16x2k|prefill2|prefill4|
-                               config4_whole|streamread|copycal|decoder16|decoder1|
+                               config4_whole|streamread|mfma_ceiling|copycal|decoder16|decoder1|
                                decoder16_int8|decoder1_int8|serving|prefill_batch|prefill_one]
 """
 from __future__ import annotations
@@ -195,6 +195,72 @@ def copy_calibration(steps: int):
     ms = start.elapsed_time(end) / max(1, steps)
     return {"bytes_read": x.numel() * 2, "bytes_written": y.numel() * 2, "ms": ms,
             "GBps_rw": 2 * x.numel() * 2 / (ms * 1e-3) / 1e9}
+
+
+def mfma_calibration(wgs: int = 256, mfma_iters: int = 20000):
+    """Matrix-core calibration by qasr_mfma_probe, one workgroup per CU:
+    - the densest v_mfma_f32_32x32x16_f16 stream (four independent chains per
+      wave, one and two waves per SIMD), as TFLOP/s and as a fraction of the
+      2.5 PFLOP/s dense f16 peak, with the shader clock under that load
+      (s_memtime against the 100 MHz s_memrealtime);
+    - a softmax-shaped VALU block (the prefill kernel's per-score mix, and
+      each of its instructions alone) in one wave of each SIMD while the
+      other wave streams MFMAs, and what fraction of the shorter part the
+      overlap hid: 1 = fully hidden, 0 = serial.
+    The prefill kernel's MFMA fraction is read against these."""
+    import torch
+
+    import qasr_attn
+
+    ctx = qasr_attn.Context(NQH, NKVH, HD, LAYERS, 1e-6, 16384, 0)
+    sink = torch.empty(wgs * 8, dtype=torch.float32, device="cuda")
+    clk = torch.zeros(4, dtype=torch.int64, device="cuda")
+
+    def run(mode, waves, mi, vi, reps=5):
+        for _ in range(2):
+            qasr_attn.mfma_probe(ctx, mode, wgs, waves, mi, vi, sink, clk)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            qasr_attn.mfma_probe(ctx, mode, wgs, waves, mi, vi, sink, clk)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        c = [int(x) for x in clk.cpu().tolist()]
+        ghz = (c[2] - c[0]) / max(1, c[3] - c[1]) * 0.1  # shader cycles per 10 ns tick
+        return us, ghz
+
+    flop = lambda waves, mi: wgs * waves * mi * 4 * 32768.0
+    out = {"workgroups": wgs, "mfma_iters": mfma_iters}
+    for _ in range(20):  # the shader clock ramps up under the first launches
+        qasr_attn.mfma_probe(ctx, 0, wgs, 4, mfma_iters, 0, sink, clk)
+    torch.cuda.synchronize()
+    for waves in (4, 8):
+        us, ghz = run(0, waves, mfma_iters, 0)
+        tf = flop(waves, mfma_iters) / (us * 1e-6) / 1e12
+        out[f"mfma_only_{waves // 4}_wave_per_simd"] = {
+            "us": round(us, 1), "TFLOPs": round(tf, 1), "frac_of_peak": round(tf / MFMA_F16_PEAK_TFS, 4),
+            "shader_GHz": round(ghz, 3)}
+    t_m, _ = run(0, 4, mfma_iters, 0)
+    out["mfma_only_us"] = round(t_m, 1)
+    # VALU blocks (qasr_mfma_probe mode / 4): the prefill softmax's whole
+    # mix, and its instructions one kind at a time; iterations scaled so the
+    # VALU part alone takes about as long as the MFMA part.
+    kinds = {"softmax_mix": 0, "exp_only": 1, "fma_only": 2, "dot2_only": 3, "cvt_pk_only": 4,
+             "max3_only": 5, "softmax_mix_f32_sum": 6}
+    out["mfma_and_valu_in_different_waves_of_a_simd"] = {}
+    for name, kind in kinds.items():
+        t1, _ = run(1 + 4 * kind, 4, 0, 1000)
+        vi = max(100, int(1000 * t_m / t1))
+        t_v, _ = run(1 + 4 * kind, 4, 0, vi)
+        t_split, ghz_s = run(2 + 4 * kind, 8, mfma_iters, vi)
+        out["mfma_and_valu_in_different_waves_of_a_simd"][name] = {
+            "valu_iters": vi, "valu_only_us": round(t_v, 1), "together_us": round(t_split, 1),
+            "hidden_fraction": round((t_m + t_v - t_split) / min(t_m, t_v), 3),
+            "shader_GHz": round(ghz_s, 3)}
+    ctx.close()
+    return out
 
 
 def stream_read_calibration(nbytes: int, steps: int, warmup: int, copies: int = LAYERS,
@@ -553,6 +619,7 @@ def main():
             "prefill4": lambda: bench_prefill(512, 7680, K, W),
             "copycal": lambda: copy_calibration(K),
             "streamread": lambda: stream_read_calibration(decode_bytes([L + 1 for L in lens3]), K, W),
+            "mfma_ceiling": lambda: mfma_calibration(),
             "config4_whole": lambda: bench_config4_whole(max(3, K // 10), 1),
             "decoder16": lambda: bench_text_decoder("1.7B", lens3, K, W),
             "decoder1": lambda: bench_text_decoder("0.6B", [511], K, W),
@@ -587,6 +654,8 @@ def main():
         log("[bench] streaming-read calibration at config 3's bytes per launch")
         extra["streamread_config3_bytes"] = stream_read_calibration(
             decode_bytes([L + 1 for L in lens3]), K, W)
+        log("[bench] matrix-core calibration")
+        extra["mfma_calibration"] = mfma_calibration()
         log("[bench] text decoder steps (whole decoder around the attention path)")
         extra["text_decoder_1p7b_16slots"] = bench_text_decoder("1.7B", lens3, K, W)
         extra["text_decoder_0p6b_1slot"] = bench_text_decoder("0.6B", [511], K, W)

@@ -319,6 +319,22 @@ int qasr_softmax_weights(qasr_ctx* ctx, const float* s_dev, const float* m_dev, 
 int qasr_stream_read(qasr_ctx* ctx, const void* src_dev, int64_t bytes, int wgs, int waves,
                      uint32_t* sink_dev, void* stream);
 
+/* Calibration: `wgs` workgroups of `waves` waves (8 for mode 2) run
+ * mfma_iters iterations of four independent v_mfma_f32_32x32x16_f16 chains
+ * and/or valu_iters iterations of a softmax-shaped VALU block (16 values: row
+ * max, FMA + v_exp_f32 each, packed f16 conversion, v_dot2 sum).  mode % 4
+ * = 0: MFMA only; 1: VALU only; 2: waves 0-3 MFMA and waves 4-7 VALU (one of
+ * each per SIMD); 3: both interleaved in every wave.  mode / 4 picks the VALU
+ * block: 0 the whole mix; 1 exponentials only; 2 FMAs only; 3 v_dot2 only;
+ * 4 packed f16 conversions only; 5 v_max3 only; 6 the mix with f32 adds for
+ * the row sum; 7 the mix with single f16 conversions.  sink_dev receives one float
+ * per wave (wgs * waves), clk_dev four uint64: s_memtime and s_memrealtime
+ * (100 MHz) of wave 0 of workgroup 0 at its start and end.  Measures what the
+ * prefill kernel's MFMA roofline and its softmax/MFMA overlap are read
+ * against.  No counterpart in the reference. */
+int qasr_mfma_probe(qasr_ctx* ctx, int mode, int wgs, int waves, int mfma_iters, int valu_iters,
+                    float* sink_dev, unsigned long long* clk_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

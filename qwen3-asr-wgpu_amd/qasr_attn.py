@@ -38,6 +38,7 @@ ABI_SYMBOLS = (
     "qasr_decoder_create", "qasr_decoder_destroy", "qasr_decoder_step", "qasr_decoder_prefill",
     "qasr_decoder_prefill_batch", "qasr_dequant_i8", "qasr_prefill_attn_batch",
     "qasr_softmax_weights", "qasr_stream_read", "qasr_prefill_attn_noalloc", "qasr_gemm_f16",
+    "qasr_mfma_probe",
 )
 MAX_PREFILL_SEGMENTS = 64  # segments per qasr_decoder_prefill_batch call
 
@@ -151,6 +152,8 @@ def load(path: str = LIB_PATH):
                                 ctypes.c_int, _vp]
     L.qasr_softmax_weights.argtypes = [_vp, _vp, _vp, ctypes.c_int64, _vp, _vp, _vp]
     L.qasr_stream_read.argtypes = [_vp, _vp, ctypes.c_int64, ctypes.c_int, ctypes.c_int, _vp, _vp]
+    L.qasr_mfma_probe.argtypes = [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_int, _vp, _vp, _vp]
     _lib = L
     return L
 
@@ -541,6 +544,19 @@ def stream_read(ctx: Context, src, wgs: int, waves: int, sink, stream=None):
     _need(sink, wgs * waves, "sink")
     _check(load().qasr_stream_read(ctx.handle, src.data_ptr(), src.numel() * src.element_size(),
                                    wgs, waves, _dev(sink, "sink", torch.int32), _stream(stream)))
+
+
+def mfma_probe(ctx: Context, mode: int, wgs: int, waves: int, mfma_iters: int, valu_iters: int,
+               sink, clk, stream=None):
+    """Matrix-core calibration (see qasr_mfma_probe); sink: f32 CUDA tensor of
+    >= wgs * waves entries (8 waves for mode 2), clk: int64 CUDA tensor of 4."""
+    import torch
+
+    _need(sink, wgs * (8 if mode == 2 else waves), "sink")
+    _need(clk, 4, "clk")
+    _check(load().qasr_mfma_probe(ctx.handle, mode, wgs, waves, mfma_iters, valu_iters,
+                                  _dev(sink, "sink", torch.float32), _dev(clk, "clk", torch.int64),
+                                  _stream(stream)))
 
 
 LAYER_WEIGHT_NAMES = ("input_layernorm", "q_proj", "k_proj", "v_proj", "q_norm", "k_norm",
