@@ -8,9 +8,11 @@
 //
 // Block tile BM x BN (256 x 256, or 256 x 128 / 128 x 128 when the larger
 // grid would leave CUs idle), K steps of 64, four waves in a 2 x 2 grid, each
-// wave (BM/2) x (BN/2) as (BM/64) x (BN/64) tiles of v_mfma_f32_32x32x16_f16;
-// the next 16-k slice's LDS operand reads are interleaved with the current
-// slice's MFMAs.
+// wave (BM/2) x (BN/2) as (BM/64) x (BN/64) tiles of v_mfma_f32_32x32x16_f16.
+// Per K step the wave runs four 16-k slices; the next slice's operand reads
+// are issued as one group ahead of the current slice's MFMAs, and the next
+// step's first reads ahead of the last slice's, so no LDS latency is waited
+// for between MFMAs.
 // Both operand tiles go global -> LDS by direct copies (buffer_load ... lds,
 // one 1 KB block per wave instruction), double buffered: the copies of K
 // step t+2 are issued as soon as every wave is done with step t's buffers,
@@ -20,9 +22,11 @@
 // covers 16 distinct 16-byte bank groups.  Rows past M are copied from row
 // M - 1 (finite values; their outputs are not stored).
 // Workgroups are dealt round-robin to the 8 XCDs: when the column blocks
-// divide by 8, XCD x takes a contiguous run of them and walks every row
-// block of one column block before the next, so a weight block is read
-// into that XCD's L2 once while the row blocks stream past it.
+// divide by 8, XCD x takes a contiguous run of them and walks them in groups
+// of a few row blocks, so the tiles an XCD runs at one time share a few A
+// and B blocks in its L2.
+// Results are rounded and stored in place; with the residual they go
+// through LDS first, so C is read and written in 8-byte row pieces.
 
 #include "kernels.hpp"
 
@@ -33,6 +37,7 @@ namespace {
 constexpr int kBK = 64;          // k per step
 constexpr int kRowBytes = kBK * 2;  // 128 bytes of one row per step
 constexpr int kThreads = 256;
+constexpr int kGroupRows = 4;  // row blocks per group of an XCD's tile walk
 
 __device__ __forceinline__ float16v mfma32(const half8v& a, const half8v& b, const float16v& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -49,8 +54,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
     constexpr int MT = WM / 32, NT = WN / 32;
     constexpr int ACOPY = BM * kRowBytes / 1024 / 4;  // copy instructions per wave and step
     constexpr int BCOPY = BN * kRowBytes / 1024 / 4;
-    __shared__ __attribute__((aligned(16))) f16 As[2][BM * kBK];
-    __shared__ __attribute__((aligned(16))) f16 Bs[2][BN * kBK];
+    // Both operand buffers in one array: the epilogue reuses all of it.
+    __shared__ __attribute__((aligned(16))) f16 smem[2 * (BM + BN) * kBK];
+    f16(*As)[BM * kBK] = reinterpret_cast<f16(*)[BM * kBK]>(smem);
+    f16(*Bs)[BN * kBK] = reinterpret_cast<f16(*)[BN * kBK]>(smem + 2 * BM * kBK);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -62,9 +69,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
     {
         const int bid = blockIdx.x;
         if (nnt % 8 == 0 && gridDim.x == (unsigned)(nmt * nnt)) {
+            // XCD x (workgroups x, x + 8, ..) takes column blocks
+            // [x nper, (x+1) nper) and walks them in groups of kGroupRows row
+            // blocks: group after group, each column block of the group's
+            // rows in turn, so the XCD's concurrent tiles share a few A and
+            // B blocks in its L2.
             const int x = bid & 7, j = bid >> 3, nper = nnt >> 3;
-            mt = j % nmt;
-            nt = x * nper + j / nmt;
+            const int grp = j / (kGroupRows * nper);
+            const int gr = min(kGroupRows, nmt - grp * kGroupRows);
+            const int r = j - grp * kGroupRows * nper;
+            mt = grp * kGroupRows + r % gr;
+            nt = x * nper + r / gr;
         } else {
             mt = bid % nmt;
             nt = bid / nmt;
@@ -121,9 +136,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
 
-    // Operand registers of two k-slices: slice ks+1's reads are issued
-    // between slice ks's MFMAs (one read per MT*NT/8 MFMAs), so the LDS
-    // latency stays under the matrix core.
+    // Operand registers of two k-slices: slice ks+1's reads are issued as
+    // one group ahead of slice ks's MFMAs, so their LDS latency runs under
+    // those MFMAs; sched_barrier keeps the compiler from moving a read next
+    // to its first use.
     half8v a[2][MT], b[2][NT];
     auto read_slice = [&](const f16* as, const f16* bs, int ks, int q) {
 #pragma unroll
@@ -133,54 +149,105 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
         for (int i = 0; i < NT; ++i)
             b[q][i] = *(const half8v*)&bs[brow[i] * kBK + slot_of(brow[i], 2 * ks + g) * 8];
     };
+    auto mfma_slice = [&](int q) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < NT; ++j) acc[i][j] = mfma32(a[q][i], b[q][j], acc[i][j]);
+    };
     constexpr int kSlices = kBK / 16;
-    constexpr int kReads = MT + NT, kMfmas = MT * NT;
-    for (int t = 0; t < nk; ++t) {
+    static_assert(kSlices == 4, "slices 0..2 then the step boundary under slice 3");
+    // K step t from buffer t & 1.  All but the last step end with the step
+    // boundary (straight-line code, so the compiler's waits track exactly
+    // which reads are outstanding).
+    auto k_step = [&](int t, bool last) {
         const int buf = t & 1;
         const f16* as = As[buf];
         const f16* bs = Bs[buf];
-        read_slice(as, bs, 0, 0);
+        // Slice 0's reads were issued under the previous step's last MFMAs:
+        // done by now.  Waiting here explicitly keeps the compiler from
+        // waiting for the reads issued next, which it would otherwise
+        // assume pending across the loop edge.
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
 #pragma unroll
-        for (int ks = 0; ks < kSlices; ++ks) {
-            const int q = ks & 1;
-            if (ks + 1 < kSlices) read_slice(as, bs, ks + 1, q ^ 1);
-#pragma unroll
-            for (int i = 0; i < MT; ++i)
-#pragma unroll
-                for (int j = 0; j < NT; ++j) acc[i][j] = mfma32(a[q][i], b[q][j], acc[i][j]);
-            if (ks + 1 < kSlices) {
-                // kReads next-slice reads spread over kMfmas MFMAs.
-#pragma unroll
-                for (int r = 0; r < kReads; ++r) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, kMfmas / kReads, 0);
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                }
-                if constexpr (kMfmas % kReads != 0)
-                    __builtin_amdgcn_sched_group_barrier(0x008, kMfmas % kReads, 0);
-            }
+        for (int ks = 0; ks + 1 < kSlices; ++ks) {
+            read_slice(as, bs, ks + 1, (ks + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_slice(ks & 1);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // Step t+1's copies have landed (the only ones outstanding) and every
-        // wave is past step t's buffers: refill them with step t+2.
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-        __syncthreads();
-        if (t + 2 < nk) copy_step(t + 2, buf);
-    }
+        // Slice 3's operands are in registers.  Once every wave has them
+        // (all of its LDS reads of this buffer returned) and step t+1's
+        // copies have landed, refill this buffer with step t+2 and read
+        // step t+1's slice 0, both under slice 3's MFMAs.
+        if (!last) {
+            __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+            __syncthreads();
+            if (t + 2 < nk) copy_step(t + 2, buf);
+            read_slice(As[buf ^ 1], Bs[buf ^ 1], 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_slice(1);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    read_slice(As[0], Bs[0], 0, 0);
+    for (int t = 0; t + 1 < nk; ++t) k_step(t, false);
+    k_step(nk - 1, true);
 
     // acc[i][j][e]: row wm WM + 32 i + 8 (e / 4) + 4 g + e % 4, column
     // wn WN + 32 j + l32 of the block.
+    if constexpr (!ACC) {
+        // Plain result: each value rounded and stored where it sits (the
+        // stores need no wait, and measured faster than staging them).
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+        for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int m = m0 + wm * WM + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
-            if (m >= M) continue;
-            f16* crow = C + (int64_t)m * N + n0 + wn * WN + l32;
+            for (int e = 0; e < 16; ++e) {
+                const int m = m0 + wm * WM + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
+                if (m >= M) continue;
+                f16* crow = C + (int64_t)m * N + n0 + wn * WN + l32;
 #pragma unroll
-            for (int j = 0; j < NT; ++j) {
-                const float v = acc[i][j][e];
-                crow[32 * j] = (f16)(ACC ? (float)crow[32 * j] + v : v);
+                for (int j = 0; j < NT; ++j) crow[32 * j] = (f16)acc[i][j][e];
             }
+        return;
+    }
+    // With the residual: row tile i of the wave (32 rows x WN columns) goes
+    // through this wave's LDS region as f32 (rows padded so the two lane
+    // halves' writes fall on different banks), then out as row-contiguous
+    // 4-column pieces: one 8-byte load of C and one 8-byte store per piece,
+    // instead of a dependent 2-byte load per value.
+    __syncthreads();  // every wave is past its last operand reads
+    constexpr int EP = WN + 8;      // padded row, floats
+    constexpr int CPR = WN / 4;     // 4-column pieces per row
+    constexpr int RPP = 64 / CPR;   // rows per pass of the wave
+    static_assert(4 * 32 * EP * 4 <= 2 * (BM + BN) * kBK * 2, "epilogue staging fits the operand buffers");
+    float* ep = reinterpret_cast<float*>(smem) + wave * (32 * EP);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) ep[(8 * (e >> 2) + 4 * g + (e & 3)) * EP + 32 * j + l32] = acc[i][j][e];
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int it = 0; it < 32 / RPP; ++it) {
+            const int rr = it * RPP + lane / CPR, cc = (lane % CPR) * 4;
+            const float4 v = *(const float4*)&ep[rr * EP + cc];
+            const int m = m0 + wm * WM + 32 * i + rr;
+            if (m >= M) continue;
+            half4v* cp = reinterpret_cast<half4v*>(C + (int64_t)m * N + n0 + wn * WN + cc);
+            const half4v old = *cp;
+            half4v o;
+            o[0] = (f16)((float)old[0] + v.x);
+            o[1] = (f16)((float)old[1] + v.y);
+            o[2] = (f16)((float)old[2] + v.z);
+            o[3] = (f16)((float)old[3] + v.w);
+            *cp = o;
         }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): reads done before the next tile's writes
+        __builtin_amdgcn_wave_barrier();
+    }
 }
 
 template <int BM, int BN>
