@@ -19,7 +19,8 @@ timed on a bounded sample of config 3 on this host.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
                        [--only decode3|decode1|decode4|decode5|decode16x2k|prefill2|prefill4|
                                config4_whole|streamread|mfma_ceiling|copycal|decoder16|decoder1|
-                               decoder16_int8|decoder1_int8|serving|prefill_batch|prefill_one]
+                               decoder16_int8|decoder1_int8|serving|prefill_batch|prefill_one|
+                               gemm]
 """
 from __future__ import annotations
 
@@ -503,6 +504,53 @@ def bench_prefill_one(model: str, rows: int, steps: int, warmup: int, seed: int 
     return {"model": model, "rows": rows, "ms": dt * 1e3, "rows_per_s": rows / dt}
 
 
+GEMM_SHAPES = [(4269, 4096, 2048, False), (4269, 2048, 2048, True), (4269, 12288, 2048, False),
+               (4269, 2048, 6144, True), (420, 2048, 6144, True), (16384, 12288, 2048, False)]
+
+
+def bench_gemm(steps: int, warmup: int, seed: int = 31):
+    """The build's prefill GEMM (qasr_gemm_f16) against the vendor BLAS
+    (torch.mm / addmm) at the 1.7B projections' shapes: the batched prefill's
+    4,269 rows, one prompt's down_proj, and a large square-ish product.  Event
+    timing on the current stream, operands resident."""
+    import torch
+
+    import qasr_attn
+
+    ctx = qasr_attn.Context()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    out = []
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    for m, n, k, acc in GEMM_SHAPES:
+        a = torch.randn((m, k), device="cuda", generator=g).half()
+        b = (torch.randn((n, k), device="cuda", generator=g) * 0.05).half()
+        c = torch.zeros((m, n), device="cuda", dtype=torch.float16)
+        bt = b.t()
+        t_own = timed(lambda: qasr_attn.gemm_f16(ctx, a, b, c, accumulate=acc))
+        t_lib = timed(lambda: c.addmm_(a, bt) if acc else torch.mm(a, bt, out=c))
+        fl = 2.0 * m * n * k
+        out.append({"m": m, "n": n, "k": k, "residual": acc, "own_us": round(t_own, 1),
+                    "library_us": round(t_lib, 1), "own_TFLOPs": round(fl / t_own / 1e6, 1),
+                    "library_TFLOPs": round(fl / t_lib / 1e6, 1)})
+        del a, b, c, bt
+    ctx.close()
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_prefill_batch(model: str, segments: int, steps: int, warmup: int, seed: int = 23):
     """qasr_decoder_prefill_batch over `segments` prompts of U[150, 450] rows
     (projections once over all rows, attention per segment), 28 layers:
@@ -628,6 +676,7 @@ def main():
             "serving": lambda: bench_serving("1.7B", 32, 16, 48),
             "prefill_batch": lambda: bench_prefill_batch("1.7B", 16, max(3, K // 10), 1),
             "prefill_one": lambda: bench_prefill_one("1.7B", 420, max(5, K // 5), 2),
+            "gemm": lambda: bench_gemm(max(5, K // 5), 3),
         }
         log(json.dumps({only: runs[only]()}))
         return
