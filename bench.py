@@ -208,6 +208,8 @@ def mfma_calibration(wgs: int = 256, mfma_iters: int = 20000):
       each of its instructions alone) in one wave of each SIMD while the
       other wave streams MFMAs, and what fraction of the shorter part the
       overlap hid: 1 = fully hidden, 0 = serial.
+    - the same blocks interleaved inside every wave (one and two waves per
+      SIMD), the schedule of a kernel overlapping its own softmax and MFMAs.
     The prefill kernel's MFMA fraction is read against these."""
     import torch
 
@@ -260,6 +262,23 @@ def mfma_calibration(wgs: int = 256, mfma_iters: int = 20000):
             "valu_iters": vi, "valu_only_us": round(t_v, 1), "together_us": round(t_split, 1),
             "hidden_fraction": round((t_m + t_v - t_split) / min(t_m, t_v), 3),
             "shader_GHz": round(ghz_s, 3)}
+    # The same blocks interleaved inside every wave (probe mode 3): the
+    # schedule of a kernel that overlaps its own softmax with its own MFMAs,
+    # at one and at two waves per SIMD.
+    out["mfma_and_valu_in_the_same_wave"] = {}
+    for waves in (4, 8):
+        t_mw, _ = run(0, waves, mfma_iters, 0)
+        for name in ("softmax_mix", "softmax_mix_f32_sum"):
+            kind = kinds[name]
+            t1, _ = run(1 + 4 * kind, waves, 0, 1000)
+            vi = max(100, int(1000 * t_mw / t1))
+            t_v, _ = run(1 + 4 * kind, waves, 0, vi)
+            t_both, ghz_b = run(3 + 4 * kind, waves, mfma_iters, vi)
+            out["mfma_and_valu_in_the_same_wave"][f"{name}_{waves // 4}_wave_per_simd"] = {
+                "valu_iters": vi, "mfma_only_us": round(t_mw, 1), "valu_only_us": round(t_v, 1),
+                "together_us": round(t_both, 1),
+                "hidden_fraction": round((t_mw + t_v - t_both) / min(t_mw, t_v), 3),
+                "shader_GHz": round(ghz_b, 3)}
     ctx.close()
     return out
 
