@@ -335,6 +335,29 @@ int qasr_stream_read(qasr_ctx* ctx, const void* src_dev, int64_t bytes, int wgs,
 int qasr_mfma_probe(qasr_ctx* ctx, int mode, int wgs, int waves, int mfma_iters, int valu_iters,
                     float* sink_dev, unsigned long long* clk_dev, void* stream);
 
+/* Launch planning on the host, for tests (no device, no context): the
+ * split plans the decode and prefill entry points launch with.  No
+ * counterpart in the reference (its chunk choice is decoder.rs:899-916,
+ * 1932-1957; its prefill dispatch has no key split).
+ *
+ * Decode (qasr_decode_attn / qasr_decode_step): `batch` (1..64) entries
+ * attending lens[b] >= 1 keys, `nkvh` kv heads, a device of `cus` compute
+ * units; the QASR_DECODE_WGS / _MIN_CHUNK / _MAX_SPLIT environment knobs
+ * apply.  chunk_out[b]: keys per workgroup of entry b (a multiple of 32);
+ * wg_base_out[0..batch]: entry b's workgroups are wg_base_out[b] ..
+ * wg_base_out[b+1]-1 (nkvh * ceil(lens[b] / chunk_out[b]) of them). */
+int qasr_plan_decode(int batch, const int32_t* lens, int nkvh, int cus, int32_t* chunk_out,
+                     int32_t* wg_base_out);
+
+/* Prefill (qasr_prefill_attn, one launch of 1..4096 rows at kv_start):
+ * *rows_per_block (64, or 32 for unsplit short key ranges), *nrb row
+ * blocks, *tiles_per_split 128-key tiles per split (QASR_PREFILL_TPS
+ * applies), sp_base_out[0..nrb]: row block rb's items are sp_base_out[rb] ..
+ * sp_base_out[rb+1]-1 within each kv head (sp_base_out[nrb] items per kv
+ * head; at most 65 entries written). */
+int qasr_plan_prefill(int rows, int kv_start, int nkvh, int32_t* rows_per_block, int32_t* nrb,
+                      int32_t* tiles_per_split, int32_t* sp_base_out);
+
 #ifdef __cplusplus
 }
 #endif

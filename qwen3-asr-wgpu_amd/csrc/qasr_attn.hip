@@ -283,6 +283,32 @@ int noalloc_max_rows(int nkvh) {
     return qasr::kPrefillRows * (int)std::min<int64_t>(qasr::kMaxRowBlocks, kScratchItems / nkvh);
 }
 
+// The plan of one prefill launch of `rows` (<= kMaxRowBlocks * kPrefillRows)
+// rows at kv_start `ks`.  Tiles per split: about one workgroup per CU (256),
+// without splitting row blocks whose key range is short.  A split's merge
+// (publish, ticket, read back) is about three memory round trips, as long as
+// several latency-bound tiles: key ranges of up to kPrefillNoSplitTiles tiles
+// are never split.  Unsplit short ranges also take 32-row blocks: twice the
+// workgroups, half the work on the longest one.  A forced split count
+// (tps_forced > 0, QASR_PREFILL_TPS) keeps 64-row blocks.
+qasr::PrefillPlan choose_prefill_plan(int rows, int ks, int nkvh, int tps_forced) {
+    const int nrb = (rows + qasr::kPrefillRows - 1) / qasr::kPrefillRows;
+    const int max_tiles = (ks + rows + qasr::kPrefillTileKeys - 1) / qasr::kPrefillTileKeys;
+    int tps = tps_forced;
+    int rb_rows = qasr::kPrefillRows;
+    if (tps <= 0) {
+        const int64_t tiles_all = (int64_t)nrb * max_tiles;
+        const int64_t want = std::max<int64_t>(1, 256 / nkvh);
+        if (max_tiles <= kPrefillNoSplitTiles) {
+            tps = max_tiles;
+            rb_rows = qasr::kPrefillRows / 2;
+        } else {
+            tps = (int)std::max<int64_t>(2, (tiles_all + want - 1) / want);
+        }
+    }
+    return qasr::plan_prefill(rows, ks, nkvh, tps, rb_rows);
+}
+
 int run_prefill(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, int s,
                 const void* q_dev, void* out_dev, void* stream, bool noalloc) {
     int rc = check_common(ctx, kv, layer);
@@ -333,29 +359,10 @@ int run_prefill(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, i
     for (int r0 = 0; r0 < s; r0 += rows_per_launch) {
         const int rows = std::min(rows_per_launch, s - r0);
         const int ks = kv_start + r0;
-        const int nrb = (rows + qasr::kPrefillRows - 1) / qasr::kPrefillRows;
         const int max_tiles = (ks + rows + qasr::kPrefillTileKeys - 1) / qasr::kPrefillTileKeys;
-        // Tiles per split: about one workgroup per CU (256), without
-        // splitting row blocks whose key range is short.  A split's merge
-        // (publish, ticket, read back) is about three memory round trips, as
-        // long as several latency-bound tiles: key ranges of up to
-        // kPrefillNoSplitTiles tiles are never split.
-        // Unsplit short ranges also take 32-row blocks: twice the workgroups,
-        // half the work on the longest one (a forced split count keeps
-        // 64-row blocks).
-        int tps = tps_forced;
-        int rb_rows = qasr::kPrefillRows;
-        if (tps <= 0) {
-            const int64_t tiles_all = (int64_t)nrb * max_tiles;
-            const int64_t want = std::max<int64_t>(1, 256 / nkvh);
-            if (max_tiles <= kPrefillNoSplitTiles) {
-                tps = max_tiles;
-                rb_rows = qasr::kPrefillRows / 2;
-            } else {
-                tps = (int)std::max<int64_t>(2, (tiles_all + want - 1) / want);
-            }
-        }
-        qasr::PrefillPlan P = qasr::plan_prefill(rows, ks, nkvh, tps, rb_rows);
+        qasr::PrefillPlan P = choose_prefill_plan(rows, ks, nkvh, tps_forced);
+        int tps = P.tps;
+        const int rb_rows = P.rows_per_block;
         if (noalloc) {
             // Coarser splits until the partials fit the scratch array; at
             // tps = max_tiles every row block is one item (s is bounded so
@@ -830,6 +837,38 @@ int qasr_prefill_attn_batch(qasr_ctx* ctx, qasr_kv* kv, int layer, const qasr_se
     a.scale_log2 = ctx->scale_log2;
     const hipError_t e = qasr::launch_prefill_attn_segs(a, S, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "prefill attention launch");
+    return QASR_OK;
+}
+
+int qasr_plan_decode(int batch, const int32_t* lens, int nkvh, int cus, int32_t* chunk_out,
+                     int32_t* wg_base_out) {
+    if (batch < 1 || batch > qasr::kMaxBatch)
+        return fail(QASR_EINVAL, "batch %d outside [1, %d]", batch, qasr::kMaxBatch);
+    if (nkvh < 1 || nkvh > 64 || cus < 1) return fail(QASR_EINVAL, "nkvh %d / cus %d", nkvh, cus);
+    if (!lens || !chunk_out || !wg_base_out) return fail(QASR_EINVAL, "null pointer");
+    qasr::DecodePlan P{};
+    P.batch = batch;
+    for (int b = 0; b < batch; ++b) {
+        if (lens[b] < 1) return fail(QASR_EINVAL, "entry %d attends %d keys", b, lens[b]);
+        P.len[b] = lens[b];
+    }
+    plan_decode_chunks(P, nkvh, cus);
+    for (int b = 0; b < batch; ++b) chunk_out[b] = P.chunk[b];
+    for (int b = 0; b <= batch; ++b) wg_base_out[b] = P.wg_base[b];
+    return QASR_OK;
+}
+
+int qasr_plan_prefill(int rows, int kv_start, int nkvh, int32_t* rows_per_block, int32_t* nrb,
+                      int32_t* tiles_per_split, int32_t* sp_base_out) {
+    if (rows < 1 || rows > qasr::kMaxRowBlocks * qasr::kPrefillRows)
+        return fail(QASR_EINVAL, "rows %d outside [1, %d]", rows, qasr::kMaxRowBlocks * qasr::kPrefillRows);
+    if (kv_start < 0 || nkvh < 1 || nkvh > 64) return fail(QASR_EINVAL, "kv_start %d / nkvh %d", kv_start, nkvh);
+    if (!rows_per_block || !nrb || !tiles_per_split || !sp_base_out) return fail(QASR_EINVAL, "null pointer");
+    const qasr::PrefillPlan P = choose_prefill_plan(rows, kv_start, nkvh, env_int("QASR_PREFILL_TPS", 0));
+    *rows_per_block = P.rows_per_block;
+    *nrb = P.nrb;
+    *tiles_per_split = P.tps;
+    for (int i = 0; i <= P.nrb; ++i) sp_base_out[i] = P.sp_base[i];
     return QASR_OK;
 }
 

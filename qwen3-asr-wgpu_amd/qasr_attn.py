@@ -38,7 +38,7 @@ ABI_SYMBOLS = (
     "qasr_decoder_create", "qasr_decoder_destroy", "qasr_decoder_step", "qasr_decoder_prefill",
     "qasr_decoder_prefill_batch", "qasr_dequant_i8", "qasr_prefill_attn_batch",
     "qasr_softmax_weights", "qasr_stream_read", "qasr_prefill_attn_noalloc", "qasr_gemm_f16",
-    "qasr_mfma_probe",
+    "qasr_mfma_probe", "qasr_plan_decode", "qasr_plan_prefill",
 )
 MAX_PREFILL_SEGMENTS = 64  # segments per qasr_decoder_prefill_batch call
 
@@ -154,6 +154,9 @@ def load(path: str = LIB_PATH):
     L.qasr_stream_read.argtypes = [_vp, _vp, ctypes.c_int64, ctypes.c_int, ctypes.c_int, _vp, _vp]
     L.qasr_mfma_probe.argtypes = [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                   ctypes.c_int, _vp, _vp, _vp]
+    i32p = ctypes.POINTER(ctypes.c_int32)
+    L.qasr_plan_decode.argtypes = [ctypes.c_int, i32p, ctypes.c_int, ctypes.c_int, i32p, i32p]
+    L.qasr_plan_prefill.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, i32p, i32p, i32p, i32p]
     _lib = L
     return L
 
@@ -552,11 +555,34 @@ def mfma_probe(ctx: Context, mode: int, wgs: int, waves: int, mfma_iters: int, v
     >= wgs * waves entries (8 waves for mode 2), clk: int64 CUDA tensor of 4."""
     import torch
 
-    _need(sink, wgs * (8 if mode == 2 else waves), "sink")
+    _need(sink, wgs * (8 if mode % 4 == 2 else waves), "sink")
     _need(clk, 4, "clk")
     _check(load().qasr_mfma_probe(ctx.handle, mode, wgs, waves, mfma_iters, valu_iters,
                                   _dev(sink, "sink", torch.float32), _dev(clk, "clk", torch.int64),
                                   _stream(stream)))
+
+
+def plan_decode(lens, nkvh: int = 8, cus: int = 256):
+    """The decode split plan the library launches for entries attending
+    lens[b] keys (qasr_plan_decode; host only, no device): (chunk keys per
+    workgroup of each entry, workgroup bases [batch + 1])."""
+    n = len(lens)
+    arr = (ctypes.c_int32 * max(1, n))(*[int(x) for x in lens])
+    chunk = (ctypes.c_int32 * max(1, n))()
+    base = (ctypes.c_int32 * (n + 1))()
+    _check(load().qasr_plan_decode(n, arr, nkvh, cus, chunk, base))
+    return list(chunk[:n]), list(base)
+
+
+def plan_prefill(rows: int, kv_start: int, nkvh: int = 8):
+    """The prefill plan of one launch (qasr_plan_prefill; host only): rows
+    per block, row blocks, tiles per split and each row block's first item."""
+    rpb, nrb, tps = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    sp = (ctypes.c_int32 * 65)()
+    _check(load().qasr_plan_prefill(rows, kv_start, nkvh, ctypes.byref(rpb), ctypes.byref(nrb),
+                                    ctypes.byref(tps), sp))
+    return {"rows_per_block": rpb.value, "nrb": nrb.value, "tiles_per_split": tps.value,
+            "sp_base": list(sp[:nrb.value + 1])}
 
 
 LAYER_WEIGHT_NAMES = ("input_layernorm", "q_proj", "k_proj", "v_proj", "q_norm", "k_norm",
