@@ -139,15 +139,19 @@ int ensure_prefill_ws(qasr_kv* kv, int64_t items) {
 }
 
 // Decode launch plan: a fixed number of workgroups (QASR_DECODE_WGS, default
-// one per CU: every CU then carries the same number of workgroups; with the
-// K/V stream's non-temporal loads one per CU measured 1.3% faster than two
-// at 16 slots, and equal at 64), whose
-// chunks are as even as possible.  Entry b is cut into n_b equal chunks of
-// whole 32-key passes; starting from one chunk per entry, the entry with the
-// largest chunk gets one more until the workgroup budget is used (and the
-// largest chunk is within 1.5x of the average) or every chunk is down to
-// QASR_DECODE_MIN_CHUNK keys or every entry has QASR_DECODE_MAX_SPLIT chunks
-// (the merge reads one partial per chunk).
+// one per CU), each streaming one chunk of one entry's keys for one kv head.
+// One CU streams at most ~45-70 GB/s (a bare stream measures the same), so
+// a CU cannot speed up when others finish: the launch ends at full HBM
+// rate only while enough CUs are still streaming.  So when the batch leaves
+// room to split (entries x kv heads below the budget), every entry is cut
+// into chunks of one common size C -- the smallest multiple of 32 keys that
+// fits the budget (and at least QASR_DECODE_MIN_CHUNK keys, at most
+// QASR_DECODE_MAX_SPLIT chunks per entry) -- plus a shorter last chunk, and
+// entries shorter than C stay whole.  Most workgroups then carry C keys and
+// stream until the end (config 3: 20.1 against 21.0 us for equal chunks
+// within each entry, the plan before).  Batches at or past the budget split
+// their longest entries while a chunk exceeds 1.5x the average keys per
+// workgroup; the extra workgroups run as the first ones finish.
 int chunk_of(int L, int n) {
     const int c = (L + n - 1) / n;
     return (c + qasr::kDecodeTileKeys - 1) / qasr::kDecodeTileKeys * qasr::kDecodeTileKeys;
@@ -158,36 +162,45 @@ void plan_decode_chunks(qasr::DecodePlan& P, int nkvh, int cus) {
     const int min_chunk = std::max(32, env_int("QASR_DECODE_MIN_CHUNK", qasr::kDecodeMinChunk));
     const int max_split = std::max(1, std::min(env_int("QASR_DECODE_MAX_SPLIT", qasr::kDecodeMaxSplit),
                                                qasr::kDecodeMaxChunksPerEntry));
-    int n[qasr::kMaxBatch];
+    int n[qasr::kMaxBatch];  // chunks per entry (greedy plan)
     int wgs = 0;
     for (int i = 0; i < P.batch; ++i) {
         n[i] = 1;
         wgs += nkvh;
     }
-    int64_t keys = 0;
-    for (int i = 0; i < P.batch; ++i) keys += (int64_t)nkvh * P.len[i];
-    // Past the budget (batches with more entries x kv heads than it), chunks
-    // more than 1.5x the average keys per workgroup are still split: the
-    // extra workgroups run as the first ones finish.
-    while (wgs + nkvh <= qasr::kDecodeMaxItems / 2) {
-        int best = -1, best_chunk = 0;
-        for (int i = 0; i < P.batch; ++i) {
-            const int c = chunk_of(P.len[i], n[i]);
-            if (n[i] < max_split && chunk_of(P.len[i], n[i] + 1) >= min_chunk &&
-                c > best_chunk) {
-                best = i;
-                best_chunk = c;
+    int common = 0;  // C of the common-size plan, 0 for the greedy plan
+    if (wgs < target) {
+        int c = chunk_of(min_chunk, 1);
+        for (int i = 0; i < P.batch; ++i) c = std::max(c, chunk_of(P.len[i], max_split));
+        auto items = [&](int cc) {
+            int64_t t = 0;
+            for (int i = 0; i < P.batch; ++i) t += (int64_t)nkvh * ((P.len[i] + cc - 1) / cc);
+            return t;
+        };
+        while (items(c) > target) c += qasr::kDecodeTileKeys;
+        common = c;
+    } else {
+        int64_t keys = 0;
+        for (int i = 0; i < P.batch; ++i) keys += (int64_t)nkvh * P.len[i];
+        while (wgs + nkvh <= qasr::kDecodeMaxItems / 2) {
+            int best = -1, best_chunk = 0;
+            for (int i = 0; i < P.batch; ++i) {
+                const int c = chunk_of(P.len[i], n[i]);
+                if (n[i] < max_split && chunk_of(P.len[i], n[i] + 1) >= min_chunk &&
+                    c > best_chunk) {
+                    best = i;
+                    best_chunk = c;
+                }
             }
+            if (best < 0 || 2 * (int64_t)best_chunk * wgs <= 3 * keys) break;
+            ++n[best];
+            wgs += nkvh;
         }
-        if (best < 0) break;
-        if (wgs + nkvh > target && 2 * (int64_t)best_chunk * wgs <= 3 * keys) break;
-        ++n[best];
-        wgs += nkvh;
     }
     P.wg_base[0] = 0;
     for (int i = 0; i < P.batch; ++i) {
         const int L = P.len[i];
-        const int chunk = chunk_of(L, n[i]);
+        const int chunk = common ? std::min(common, chunk_of(L, 1)) : chunk_of(L, n[i]);
         P.chunk[i] = chunk;
         P.wg_base[i + 1] = P.wg_base[i] + nkvh * ((L + chunk - 1) / chunk);
     }

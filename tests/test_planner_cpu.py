@@ -57,6 +57,8 @@ def test_decode_plan_covers_every_key_random_batches():
         check_decode_plan(lens, chunk, base)
         # the budget is one workgroup per CU unless the batch alone exceeds it
         assert base[-1] >= NKVH * n
+        if NKVH * n < 256:
+            assert base[-1] <= 256
 
 
 def test_decode_plan_bench_configs():
@@ -64,14 +66,24 @@ def test_decode_plan_bench_configs():
     chunk, base = qasr_attn.plan_decode([L + 1 for L in lens3], NKVH, 256)
     check_decode_plan([L + 1 for L in lens3], chunk, base)
     assert base[-1] == 256 and max(chunk) == 960  # config 3: one workgroup per CU
+    # one common chunk size; only entries shorter than it stay whole
+    lens3p = [L + 1 for L in lens3]
+    assert all(c == 960 or c >= L for c, L in zip(chunk, lens3p))
+    full = sum(NKVH * (L // 960) for L in lens3p if L > 960)
+    assert full >= 128  # most workgroups stream a full chunk until the end
     chunk, base = qasr_attn.plan_decode([8193], NKVH, 256)
     assert chunk == [288] and base == [0, 8 * 29]  # config 4: 29 chunks of 288 keys
     chunk, base = qasr_attn.plan_decode([512], NKVH, 256)
     assert chunk == [128] and base == [0, 32]  # config 1: 128-key minimum chunk
     # below two minimum chunks an entry stays whole: one chunk of whole passes
     chunk, base = qasr_attn.plan_decode([1, 2, 31, 32, 33, 255, 256, 257], NKVH, 256)
-    assert chunk == [32, 32, 32, 32, 64, 128, 128, 160]
-    assert base == [0, 8, 16, 24, 32, 40, 56, 72, 88]
+    assert chunk == [32, 32, 32, 32, 64, 128, 128, 128]
+    assert base == [0, 8, 16, 24, 32, 40, 56, 72, 96]
+    # a batch at the budget (64 entries x 8 kv heads) splits only its longest entries
+    lens = [100] * 63 + [4000]
+    chunk, base = qasr_attn.plan_decode(lens, NKVH, 256)
+    check_decode_plan(lens, chunk, base)
+    assert chunk[:63] == [128] * 63 and base[-1] > 512
 
 
 def test_decode_plan_knobs(monkeypatch):
