@@ -18,7 +18,8 @@ timed on a bounded sample of config 3 on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
                        [--only decode3|decode1|decode4|decode5|decode16x2k|prefill2|prefill4|
-                               config4_whole|streamread|mfma_ceiling|copycal|decoder16|decoder1|
+                               config4_whole|streamread|streamread_per_cu|mfma_ceiling|copycal|
+                               decoder16|decoder1|
                                decoder16_int8|decoder1_int8|serving|prefill_batch|prefill_one|
                                gemm]
 """
@@ -325,6 +326,42 @@ def stream_read_calibration(nbytes: int, steps: int, warmup: int, copies: int = 
     ctx.close()
     out["best"] = {"shape": best[2], "us_per_launch": round(best[0], 3), "GBps": round(best[1], 1),
                    "frac_of_peak": round(best[1] / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def stream_per_cu_calibration(steps: int, warmup: int, per_wg: int = 1216 * 1024,
+                              counts=(8, 32, 128, 256), waves=(4, 8)):
+    """What one CU streams: qasr_stream_read with few workgroups (at most one
+    per CU), each reading `per_wg` contiguous bytes (about the largest config-3
+    entry's K+V of one kv head), four rotating buffers per count so that no
+    launch reads data the previous one left in the Infinity Cache.  A CU's
+    rate does not rise when others are idle: the decode planner keeps most
+    CUs streaming until the end for that reason."""
+    import torch
+
+    import qasr_attn
+
+    ctx = qasr_attn.Context(NQH, NKVH, HD, LAYERS, 1e-6, 16384, 0)
+    out = {"bytes_per_workgroup": per_wg, "shapes": {}}
+    for w in waves:
+        for n in counts:
+            total = n * per_wg
+            bufs = [torch.empty(total // 2, dtype=torch.float16, device="cuda").normal_() for _ in range(4)]
+            sink = torch.empty(n * w, dtype=torch.int32, device="cuda")
+
+            def step():
+                for b in bufs:
+                    qasr_attn.stream_read(ctx, b, n, w, sink)
+
+            ms, graph = graph_time(torch, step, steps, warmup)
+            del graph
+            us = ms * 1e3 / len(bufs)
+            out["shapes"][f"{n}x{w}"] = {"us_per_launch": round(us, 2),
+                                        "GBps_per_workgroup": round(per_wg / (us * 1e-6) / 1e9, 1),
+                                        "GBps": round(total / (us * 1e-6) / 1e9, 1)}
+            del bufs
+            torch.cuda.empty_cache()
+    ctx.close()
     return out
 
 
@@ -686,6 +723,7 @@ def main():
             "prefill4": lambda: bench_prefill(512, 7680, K, W),
             "copycal": lambda: copy_calibration(K),
             "streamread": lambda: stream_read_calibration(decode_bytes([L + 1 for L in lens3]), K, W),
+            "streamread_per_cu": lambda: stream_per_cu_calibration(K, W),
             "mfma_ceiling": lambda: mfma_calibration(),
             "config4_whole": lambda: bench_config4_whole(max(3, K // 10), 1),
             "decoder16": lambda: bench_text_decoder("1.7B", lens3, K, W),
@@ -722,6 +760,8 @@ def main():
         log("[bench] streaming-read calibration at config 3's bytes per launch")
         extra["streamread_config3_bytes"] = stream_read_calibration(
             decode_bytes([L + 1 for L in lens3]), K, W)
+        log("[bench] what one CU streams (few workgroups)")
+        extra["stream_per_cu"] = stream_per_cu_calibration(max(5, K // 5), 2)
         log("[bench] matrix-core calibration")
         extra["mfma_calibration"] = mfma_calibration()
         log("[bench] text decoder steps (whole decoder around the attention path)")
