@@ -418,7 +418,8 @@ struct NormPrologue {
 // rows' chunk sums of squares.  s_y: 256 floats of this wave's LDS.
 template <int OUT>
 __device__ __forceinline__ void skinny_tile_out(const SkinnyArgs& p, qasr::float4v sum, int tile,
-                                                int group, int lane, float* s_y) {
+                                                int group, int lane, float* s_y,
+                                                const f16* y_pre = nullptr) {
     const int r = lane & 15, g = lane >> 4;
     const int M = p.M, N = p.N, groups = p.groups;
     const int n0 = tile * 16;
@@ -463,7 +464,8 @@ __device__ __forceinline__ void skinny_tile_out(const SkinnyArgs& p, qasr::float
             ((float*)p.Y)[idx] = sum[i];
         } else {
             f16* y = (f16*)p.Y;
-            const f16 out = (f16)(OUT == kOutAcc ? (float)y[idx] + sum[i] : sum[i]);
+            const f16 yv = OUT == kOutAcc ? (y_pre ? y_pre[i] : y[idx]) : (f16)0.0f;
+            const f16 out = (f16)(OUT == kOutAcc ? (float)yv + sum[i] : sum[i]);
             y[idx] = out;
             if constexpr (OUT == kOutAcc) sum[i] = (float)out;  // for the chunk sums below
         }
@@ -580,6 +582,18 @@ __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
     Stage s0, s1;
     NormPrologue<KS> np;
     if constexpr (NORM) np.issue(p, wave, lane);
+    // The residual this lane's outputs add (rows 4 g + i, column n0 + r),
+    // requested ahead of the weight stream so the epilogue does not wait a
+    // memory round trip for it (nothing in this launch writes it before the
+    // epilogue reads it).
+    f16 y_pre[4] = {};
+    if constexpr (OUT == kOutAcc) {
+        if (wave == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (4 * g + i < M) y_pre[i] = ((const f16*)p.Y)[(int64_t)(4 * g + i) * N + n0 + r];
+        }
+    }
     load_stage(0, s0);
     load_stage(1, s1);
     if constexpr (NORM) inv = np.finish(p, s_gain, s_part, wave, lane, r);
@@ -604,7 +618,8 @@ __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
     qasr::float4v sum = s_red[0][lane];
 #pragma unroll
     for (int w = 1; w < KS; ++w) sum += s_red[w][lane];
-    skinny_tile_out<OUT>(p, sum, tile, blockIdx.y, lane, reinterpret_cast<float*>(&s_red[0][0]));
+    skinny_tile_out<OUT>(p, sum, tile, blockIdx.y, lane, reinterpret_cast<float*>(&s_red[0][0]),
+                         OUT == kOutAcc ? y_pre : nullptr);
 }
 
 // ---- skinny GEMM with the weight rows staged in LDS ------------------------
