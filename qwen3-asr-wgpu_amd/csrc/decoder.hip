@@ -748,6 +748,156 @@ __global__ __launch_bounds__(kLdsWaves * 64) void skinny_lds_kernel(SkinnyArgs p
     }
 }
 
+// ---- skinny GEMM with the activation rows shared in LDS ---------------------
+// The product of skinny_gemm_kernel, with its K slices and summation order,
+// for wide outputs: a workgroup takes TPW consecutive column tiles with KS
+// waves each (wave w: tile w / KS, K slice w % KS of the workgroup's K
+// range), and the 16 activation rows of that K range are read once into LDS
+// -- normed there once when NORM, as skinny_gemm_kernel norms them on their
+// way into the MFMA -- and shared by the TPW tiles.  skinny_gemm_kernel
+// requests them again for every tile: at 16 rows as many bytes, from L2, as
+// the weights it streams.  The weights still go straight from the buffer
+// loads into the MFMA B operand, two stages of U k-steps in flight per wave.
+// Activation rows are padded by 16 bytes, so the 16-row operand read hits 16
+// different bank groups.  The results equal skinny_gemm_kernel's bit for bit.
+constexpr int kSharedMaxK = 3072;  // K per workgroup (the K range of one group)
+constexpr int kSharedPad = 8;      // halves of padding per activation row
+constexpr int kSharedMinRows = 8;  // fewer rows: their loads are mostly out of range, nothing to share
+
+template <int KS, int TPW, int KMAX, bool W8, int OUT, bool NORM>
+__global__ __launch_bounds__(KS * TPW * 64) void skinny_shared_kernel(SkinnyArgs p) {
+    constexpr int NW = KS * TPW, NT = NW * 64;
+    constexpr int U = kSkinnyUnroll;
+    constexpr int AROW = KMAX + kSharedPad;
+    static_assert(kSkinnyRows * AROW * 2 >= NW * 64 * 16, "the partials reuse the activation rows");
+    __shared__ __attribute__((aligned(16))) f16 s_act[kSkinnyRows * AROW];
+    // After the MFMAs the activation rows hold the per-wave partials.
+    qasr::float4v(*s_red)[64] = reinterpret_cast<qasr::float4v(*)[64]>(s_act);
+    __shared__ __attribute__((aligned(16))) float s_gain[NORM ? kNormMaxK : 1];
+    __shared__ float s_part[NORM ? kSkinnyRows * 4 : 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int M = p.M, N = p.N, K = p.K, groups = p.groups;
+    const int t = wave / KS, ks = wave % KS;
+    const int ntiles = N / 16;
+    const int tile = blockIdx.x * TPW + t;
+    const bool tile_ok = tile < ntiles;
+    const int tile_c = tile_ok ? tile : ntiles - 1;  // a wave past the last tile streams a real one, unused
+    const int kg = K / groups, kbase = blockIdx.y * kg;
+    const int kw = kg / KS, kbeg = kbase + ks * kw;
+    constexpr int wbytes = W8 ? 1 : 2;
+    constexpr bool kGlu = OUT == kOutGlu;
+    const int n0 = tile_c * 16;
+    const int w0 = kGlu ? 8 * tile_c : n0;
+    const int rr = kGlu ? (r < 8 ? r : N / 2 + r - 8) : r;
+    const int64_t wrows = kGlu ? (int64_t)(N / 2 + 8) : 16;
+    const __amdgpu_buffer_rsrc_t wres =
+        rsrc((const char*)p.W + (int64_t)w0 * K * wbytes, wrows * K * wbytes);
+    float wsc = 0.0f;
+    if constexpr (W8) wsc = p.scale[w0 + rr];
+    const int woff = rr * K * 2 + g * 16;
+
+    struct Stage {
+        qasr::half8v b[U];
+        uint2 q[U];
+    };
+    const int nst = kw / (32 * U);
+    auto load_stage = [&](int st, Stage& S) {
+        const int k0 = kbeg + st * 32 * U;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kk = k0 + 32 * u;
+            if constexpr (W8)
+                S.q[u] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wres, rr * K + g * 8 + kk, 0, 0));
+            else
+                S.b[u] = load8(wres, woff + kk * 2);
+        }
+    };
+    // The residual of this tile's outputs (kOutAcc), ahead of the stream.
+    f16 y_pre[4] = {};
+    if constexpr (OUT == kOutAcc) {
+        if (ks == 0 && tile_ok) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (4 * g + i < M) y_pre[i] = ((const f16*)p.Y)[(int64_t)(4 * g + i) * N + n0 + r];
+        }
+    }
+    NormPrologue<NW> np;
+    if constexpr (NORM) np.issue(p, wave, lane);
+    Stage s0, s1;
+    load_stage(0, s0);
+    load_stage(1, s1);
+    // The workgroup's activation rows: piece q = threadIdx.x + i NT is row
+    // q % 16 (= r, this lane's row: NT is a multiple of 16), chunk q / 16 of 8
+    // values; rows past M read as zeros.  Up to 8 pieces per thread and round.
+    const int nchunk = kg / 8, npieces = kSkinnyRows * nchunk;
+    float inv = 0.0f;
+    if constexpr (NORM) inv = np.finish(p, s_gain, s_part, wave, lane, r);
+    for (int base = 0; base < npieces; base += 8 * NT) {
+        uint4 x[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int q = base + threadIdx.x + i * NT, c = q >> 4;
+            x[i] = (q < npieces && r < M) ? *(const uint4*)(p.X + (int64_t)r * K + kbase + 8 * c)
+                                          : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int q = base + threadIdx.x + i * NT, c = q >> 4;
+            if (q >= npieces) continue;
+            H8 v;
+            v.u = x[i];
+            if constexpr (NORM) {
+                const float* gv = &s_gain[kbase + 8 * c];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v.e[e] = f16_of_f32(((float)v.e[e] * inv) * gv[e]);
+            }
+            *(uint4*)&s_act[r * AROW + 8 * c] = v.u;
+        }
+    }
+    __syncthreads();
+
+    qasr::float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const f16* arow = &s_act[r * AROW + 8 * g];
+    auto mma_stage = [&](const Stage& S, int st) {
+        const int k0 = kbeg - kbase + st * 32 * U;  // within the workgroup's K range
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const qasr::half8v xa = *(const qasr::half8v*)&arow[k0 + 32 * u];
+            if constexpr (W8) {
+                const qasr::half8v b = dequant8(S.q[u].x, S.q[u].y, wsc);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, b, acc, 0, 0, 0);
+            } else {
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, S.b[u], acc, 0, 0, 0);
+            }
+        }
+    };
+    int st = 0;
+    for (; st + 2 < nst; st += 2) {
+        __builtin_amdgcn_sched_barrier(0);
+        mma_stage(s0, st);
+        __builtin_amdgcn_sched_barrier(0);
+        load_stage(st + 2, s0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_stage(s1, st + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_stage(st + 3, s1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mma_stage(s0, st);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_stage(s1, st + 1);
+    __syncthreads();  // every wave is done reading the activation rows
+    s_red[wave][lane] = acc;
+    __syncthreads();
+    if (ks != 0 || !tile_ok) return;
+    qasr::float4v sum = s_red[t * KS][lane];
+#pragma unroll
+    for (int w = 1; w < KS; ++w) sum += s_red[t * KS + w][lane];
+    skinny_tile_out<OUT>(p, sum, tile, blockIdx.y, lane, reinterpret_cast<float*>(&s_red[t * KS][0]),
+                         OUT == kOutAcc ? y_pre : nullptr);
+}
+
 const char* blas_msg(rocblas_status st) { return rocblas_status_to_string(st); }
 
 }  // namespace
@@ -766,6 +916,8 @@ struct qasr_decoder {
     int lds_gemm = 1;              // QASR_SKINNY_LDS: 0 older kernel only, 2 LDS kernel wherever it fits
     int lds_tpw = 0, lds_groups = 0;  // QASR_SKINNY_TPW / _GROUPS: shape overrides (0 = planner)
     bool own_gemm = false;            // QASR_PREFILL_GEMM=own: gemm_f16_kernel for the prefill projections
+    int shared_tiles = 3;             // QASR_SKINNY_SHARED: skinny_shared_kernel tiles per workgroup (0 off)
+    int shared_min_tiles = 512;       // QASR_SKINNY_SHARED_MIN_TILES: narrower outputs keep skinny_gemm_kernel
     // activations, max_rows rows each
     f16* x = nullptr;     // residual stream [rows][hs]
     f16* n = nullptr;     // normed rows [rows][hs]
@@ -828,6 +980,7 @@ void free_decoder(qasr_decoder* d) {
 struct SkinnyShape {
     int ks = 0, groups = 1;
     int nks = 0, tpw = 1, nbuf = 1;  // nks > 0: skinny_lds_kernel
+    int shared_tiles = 0;            // > 1: skinny_shared_kernel, this many tiles per workgroup
 };
 
 SkinnyShape lds_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8) {
@@ -851,7 +1004,7 @@ SkinnyShape lds_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8) {
     return sh;
 }
 
-SkinnyShape skinny_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8 = false) {
+SkinnyShape skinny_base_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8) {
     if (d->force_blas || rows > kSkinnyRows || n_out % 16) return SkinnyShape{};
     if (d->lds_gemm) {
         const SkinnyShape sh = lds_shape(d, rows, n_out, k, w8);
@@ -866,6 +1019,34 @@ SkinnyShape skinny_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8 = 
     for (int ks : {12, 8, 4})
         if (k % (ks * kSkinnyPair) == 0) return SkinnyShape{ks, 1};
     return SkinnyShape{};
+}
+
+// Tiles per workgroup of skinny_shared_kernel for a base shape, or 0 where
+// it does not apply: fewer than kSharedMinRows rows, or outputs narrower than
+// QASR_SKINNY_SHARED_MIN_TILES column tiles (512: 1.7B gate|up).  Three tiles
+// of four waves took the 1.7B 16-slot gate|up from 17.1 to 16.1 us and the
+// whole step from 1929 to 1913 us (int8: 1902 to 1835 us, where the per-tile
+// kernel's activation bytes are twice its weight bytes); four tiles, or
+// narrower projections (down_proj 11.8 -> 17.0 us at three tiles: too few
+// workgroups) measured slower.
+// QASR_SKINNY_SHARED: 0 never, T forces T tiles.
+int shared_tiles(qasr_decoder* d, const SkinnyShape& sh, int rows, int n_out, int k) {
+    if (!sh.ks || sh.nks || rows < kSharedMinRows || k / sh.groups > kSharedMaxK) return 0;
+    const int want = d->shared_tiles;
+    if (want == 0) return 0;
+    const int tiles = n_out / 16;
+    if (tiles < d->shared_min_tiles) return 0;
+    for (int t : {4, 3, 2}) {
+        if (want > 1 && t != want) continue;
+        if (sh.ks * t <= 16 && (sh.ks == 4 || t == 2) && tiles >= t) return t;
+    }
+    return 0;
+}
+
+SkinnyShape skinny_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8 = false) {
+    SkinnyShape sh = skinny_base_shape(d, rows, n_out, k, w8);
+    sh.shared_tiles = shared_tiles(d, sh, rows, n_out, k);
+    return sh;
 }
 
 template <bool W8, int OUT, bool NORM>
@@ -910,8 +1091,38 @@ int launch_skinny_lds(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
     return QASR_OK;
 }
 
+template <bool W8, int OUT, bool NORM>
+int launch_skinny_shared(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
+    const int t = sh.shared_tiles;
+    const dim3 grid((a.N / 16 + t - 1) / t, sh.groups);
+    const bool k2 = a.K / sh.groups <= 2048;  // 66 KB of activation rows: two workgroups per CU
+    if (sh.ks == 4 && t == 4 && k2)
+        hipLaunchKernelGGL((skinny_shared_kernel<4, 4, 2048, W8, OUT, NORM>), grid, dim3(16 * 64), 0, d->stream, a);
+    else if (sh.ks == 4 && t == 4)
+        hipLaunchKernelGGL((skinny_shared_kernel<4, 4, kSharedMaxK, W8, OUT, NORM>), grid, dim3(16 * 64), 0, d->stream, a);
+    else if (sh.ks == 4 && t == 3 && k2)
+        hipLaunchKernelGGL((skinny_shared_kernel<4, 3, 2048, W8, OUT, NORM>), grid, dim3(12 * 64), 0, d->stream, a);
+    else if (sh.ks == 4 && t == 3)
+        hipLaunchKernelGGL((skinny_shared_kernel<4, 3, kSharedMaxK, W8, OUT, NORM>), grid, dim3(12 * 64), 0, d->stream, a);
+    else if (sh.ks == 4 && t == 2 && k2)
+        hipLaunchKernelGGL((skinny_shared_kernel<4, 2, 2048, W8, OUT, NORM>), grid, dim3(8 * 64), 0, d->stream, a);
+    else if (sh.ks == 4 && t == 2)
+        hipLaunchKernelGGL((skinny_shared_kernel<4, 2, kSharedMaxK, W8, OUT, NORM>), grid, dim3(8 * 64), 0, d->stream, a);
+    else if (sh.ks == 8 && t == 2 && k2)
+        hipLaunchKernelGGL((skinny_shared_kernel<8, 2, 2048, W8, OUT, NORM>), grid, dim3(16 * 64), 0, d->stream, a);
+    else if (sh.ks == 8 && t == 2)
+        hipLaunchKernelGGL((skinny_shared_kernel<8, 2, kSharedMaxK, W8, OUT, NORM>), grid, dim3(16 * 64), 0, d->stream, a);
+    else
+        return fail(QASR_EINVAL, "skinny GEMM: %d waves x %d shared tiles", sh.ks, t);
+    HIP_TRY(hipGetLastError(), "projection launch");
+    return QASR_OK;
+}
+
 template <int OUT, bool NORM = false>
 int launch_skinny(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
+    if (sh.shared_tiles > 1)
+        return a.scale ? launch_skinny_shared<true, OUT, NORM>(d, sh, a)
+                       : launch_skinny_shared<false, OUT, NORM>(d, sh, a);
     if (sh.nks)
         return a.scale ? launch_skinny_lds<true, OUT, NORM>(d, sh, a)
                        : launch_skinny_lds<false, OUT, NORM>(d, sh, a);
@@ -1130,6 +1341,10 @@ int bind_stream(qasr_decoder* d, void* stream) {
     d->lds_groups = gp ? std::atoi(gp) : 0;
     const char* pg = std::getenv("QASR_PREFILL_GEMM");
     d->own_gemm = pg && std::string(pg) == "own";
+    const char* sh = std::getenv("QASR_SKINNY_SHARED");
+    d->shared_tiles = sh ? std::atoi(sh) : 3;
+    const char* smt = std::getenv("QASR_SKINNY_SHARED_MIN_TILES");
+    d->shared_min_tiles = smt ? std::atoi(smt) : 512;
     const rocblas_status st = rocblas_set_stream(d->blas, (hipStream_t)stream);
     if (st != rocblas_status_success) return fail(QASR_EDEVICE, "rocblas_set_stream: %s", blas_msg(st));
     return QASR_OK;

@@ -444,6 +444,49 @@ def test_fused_epilogues_equal_unfused(gpu, model, batch, int8, lds, monkeypatch
     assert np.array_equal(out["fused"][1], out["unfused"][1])
 
 
+@pytest.mark.parametrize("tiles", ["2", "3", "4"])
+@pytest.mark.parametrize("model,batch,int8", [("1.7B", 16, False), ("1.7B", 8, True),
+                                              ("0.6B", 16, True), ("0.6B", 9, False)])
+def test_shared_activation_projections_equal_per_tile(gpu, model, batch, int8, tiles, monkeypatch):
+    """The decode step's projections with the activation rows shared in LDS
+    by several column tiles (QASR_SKINNY_SHARED=tiles: skinny_shared_kernel,
+    the same K slices, summation order and norm rounding as
+    skinny_gemm_kernel) against the per-tile kernel: identical logits and
+    tokens, bitwise -- at both model shapes, f16 and int8, with the folded
+    norms, gate|up with SiLU * up, the residual projections and down_proj's
+    K split across workgroups."""
+    import torch
+
+    from decoder_model import CFG_1P7B
+    from gpu_helpers import say
+
+    cfg = dict(CFG_1P7B if model == "1.7B" else CFG_0P6B, layers=3, vocab=8192)
+    W = synth_weights(cfg, SEED_BASE + 1300 + batch, device="cuda")
+    if int8:
+        for key in list(W):
+            if isinstance(key, tuple) and key[1] in PROJECTIONS:
+                q, s = _quantize_rows(W[key])
+                W[key], W[(key[0], key[1] + "_scale")] = q, s
+    dec = _native(cfg, W, batch, 1024, max_rows=16)
+    for i in range(batch):
+        dec.prefill(_prompt(SEED_BASE + 1310 + i, 7 + 2 * i, cfg["hs"]), 0, slot=i)
+    slots, pos = list(range(batch)), [dec.pos[i] for i in range(batch)]
+    tok = torch.tensor([dec.last[i] for i in range(batch)], dtype=torch.int32, device="cuda")
+    out = {}
+    monkeypatch.setenv("QASR_SKINNY_SHARED_MIN_TILES", "0")  # every eligible projection, not only the widest
+    for name, shared in (("per_tile", "0"), ("shared", tiles)):
+        monkeypatch.setenv("QASR_SKINNY_SHARED", shared)
+        nxt = torch.empty(batch, dtype=torch.int32, device="cuda")
+        lg = torch.empty((batch, cfg["vocab"]), dtype=torch.float32, device="cuda")
+        say(f"{model} batch {batch} int8={int8}: {name} step (tiles {tiles})")
+        dec.step_tokens(slots, pos, tok, nxt, lg)
+        torch.cuda.synchronize()
+        out[name] = (nxt.cpu().numpy(), lg.cpu().numpy())
+    dec.close()
+    assert np.array_equal(out["shared"][0], out["per_tile"][0])
+    assert np.array_equal(out["shared"][1], out["per_tile"][1])
+
+
 @pytest.mark.parametrize("model,int8", [("1.7B", False), ("0.6B", True)])
 def test_prefill_own_gemm_close_to_rocblas(gpu, model, int8, monkeypatch):
     """The prefill projections through the build's own MFMA GEMM
