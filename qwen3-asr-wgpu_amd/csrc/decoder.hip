@@ -898,6 +898,145 @@ __global__ __launch_bounds__(KS * TPW * 64) void skinny_shared_kernel(SkinnyArgs
                          OUT == kOutAcc ? y_pre : nullptr);
 }
 
+// ---- skinny GEMM with several column tiles per wave ------------------------
+// The product of skinny_gemm_kernel, each wave taking TW consecutive column
+// tiles over its K slice: one activation load per k-step feeds TW MFMAs
+// (skinny_gemm_kernel loads the activations again for every tile).  A
+// workgroup of KS waves covers TW tiles with K cut KS ways, the K slices and
+// summation order of skinny_gemm_kernel's KS waves, so the results are
+// bitwise its results.  For the 1.7B gate|up (f16) four tiles per wave took
+// the 16-slot step from 1917 us (skinny_shared_kernel) to 1898 us; two
+// tiles, or the narrower projections (fewer workgroups than CUs), measured
+// slower, and so did int8 weights, whose dequantisation then runs on one
+// wave per SIMD (1904 against 1837 us).
+template <int KS, int TW, int U, bool W8, int OUT, bool NORM>
+__global__ __launch_bounds__(KS * 64) void skinny_multi_kernel(SkinnyArgs p) {
+    static_assert(TW <= KS, "one epilogue wave per tile");
+    __shared__ qasr::float4v s_red[TW][KS][64];
+    __shared__ __attribute__((aligned(16))) float s_gain[NORM ? kNormMaxK : 1];
+    __shared__ float s_part[NORM ? kSkinnyRows * 4 : 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int M = p.M, N = p.N, K = p.K, groups = p.groups;
+    const int ntiles = N / 16;
+    const int t0 = blockIdx.x * TW;
+    const int kw = K / (KS * groups);
+    const int kbeg = (blockIdx.y * KS + wave) * kw;
+    constexpr int wbytes = W8 ? 1 : 2;
+    constexpr bool kGlu = OUT == kOutGlu;
+    // Weight row of this lane in tile j (clamped to the last tile: a tile
+    // past the end streams a real one, unused).
+    __amdgpu_buffer_rsrc_t wres[TW];
+    float wsc[TW];
+    int rrow[TW];
+#pragma unroll
+    for (int j = 0; j < TW; ++j) {
+        const int tile = min(t0 + j, ntiles - 1);
+        const int w0 = kGlu ? 8 * tile : tile * 16;
+        rrow[j] = kGlu ? (r < 8 ? r : N / 2 + r - 8) : r;
+        const int64_t wrows = kGlu ? (int64_t)(N / 2 + 8) : 16;
+        wres[j] = rsrc((const char*)p.W + (int64_t)w0 * K * wbytes, wrows * K * wbytes);
+        wsc[j] = 0.0f;
+        if constexpr (W8) wsc[j] = p.scale[w0 + rrow[j]];
+    }
+    const __amdgpu_buffer_rsrc_t xres = rsrc(p.X, (int64_t)M * K * 2);
+    const int xoff = r * K * 2 + g * 16;
+    struct Stage {
+        qasr::half8v b[TW][U], x[U];
+        uint2 q[TW][U];
+    };
+    const int nst = kw / (32 * U);
+    auto load_stage = [&](int st, Stage& S) {
+        const int k0 = kbeg + st * 32 * U;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int kk = k0 + 32 * u;
+#pragma unroll
+            for (int j = 0; j < TW; ++j) {
+                if constexpr (W8)
+                    S.q[j][u] = __builtin_bit_cast(
+                        uint2, __builtin_amdgcn_raw_buffer_load_b64(wres[j], rrow[j] * K + g * 8 + kk, 0, 0));
+                else
+                    S.b[j][u] = load8(wres[j], rrow[j] * K * 2 + g * 16 + kk * 2);
+            }
+            S.x[u] = load8(xres, xoff + kk * 2);
+        }
+    };
+    qasr::float4v acc[TW];
+#pragma unroll
+    for (int j = 0; j < TW; ++j) acc[j] = qasr::float4v{0.0f, 0.0f, 0.0f, 0.0f};
+    float inv = 0.0f;
+    auto act = [&](const qasr::half8v& x, int kk) {
+        if constexpr (NORM) {
+            const float4 g0 = *(const float4*)&s_gain[kk + 8 * g];
+            const float4 g1 = *(const float4*)&s_gain[kk + 8 * g + 4];
+            const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+            qasr::half8v n;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) n[e] = f16_of_f32(((float)x[e] * inv) * gv[e]);
+            return n;
+        } else {
+            return x;
+        }
+    };
+    auto mma_stage = [&](const Stage& S, int st) {
+        const int k0 = kbeg + st * 32 * U;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const qasr::half8v xa = act(S.x[u], k0 + 32 * u);
+#pragma unroll
+            for (int j = 0; j < TW; ++j) {
+                if constexpr (W8) {
+                    const qasr::half8v b = dequant8(S.q[j][u].x, S.q[j][u].y, wsc[j]);
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, b, acc[j], 0, 0, 0);
+                } else {
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, S.b[j][u], acc[j], 0, 0, 0);
+                }
+            }
+        }
+    };
+    // The residual of the tile this wave finishes (kOutAcc), ahead of the stream.
+    f16 y_pre[4] = {};
+    const int my_tile = t0 + wave;  // the tile this wave finishes, if wave < TW
+    if constexpr (OUT == kOutAcc) {
+        if (wave < TW && my_tile < ntiles) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (4 * g + i < M) y_pre[i] = ((const f16*)p.Y)[(int64_t)(4 * g + i) * N + my_tile * 16 + r];
+        }
+    }
+    Stage s0, s1;
+    NormPrologue<KS> np;
+    if constexpr (NORM) np.issue(p, wave, lane);
+    load_stage(0, s0);
+    load_stage(1, s1);
+    if constexpr (NORM) inv = np.finish(p, s_gain, s_part, wave, lane, r);
+    int st = 0;
+    for (; st + 2 < nst; st += 2) {
+        __builtin_amdgcn_sched_barrier(0);
+        mma_stage(s0, st);
+        __builtin_amdgcn_sched_barrier(0);
+        load_stage(st + 2, s0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_stage(s1, st + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_stage(st + 3, s1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mma_stage(s0, st);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_stage(s1, st + 1);
+#pragma unroll
+    for (int j = 0; j < TW; ++j) s_red[j][wave][lane] = acc[j];
+    __syncthreads();
+    if (wave >= TW || my_tile >= ntiles) return;
+    qasr::float4v sum = s_red[wave][0][lane];
+#pragma unroll
+    for (int w = 1; w < KS; ++w) sum += s_red[wave][w][lane];
+    skinny_tile_out<OUT>(p, sum, my_tile, blockIdx.y, lane, reinterpret_cast<float*>(&s_red[wave][0][0]),
+                         OUT == kOutAcc ? y_pre : nullptr);
+}
+
 const char* blas_msg(rocblas_status st) { return rocblas_status_to_string(st); }
 
 }  // namespace
@@ -918,6 +1057,7 @@ struct qasr_decoder {
     bool own_gemm = false;            // QASR_PREFILL_GEMM=own: gemm_f16_kernel for the prefill projections
     int shared_tiles = 3;             // QASR_SKINNY_SHARED: skinny_shared_kernel tiles per workgroup (0 off)
     int shared_min_tiles = 512;       // QASR_SKINNY_SHARED_MIN_TILES: narrower outputs keep skinny_gemm_kernel
+    int multi_tiles = 4;              // QASR_SKINNY_MULTI: skinny_multi_kernel tiles per wave (0 off)
     // activations, max_rows rows each
     f16* x = nullptr;     // residual stream [rows][hs]
     f16* n = nullptr;     // normed rows [rows][hs]
@@ -981,6 +1121,7 @@ struct SkinnyShape {
     int ks = 0, groups = 1;
     int nks = 0, tpw = 1, nbuf = 1;  // nks > 0: skinny_lds_kernel
     int shared_tiles = 0;            // > 1: skinny_shared_kernel, this many tiles per workgroup
+    int multi_tiles = 0, multi_ks = 0;  // > 1: skinny_multi_kernel, tiles per wave and waves
 };
 
 SkinnyShape lds_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8) {
@@ -1045,6 +1186,17 @@ int shared_tiles(qasr_decoder* d, const SkinnyShape& sh, int rows, int n_out, in
 
 SkinnyShape skinny_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8 = false) {
     SkinnyShape sh = skinny_base_shape(d, rows, n_out, k, w8);
+    // Wide outputs of at least kSharedMinRows rows: f16 weights take several
+    // tiles per wave (skinny_multi_kernel), int8 weights the LDS-shared
+    // activation rows (skinny_shared_kernel), whose twelve waves hide the
+    // dequantisation better.  Both keep the base shape's K slices.
+    const bool wide = sh.ks && !sh.nks && rows >= kSharedMinRows && n_out / 16 >= d->shared_min_tiles;
+    const int tw = d->multi_tiles;
+    if (wide && !w8 && tw > 1 && (sh.ks == 4 || sh.ks == 8) && (tw == 2 || tw == 4)) {
+        sh.multi_tiles = tw;
+        sh.multi_ks = sh.ks;
+        return sh;
+    }
     sh.shared_tiles = shared_tiles(d, sh, rows, n_out, k);
     return sh;
 }
@@ -1118,8 +1270,28 @@ int launch_skinny_shared(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
     return QASR_OK;
 }
 
+template <bool W8, int OUT, bool NORM>
+int launch_skinny_multi(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
+    const int tw = sh.multi_tiles, ks = sh.multi_ks;
+    const dim3 grid((a.N / 16 + tw - 1) / tw, sh.groups);
+    constexpr int U = kSkinnyUnroll;
+#define QASR_MULTI(KS_, TW_)                                                                      \
+    else if (ks == KS_ && tw == TW_) hipLaunchKernelGGL((skinny_multi_kernel<KS_, TW_, U, W8, OUT, NORM>), \
+                                                        grid, dim3(KS_ * 64), 0, d->stream, a);
+    if (false) {
+    }
+    QASR_MULTI(4, 2) QASR_MULTI(8, 2) QASR_MULTI(4, 4) QASR_MULTI(8, 4)
+    else return fail(QASR_EINVAL, "skinny GEMM: %d waves x %d tiles per wave", ks, tw);
+#undef QASR_MULTI
+    HIP_TRY(hipGetLastError(), "projection launch");
+    return QASR_OK;
+}
+
 template <int OUT, bool NORM = false>
 int launch_skinny(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
+    if (sh.multi_tiles > 1)
+        return a.scale ? launch_skinny_multi<true, OUT, NORM>(d, sh, a)
+                       : launch_skinny_multi<false, OUT, NORM>(d, sh, a);
     if (sh.shared_tiles > 1)
         return a.scale ? launch_skinny_shared<true, OUT, NORM>(d, sh, a)
                        : launch_skinny_shared<false, OUT, NORM>(d, sh, a);
@@ -1343,6 +1515,8 @@ int bind_stream(qasr_decoder* d, void* stream) {
     d->own_gemm = pg && std::string(pg) == "own";
     const char* sh = std::getenv("QASR_SKINNY_SHARED");
     d->shared_tiles = sh ? std::atoi(sh) : 3;
+    const char* mt = std::getenv("QASR_SKINNY_MULTI");
+    d->multi_tiles = mt ? std::atoi(mt) : 4;
     const char* smt = std::getenv("QASR_SKINNY_SHARED_MIN_TILES");
     d->shared_min_tiles = smt ? std::atoi(smt) : 512;
     const rocblas_status st = rocblas_set_stream(d->blas, (hipStream_t)stream);

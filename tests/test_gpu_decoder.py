@@ -444,22 +444,24 @@ def test_fused_epilogues_equal_unfused(gpu, model, batch, int8, lds, monkeypatch
     assert np.array_equal(out["fused"][1], out["unfused"][1])
 
 
-@pytest.mark.parametrize("tiles", ["2", "3", "4"])
+@pytest.mark.parametrize("variant", ["shared=2", "shared=3", "shared=4", "multi=2", "multi=4"])
 @pytest.mark.parametrize("model,batch,int8", [("1.7B", 16, False), ("1.7B", 8, True),
                                               ("0.6B", 16, True), ("0.6B", 9, False)])
-def test_shared_activation_projections_equal_per_tile(gpu, model, batch, int8, tiles, monkeypatch):
-    """The decode step's projections with the activation rows shared in LDS
-    by several column tiles (QASR_SKINNY_SHARED=tiles: skinny_shared_kernel,
-    the same K slices, summation order and norm rounding as
-    skinny_gemm_kernel) against the per-tile kernel: identical logits and
-    tokens, bitwise -- at both model shapes, f16 and int8, with the folded
-    norms, gate|up with SiLU * up, the residual projections and down_proj's
-    K split across workgroups."""
+def test_wide_projection_variants_equal_per_tile(gpu, model, batch, int8, variant, monkeypatch):
+    """The decode step's projections through the kernels that cut activation
+    reloads -- activation rows shared in LDS by several column tiles
+    (QASR_SKINNY_SHARED, skinny_shared_kernel) or several column tiles per
+    wave (QASR_SKINNY_MULTI, skinny_multi_kernel, f16 weights), both with the
+    per-tile kernel's K slices, summation order and norm rounding -- against
+    the per-tile kernel alone: identical logits and tokens, bitwise -- at both
+    model shapes, f16 and int8, with the folded norms, gate|up with SiLU * up,
+    the residual projections and down_proj's K split across workgroups."""
     import torch
 
     from decoder_model import CFG_1P7B
     from gpu_helpers import say
 
+    knob, value = variant.split("=")
     cfg = dict(CFG_1P7B if model == "1.7B" else CFG_0P6B, layers=3, vocab=8192)
     W = synth_weights(cfg, SEED_BASE + 1300 + batch, device="cuda")
     if int8:
@@ -474,17 +476,19 @@ def test_shared_activation_projections_equal_per_tile(gpu, model, batch, int8, t
     tok = torch.tensor([dec.last[i] for i in range(batch)], dtype=torch.int32, device="cuda")
     out = {}
     monkeypatch.setenv("QASR_SKINNY_SHARED_MIN_TILES", "0")  # every eligible projection, not only the widest
-    for name, shared in (("per_tile", "0"), ("shared", tiles)):
+    for name, shared, multi in (("per_tile", "0", "0"),
+                                (variant, value if knob == "shared" else "0", value if knob == "multi" else "0")):
         monkeypatch.setenv("QASR_SKINNY_SHARED", shared)
+        monkeypatch.setenv("QASR_SKINNY_MULTI", multi)
         nxt = torch.empty(batch, dtype=torch.int32, device="cuda")
         lg = torch.empty((batch, cfg["vocab"]), dtype=torch.float32, device="cuda")
-        say(f"{model} batch {batch} int8={int8}: {name} step (tiles {tiles})")
+        say(f"{model} batch {batch} int8={int8}: {name} step")
         dec.step_tokens(slots, pos, tok, nxt, lg)
         torch.cuda.synchronize()
         out[name] = (nxt.cpu().numpy(), lg.cpu().numpy())
     dec.close()
-    assert np.array_equal(out["shared"][0], out["per_tile"][0])
-    assert np.array_equal(out["shared"][1], out["per_tile"][1])
+    assert np.array_equal(out[variant][0], out["per_tile"][0])
+    assert np.array_equal(out[variant][1], out["per_tile"][1])
 
 
 @pytest.mark.parametrize("model,int8", [("1.7B", False), ("0.6B", True)])
