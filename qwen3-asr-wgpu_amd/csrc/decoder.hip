@@ -1145,9 +1145,9 @@ SkinnyShape lds_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8) {
     return sh;
 }
 
-SkinnyShape skinny_base_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8) {
+SkinnyShape skinny_base_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8, bool allow_lds) {
     if (d->force_blas || rows > kSkinnyRows || n_out % 16) return SkinnyShape{};
-    if (d->lds_gemm) {
+    if (d->lds_gemm && allow_lds) {
         const SkinnyShape sh = lds_shape(d, rows, n_out, k, w8);
         if (sh.nks) return sh;
     }
@@ -1185,13 +1185,16 @@ int shared_tiles(qasr_decoder* d, const SkinnyShape& sh, int rows, int n_out, in
 }
 
 SkinnyShape skinny_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8 = false) {
-    SkinnyShape sh = skinny_base_shape(d, rows, n_out, k, w8);
     // Wide outputs of at least kSharedMinRows rows: f16 weights take several
-    // tiles per wave (skinny_multi_kernel), int8 weights the LDS-shared
+    // tiles per wave (skinny_multi_kernel; the logits too, 1889 against 1897
+    // us per 16-slot step with skinny_lds_kernel), int8 weights the LDS-shared
     // activation rows (skinny_shared_kernel), whose twelve waves hide the
     // dequantisation better.  Both keep the base shape's K slices.
-    const bool wide = sh.ks && !sh.nks && rows >= kSharedMinRows && n_out / 16 >= d->shared_min_tiles;
     const int tw = d->multi_tiles;
+    const bool multi_ok = !w8 && tw > 1 && rows >= kSharedMinRows && n_out / 16 >= d->shared_min_tiles &&
+                          d->lds_gemm < 2;
+    SkinnyShape sh = skinny_base_shape(d, rows, n_out, k, w8, !multi_ok);
+    const bool wide = sh.ks && !sh.nks && rows >= kSharedMinRows && n_out / 16 >= d->shared_min_tiles;
     if (wide && !w8 && tw > 1 && (sh.ks == 4 || sh.ks == 8) && (tw == 2 || tw == 4)) {
         sh.multi_tiles = tw;
         sh.multi_ks = sh.ks;
