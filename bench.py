@@ -757,13 +757,6 @@ def main():
         extra["config5_decode"] = bench_decode(64, lens5, max(5, K // 5), W)
         log("[bench] 16 slots at a uniform 2048-token context (the target's ~2k context)")
         extra["decode_16slots_2k_context"] = bench_decode(16, [2048] * 16, K, W)
-        log("[bench] streaming-read calibration at config 3's bytes per launch")
-        extra["streamread_config3_bytes"] = stream_read_calibration(
-            decode_bytes([L + 1 for L in lens3]), K, W)
-        log("[bench] what one CU streams (few workgroups)")
-        extra["stream_per_cu"] = stream_per_cu_calibration(max(5, K // 5), 2)
-        log("[bench] matrix-core calibration")
-        extra["mfma_calibration"] = mfma_calibration()
         log("[bench] text decoder steps (whole decoder around the attention path)")
         extra["text_decoder_1p7b_16slots"] = bench_text_decoder("1.7B", lens3, K, W)
         extra["text_decoder_0p6b_1slot"] = bench_text_decoder("0.6B", [511], K, W)
@@ -776,6 +769,15 @@ def main():
         extra["decoder_prefill_batch_1p7b_16prompts"] = bench_prefill_batch("1.7B", 16, max(3, K // 10), 1)
         log("[bench] batch job through the slot scheduler (32 segments, width 16 vs 1)")
         extra["serving_1p7b_32seg_width16"] = bench_serving("1.7B", 32, 16, 48)
+        # Calibrations last: the matrix-core probe's long dense launches can
+        # leave the clocks lower for whatever runs right after them.
+        log("[bench] streaming-read calibration at config 3's bytes per launch")
+        extra["streamread_config3_bytes"] = stream_read_calibration(
+            decode_bytes([L + 1 for L in lens3]), K, W)
+        log("[bench] what one CU streams (few workgroups)")
+        extra["stream_per_cu"] = stream_per_cu_calibration(max(5, K // 5), 2)
+        log("[bench] matrix-core calibration")
+        extra["mfma_calibration"] = mfma_calibration()
         for k, v in extra.items():
             log(f"[bench] {k}: {json.dumps(v)}")
 
