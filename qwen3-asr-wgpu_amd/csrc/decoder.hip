@@ -1057,7 +1057,7 @@ struct qasr_decoder {
     bool own_gemm = false;            // QASR_PREFILL_GEMM=own: gemm_f16_kernel for the prefill projections
     int shared_tiles = 3;             // QASR_SKINNY_SHARED: skinny_shared_kernel tiles per workgroup (0 off)
     int shared_min_tiles = 512;       // QASR_SKINNY_SHARED_MIN_TILES: narrower outputs keep skinny_gemm_kernel
-    int multi_tiles = 4;              // QASR_SKINNY_MULTI: skinny_multi_kernel tiles per wave (0 off)
+    int multi_tiles = -1;             // QASR_SKINNY_MULTI: skinny_multi_kernel tiles per wave (0 off, -1 by width)
     // activations, max_rows rows each
     f16* x = nullptr;     // residual stream [rows][hs]
     f16* n = nullptr;     // normed rows [rows][hs]
@@ -1189,13 +1189,18 @@ SkinnyShape skinny_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8 = 
     // tiles per wave (skinny_multi_kernel; the logits too, 1889 against 1897
     // us per 16-slot step with skinny_lds_kernel), int8 weights the LDS-shared
     // activation rows (skinny_shared_kernel), whose twelve waves hide the
-    // dequantisation better.  Both keep the base shape's K slices.
-    const int tw = d->multi_tiles;
+    // dequantisation better.  Both keep the base shape's K slices.  Tiles per
+    // wave: the fewest (two to four) that need no more than one workgroup per
+    // CU -- the 1.7B gate|up's 768 tiles take three (256 workgroups: 14.1 us
+    // against 15.6 with four on 192), the logits' 9,496 four (126.9 against
+    // 130.5 us with three).  QASR_SKINNY_MULTI=T forces T (0: off).
+    const int tiles = n_out / 16, cus = std::max(d->ctx->cus, 1);
+    const int tw = d->multi_tiles < 0 ? std::min(4, std::max(2, (tiles + cus - 1) / cus)) : d->multi_tiles;
     const bool multi_ok = !w8 && tw > 1 && rows >= kSharedMinRows && n_out / 16 >= d->shared_min_tiles &&
                           d->lds_gemm < 2;
     SkinnyShape sh = skinny_base_shape(d, rows, n_out, k, w8, !multi_ok);
     const bool wide = sh.ks && !sh.nks && rows >= kSharedMinRows && n_out / 16 >= d->shared_min_tiles;
-    if (wide && !w8 && tw > 1 && (sh.ks == 4 || sh.ks == 8) && (tw == 2 || tw == 4)) {
+    if (wide && !w8 && tw > 1 && (sh.ks == 4 || sh.ks == 8) && (tw >= 2 && tw <= 4)) {
         sh.multi_tiles = tw;
         sh.multi_ks = sh.ks;
         return sh;
@@ -1283,7 +1288,7 @@ int launch_skinny_multi(qasr_decoder* d, SkinnyShape sh, const SkinnyArgs& a) {
                                                         grid, dim3(KS_ * 64), 0, d->stream, a);
     if (false) {
     }
-    QASR_MULTI(4, 2) QASR_MULTI(8, 2) QASR_MULTI(4, 4) QASR_MULTI(8, 4)
+    QASR_MULTI(4, 2) QASR_MULTI(8, 2) QASR_MULTI(4, 3) QASR_MULTI(8, 3) QASR_MULTI(4, 4) QASR_MULTI(8, 4)
     else return fail(QASR_EINVAL, "skinny GEMM: %d waves x %d tiles per wave", ks, tw);
 #undef QASR_MULTI
     HIP_TRY(hipGetLastError(), "projection launch");
@@ -1519,7 +1524,7 @@ int bind_stream(qasr_decoder* d, void* stream) {
     const char* sh = std::getenv("QASR_SKINNY_SHARED");
     d->shared_tiles = sh ? std::atoi(sh) : 3;
     const char* mt = std::getenv("QASR_SKINNY_MULTI");
-    d->multi_tiles = mt ? std::atoi(mt) : 4;
+    d->multi_tiles = mt ? std::atoi(mt) : -1;
     const char* smt = std::getenv("QASR_SKINNY_SHARED_MIN_TILES");
     d->shared_min_tiles = smt ? std::atoi(smt) : 512;
     const rocblas_status st = rocblas_set_stream(d->blas, (hipStream_t)stream);

@@ -444,7 +444,7 @@ def test_fused_epilogues_equal_unfused(gpu, model, batch, int8, lds, monkeypatch
     assert np.array_equal(out["fused"][1], out["unfused"][1])
 
 
-@pytest.mark.parametrize("variant", ["shared=2", "shared=3", "shared=4", "multi=2", "multi=4"])
+@pytest.mark.parametrize("variant", ["shared=2", "shared=3", "shared=4", "multi=2", "multi=3", "multi=4"])
 @pytest.mark.parametrize("model,batch,int8", [("1.7B", 16, False), ("1.7B", 8, True),
                                               ("0.6B", 16, True), ("0.6B", 9, False)])
 def test_wide_projection_variants_equal_per_tile(gpu, model, batch, int8, variant, monkeypatch):
