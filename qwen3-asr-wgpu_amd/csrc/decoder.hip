@@ -268,6 +268,55 @@ __global__ __launch_bounds__(64) void argmax_final_kernel(const float* __restric
     if (lane == 0) out[row] = bi < vocab ? bi : 0;
 }
 
+// The argmax over the skinny logits kernel's per-tile candidates (one
+// workgroup per row): the same (value, index) order, so the same token as the
+// two passes over the logits.
+constexpr int kArgTilesThreads = 1024;
+constexpr int kArgTilesUnroll = 10;  // 10,240 candidates per round: the 151,936-entry vocabulary's 9,496 tiles
+__global__ __launch_bounds__(kArgTilesThreads) void argmax_tiles_kernel(const float* __restrict__ pv,
+                                                                        const int* __restrict__ pi,
+                                                                        int ntiles, int vocab,
+                                                                        int32_t* __restrict__ out) {
+    __shared__ float s_v[kArgTilesThreads / 64];
+    __shared__ int s_i[kArgTilesThreads / 64];
+    const int row = blockIdx.x;
+    const float* rv = pv + (int64_t)row * ntiles;
+    const int* ri = pi + (int64_t)row * ntiles;
+    float bv = -__builtin_inff();
+    int bi = vocab;
+    for (int base = 0; base < ntiles; base += kArgTilesThreads * kArgTilesUnroll) {
+        // Every load of the round is issued before the first compare.
+        float v[kArgTilesUnroll];
+        int ix[kArgTilesUnroll];
+#pragma unroll
+        for (int u = 0; u < kArgTilesUnroll; ++u) {
+            const int t = base + u * kArgTilesThreads + (int)threadIdx.x;
+            v[u] = t < ntiles ? rv[t] : -__builtin_inff();
+            ix[u] = t < ntiles ? ri[t] : vocab;
+        }
+#pragma unroll
+        for (int u = 0; u < kArgTilesUnroll; ++u)
+            if (better(v[u], ix[u], bv, bi)) {
+                bv = v[u];
+                bi = ix[u];
+            }
+    }
+    wave_argmax(bv, bi);
+    if ((threadIdx.x & 63) == 0) {
+        s_v[threadIdx.x >> 6] = bv;
+        s_i[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kArgTilesThreads / 64; ++w)
+            if (better(s_v[w], s_i[w], bv, bi)) {
+                bv = s_v[w];
+                bi = s_i[w];
+            }
+        out[row] = bi < vocab ? bi : 0;
+    }
+}
+
 // ---- skinny GEMM: the projections of a decode step ----------------------
 // Y[m][n] = X[m][k] . W[n][k]^T over at most 16 activation rows: a weight
 // stream, HBM-bound, so each weight byte is read once and fed to
@@ -348,7 +397,7 @@ struct SkinnyArgs {
     const void* W;        // [N][K] f16, or int8 when `scale` is set
     const float* scale;   // int8 weights: [N] per-row scales
     const f16* X;  // [M][K]
-    void* Y;       // [M][N] f16, or f32 logits
+    void* Y;       // [M][N] f16, or f32 logits (null: am_v / am_i only)
     int M, N, K, groups;
     float* ws;           // split partials
     uint32_t* counters;  // split tickets
@@ -356,6 +405,8 @@ struct SkinnyArgs {
     float eps;
     const float* ss_in;  // fused RMSNorm: X's chunk sums of squares [kSkinnyRows][kNormMaxChunks]
     float* ss_out;       // kOutAcc: write the result rows' chunk sums there (or null)
+    float* am_v;         // kOutF32: each row's best (value, index) per column tile,
+    int* am_i;           //   [M][N / 16], for argmax_tiles_kernel (or null)
 };
 
 // Fused RMSNorm prologue, in two halves so that its loads are issued ahead
@@ -461,13 +512,43 @@ __device__ __forceinline__ void skinny_tile_out(const SkinnyArgs& p, qasr::float
         if (m >= M) continue;
         const int64_t idx = (int64_t)m * N + n;
         if constexpr (OUT == kOutF32) {
-            ((float*)p.Y)[idx] = sum[i];
+            if (p.Y) ((float*)p.Y)[idx] = sum[i];  // null: only the argmax candidates
         } else {
             f16* y = (f16*)p.Y;
             const f16 yv = OUT == kOutAcc ? (y_pre ? y_pre[i] : y[idx]) : (f16)0.0f;
             const f16 out = (f16)(OUT == kOutAcc ? (float)yv + sum[i] : sum[i]);
             y[idx] = out;
             if constexpr (OUT == kOutAcc) sum[i] = (float)out;  // for the chunk sums below
+        }
+    }
+    if constexpr (OUT == kOutF32) {
+        if (p.am_v) {
+            // This tile's best (value, index) of each row, the argmax's first
+            // pass without re-reading the logits: the 16 lanes of a row group
+            // hold its 16 columns.  A NaN never becomes a candidate.
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float bv = -__builtin_inff();
+                int bi = N;
+                if (better(sum[i], n, bv, bi)) {
+                    bv = sum[i];
+                    bi = n;
+                }
+#pragma unroll
+                for (int msk = 8; msk >= 1; msk >>= 1) {
+                    const float ov = __shfl_xor(bv, msk);
+                    const int oi = __shfl_xor(bi, msk);
+                    if (better(ov, oi, bv, bi)) {
+                        bv = ov;
+                        bi = oi;
+                    }
+                }
+                const int m = 4 * g + i;
+                if (r == 0 && m < M) {
+                    p.am_v[(int64_t)m * (N / 16) + tile] = bv;
+                    p.am_i[(int64_t)m * (N / 16) + tile] = bi;
+                }
+            }
         }
     }
     if constexpr (OUT == kOutAcc) {
@@ -1057,6 +1138,7 @@ struct qasr_decoder {
     bool own_gemm = false;            // QASR_PREFILL_GEMM=own: gemm_f16_kernel for the prefill projections
     int shared_tiles = 3;             // QASR_SKINNY_SHARED: skinny_shared_kernel tiles per workgroup (0 off)
     int shared_min_tiles = 512;       // QASR_SKINNY_SHARED_MIN_TILES: narrower outputs keep skinny_gemm_kernel
+    bool argmax_tiles = true;         // QASR_ARGMAX_TILES=0: the two-pass argmax over the logits
     int multi_tiles = -1;             // QASR_SKINNY_MULTI: skinny_multi_kernel tiles per wave (0 off, -1 by width)
     // activations, max_rows rows each
     f16* x = nullptr;     // residual stream [rows][hs]
@@ -1067,7 +1149,7 @@ struct qasr_decoder {
     f16* gu = nullptr;    // [rows][2 inter]
     f16* h = nullptr;     // [rows][inter]
     float* logits = nullptr;  // [kHeadRows][vocab]
-    float* am_v = nullptr;    // argmax candidates [kHeadRows][kArgmaxChunks]
+    float* am_v = nullptr;    // argmax candidates [kHeadRows][kArgmaxChunks] or [kSkinnyRows][vocab / 16]
     int* am_i = nullptr;
     // split projections: partials [tile][group][64 lanes][4] and one arrival
     // ticket per column tile (zero at rest: the last arrival resets it)
@@ -1418,18 +1500,29 @@ int normed_proj(qasr_decoder* d, int rows, int n_out, const void* W, const f16* 
 
 // logits[rows][vocab] (f32) = n[rows][hs] . E[vocab][hs]^T; with nw set,
 // `nrows` are raw rows normed by gain nw first (in the kernel's prologue).
-int gemm_logits(qasr_decoder* d, int rows, const f16* nrows, float* out, const void* nw = nullptr) {
+// *tile_cands is set when the skinny kernel also left each row's best
+// (value, index) per column tile in am_v / am_i (argmax_tiles_kernel's input).
+int gemm_logits(qasr_decoder* d, int rows, const f16* nrows, float* out, bool* tile_cands,
+                const void* nw = nullptr) {
     const int hs = d->cfg.hidden_size, vocab = d->cfg.vocab_size;
     const SkinnyShape sh = skinny_shape(d, rows, vocab, hs);
-    if (nw) {
-        if (!norm_fusable(d, sh, hs, nrows))
-            return fail(QASR_EINVAL, "logits with a fused norm: not a skinny shape");
-        return launch_skinny<kOutF32, true>(
-            d, sh, with_norm(d, skinny_args(d, sh, rows, vocab, hs, d->embed, nrows, out), nw));
+    *tile_cands = false;
+    if (sh.ks || sh.nks) {
+        SkinnyArgs a = skinny_args(d, sh, rows, vocab, hs, d->embed, nrows, out);
+        if (d->argmax_tiles && rows <= kSkinnyRows && vocab % 16 == 0) {
+            a.am_v = d->am_v;
+            a.am_i = d->am_i;
+            *tile_cands = true;
+            if (out == d->logits) a.Y = nullptr;  // no caller reads the scratch logits
+        }
+        if (nw) {
+            if (!norm_fusable(d, sh, hs, nrows))
+                return fail(QASR_EINVAL, "logits with a fused norm: not a skinny shape");
+            return launch_skinny<kOutF32, true>(d, sh, with_norm(d, a, nw));
+        }
+        return launch_skinny<kOutF32>(d, sh, a);
     }
-    if (sh.ks || sh.nks)
-        return launch_skinny<kOutF32>(
-            d, sh, skinny_args(d, sh, rows, vocab, hs, d->embed, nrows, out));
+    if (nw) return fail(QASR_EINVAL, "logits with a fused norm: not a skinny shape");
     const float alpha = 1.0f, beta = 0.0f;
     const rocblas_status st = rocblas_gemm_ex(
         d->blas, rocblas_operation_transpose, rocblas_operation_none, vocab, rows, hs, &alpha,
@@ -1488,15 +1581,22 @@ int head(qasr_decoder* d, const f16* x_rows, int rows, int32_t* next_dev, float*
         const int nr = std::min(kHeadRows, rows - r0);
         float* lg = logits_dev ? logits_dev + (int64_t)r0 * vocab : d->logits;
         int rc;
+        bool tile_cands = false;
         if (r0 == 0 && norm_fusable(d, skinny_shape(d, nr, vocab, hs), hs, x_rows)) {
-            rc = gemm_logits(d, nr, x_rows + (int64_t)r0 * hs, lg, d->final_norm);  // norm folded
+            rc = gemm_logits(d, nr, x_rows + (int64_t)r0 * hs, lg, &tile_cands, d->final_norm);  // norm folded
         } else {
             rc = launch_rms_norm(x_rows + (int64_t)r0 * hs, hs, d->final_norm, d->n, nr, hs,
                                  d->ctx->cfg.rms_norm_eps, st);
             if (rc) return rc;
-            rc = gemm_logits(d, nr, d->n, lg);
+            rc = gemm_logits(d, nr, d->n, lg, &tile_cands);
         }
         if (rc) return rc;
+        if (tile_cands) {
+            hipLaunchKernelGGL(argmax_tiles_kernel, dim3(nr), dim3(kArgTilesThreads), 0, st, d->am_v,
+                               d->am_i, vocab / 16, vocab, next_dev + r0);
+            HIP_TRY(hipGetLastError(), "argmax launch");
+            continue;
+        }
         hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgmaxChunks, nr), dim3(kArgmaxThreads), 0,
                            st, lg, vocab, d->am_v, d->am_i);
         HIP_TRY(hipGetLastError(), "argmax launch");
@@ -1525,6 +1625,8 @@ int bind_stream(qasr_decoder* d, void* stream) {
     d->shared_tiles = sh ? std::atoi(sh) : 3;
     const char* mt = std::getenv("QASR_SKINNY_MULTI");
     d->multi_tiles = mt ? std::atoi(mt) : -1;
+    const char* at = std::getenv("QASR_ARGMAX_TILES");
+    d->argmax_tiles = !(at && *at == '0');
     const char* smt = std::getenv("QASR_SKINNY_SHARED_MIN_TILES");
     d->shared_min_tiles = smt ? std::atoi(smt) : 512;
     const rocblas_status st = rocblas_set_stream(d->blas, (hipStream_t)stream);
@@ -1647,6 +1749,8 @@ int qasr_decoder_create(qasr_ctx* ctx, const qasr_decoder_cfg* cfg, const void* 
     const size_t R = (size_t)cfg->max_rows;
     const size_t qdim = (size_t)a.num_attention_heads * a.head_dim;
     const size_t qkvdim = qdim + 2 * (size_t)a.num_key_value_heads * a.head_dim;
+    // argmax candidates: the two-pass argmax's, or per column tile of the logits
+    const size_t am_bytes = std::max((size_t)kHeadRows * kArgmaxChunks, (size_t)kSkinnyRows * (vocab / 16)) * 4;
     struct Alloc {
         void** p;
         size_t bytes;
@@ -1656,8 +1760,8 @@ int qasr_decoder_create(qasr_ctx* ctx, const qasr_decoder_cfg* cfg, const void* 
         {(void**)&d->attn, R * qdim * 2},     {(void**)&d->gu, R * 2 * (size_t)inter * 2},
         {(void**)&d->h, R * (size_t)inter * 2},
         {(void**)&d->logits, (size_t)kHeadRows * vocab * 4},
-        {(void**)&d->am_v, (size_t)kHeadRows * kArgmaxChunks * 4},
-        {(void**)&d->am_i, (size_t)kHeadRows * kArgmaxChunks * 4},
+        {(void**)&d->am_v, am_bytes},
+        {(void**)&d->am_i, am_bytes},
         {&d->blas_ws, kBlasWorkspace},
         {(void**)&d->sk_ws, (size_t)kSkinnyMaxTiles * kSkinnyMaxGroups * 1024},
         {(void**)&d->sk_ctr, (size_t)kSkinnyMaxTiles * 4},

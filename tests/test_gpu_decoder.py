@@ -444,6 +444,52 @@ def test_fused_epilogues_equal_unfused(gpu, model, batch, int8, lds, monkeypatch
     assert np.array_equal(out["fused"][1], out["unfused"][1])
 
 
+@pytest.mark.parametrize("model,batch", [("1.7B", 16), ("0.6B", 1), ("0.6B", 9), ("1.7B", 3)])
+def test_argmax_from_logits_tiles_equals_two_pass(gpu, model, batch, monkeypatch):
+    """The greedy token from the logits kernel's per-tile candidates
+    (argmax_tiles_kernel) against the two passes over the f32 logits
+    (QASR_ARGMAX_TILES=0) and numpy's first maximal index, with ties planted:
+    the tied embedding repeats 256 distinct rows in adjacent pairs and every
+    512 columns, so each logit value occurs 32 times, inside a 16-column tile
+    and across tiles.  The smaller index must win, as the reference's
+    `if v > logits[best]` loop keeps the first maximum.  Also without logits
+    requested (the scratch logits are then not written)."""
+    import torch
+
+    from decoder_model import CFG_1P7B
+    from gpu_helpers import say
+
+    cfg = dict(CFG_1P7B if model == "1.7B" else CFG_0P6B, layers=2, vocab=8192)
+    W = synth_weights(cfg, SEED_BASE + 1300 + batch, device="cuda")
+    base = W["embed"][:256].clone()
+    idx = torch.arange(cfg["vocab"], device="cuda")
+    W["embed"] = base[(idx % 512) // 2].contiguous()
+    dec = _native(cfg, W, batch, 1024, max_rows=16)
+    for i in range(batch):
+        dec.prefill(_prompt(SEED_BASE + 1310 + i, 7 + 2 * i, cfg["hs"]), 0, slot=i)
+    slots, pos = list(range(batch)), [dec.pos[i] for i in range(batch)]
+    tok = torch.tensor([dec.last[i] for i in range(batch)], dtype=torch.int32, device="cuda")
+    out = {}
+    for name, tiles, want_logits in (("tiles", "1", True), ("tiles, no logits", "1", False),
+                                     ("two-pass", "0", True)):
+        monkeypatch.setenv("QASR_ARGMAX_TILES", tiles)
+        nxt = torch.empty(batch, dtype=torch.int32, device="cuda")
+        lg = torch.empty((batch, cfg["vocab"]), dtype=torch.float32, device="cuda") if want_logits else None
+        say(f"{model} batch {batch}: {name}")
+        dec.step_tokens(slots, pos, tok, nxt, lg)
+        torch.cuda.synchronize()
+        out[name] = (nxt.cpu().numpy(), lg.cpu().numpy() if want_logits else None)
+    dec.close()
+    logits = out["two-pass"][1]
+    first_max = np.argmax(logits, axis=1).astype(np.int32)
+    # the planted ties: the first copy of each value (an even index below 512) wins
+    assert (first_max < 512).all() and (first_max % 2 == 0).all()
+    assert np.array_equal(out["two-pass"][0], first_max)
+    assert np.array_equal(out["tiles"][0], first_max)
+    assert np.array_equal(out["tiles, no logits"][0], first_max)
+    assert np.array_equal(out["tiles"][1], logits)
+
+
 @pytest.mark.parametrize("variant", ["shared=2", "shared=3", "shared=4", "multi=2", "multi=3", "multi=4"])
 @pytest.mark.parametrize("model,batch,int8", [("1.7B", 16, False), ("1.7B", 8, True),
                                               ("0.6B", 16, True), ("0.6B", 9, False)])
