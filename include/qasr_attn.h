@@ -58,7 +58,7 @@ typedef struct qasr_attn_cfg {
     int32_t head_dim;            /* 128 */
     int32_t num_hidden_layers;   /* 28 */
     float rms_norm_eps;          /* 1e-6 */
-    int32_t max_seq;             /* ceiling on positions (DECODER_MAX_SEQ) */
+    int32_t max_seq;             /* ceiling on positions (DECODER_MAX_SEQ); 1 .. 1 << 24 */
 } qasr_attn_cfg;
 
 typedef struct qasr_ctx qasr_ctx;
@@ -345,7 +345,8 @@ int qasr_mfma_probe(qasr_ctx* ctx, int mode, int wgs, int waves, int mfma_iters,
  * units; the QASR_DECODE_WGS / _MIN_CHUNK / _MAX_SPLIT environment knobs
  * apply.  chunk_out[b]: keys per workgroup of entry b (a multiple of 32);
  * wg_base_out[0..batch]: entry b's workgroups are wg_base_out[b] ..
- * wg_base_out[b+1]-1 (nkvh * ceil(lens[b] / chunk_out[b]) of them). */
+ * wg_base_out[b+1]-1 (nkvh * ceil(lens[b] / chunk_out[b]) of them).
+ * lens[b] in [1, 1 << 24]. */
 int qasr_plan_decode(int batch, const int32_t* lens, int nkvh, int cus, int32_t* chunk_out,
                      int32_t* wg_base_out);
 
@@ -354,7 +355,7 @@ int qasr_plan_decode(int batch, const int32_t* lens, int nkvh, int cus, int32_t*
  * blocks, *tiles_per_split 128-key tiles per split (QASR_PREFILL_TPS
  * applies), sp_base_out[0..nrb]: row block rb's items are sp_base_out[rb] ..
  * sp_base_out[rb+1]-1 within each kv head (sp_base_out[nrb] items per kv
- * head; at most 65 entries written). */
+ * head; at most 65 entries written).  kv_start in [0, 1 << 24]. */
 int qasr_plan_prefill(int rows, int kv_start, int nkvh, int32_t* rows_per_block, int32_t* nrb,
                       int32_t* tiles_per_split, int32_t* sp_base_out);
 

@@ -60,6 +60,11 @@ uint16_t f16_bits(float f) {
     return (uint16_t)(sign | h);
 }
 
+// Positions a context may address (max_seq) and the planners accept: far
+// past any KV pool that fits a GPU, small enough that no position, key or
+// tile count of a plan overflows 32 bits.
+constexpr int kMaxPositions = 1 << 24;
+
 int env_int(const char* name, int dflt) {
     const char* v = std::getenv(name);
     if (!v || !*v) return dflt;
@@ -432,7 +437,8 @@ int qasr_ctx_create(const qasr_attn_cfg* cfg, int device, qasr_ctx** out) {
         return fail(QASR_EINVAL, "too many heads (%d + %d)", c.num_attention_heads,
                     c.num_key_value_heads);
     if (c.num_hidden_layers <= 0) return fail(QASR_EINVAL, "num_hidden_layers must be > 0");
-    if (c.max_seq <= 0) return fail(QASR_EINVAL, "max_seq must be > 0");
+    if (c.max_seq <= 0 || c.max_seq > kMaxPositions)
+        return fail(QASR_EINVAL, "max_seq %d outside [1, %d]", c.max_seq, kMaxPositions);
     if (!(c.rms_norm_eps >= 0.0f) || !std::isfinite(c.rms_norm_eps))
         return fail(QASR_EINVAL, "rms_norm_eps must be finite and >= 0");
     int ndev = 0;
@@ -862,7 +868,8 @@ int qasr_plan_decode(int batch, const int32_t* lens, int nkvh, int cus, int32_t*
     qasr::DecodePlan P{};
     P.batch = batch;
     for (int b = 0; b < batch; ++b) {
-        if (lens[b] < 1) return fail(QASR_EINVAL, "entry %d attends %d keys", b, lens[b]);
+        if (lens[b] < 1 || lens[b] > kMaxPositions)
+            return fail(QASR_EINVAL, "entry %d attends %d keys (at most %d)", b, lens[b], kMaxPositions);
         P.len[b] = lens[b];
     }
     plan_decode_chunks(P, nkvh, cus);
@@ -875,7 +882,8 @@ int qasr_plan_prefill(int rows, int kv_start, int nkvh, int32_t* rows_per_block,
                       int32_t* tiles_per_split, int32_t* sp_base_out) {
     if (rows < 1 || rows > qasr::kMaxRowBlocks * qasr::kPrefillRows)
         return fail(QASR_EINVAL, "rows %d outside [1, %d]", rows, qasr::kMaxRowBlocks * qasr::kPrefillRows);
-    if (kv_start < 0 || nkvh < 1 || nkvh > 64) return fail(QASR_EINVAL, "kv_start %d / nkvh %d", kv_start, nkvh);
+    if (kv_start < 0 || kv_start > kMaxPositions || nkvh < 1 || nkvh > 64)
+        return fail(QASR_EINVAL, "kv_start %d / nkvh %d", kv_start, nkvh);
     if (!rows_per_block || !nrb || !tiles_per_split || !sp_base_out) return fail(QASR_EINVAL, "null pointer");
     const qasr::PrefillPlan P = choose_prefill_plan(rows, kv_start, nkvh, env_int("QASR_PREFILL_TPS", 0));
     *rows_per_block = P.rows_per_block;

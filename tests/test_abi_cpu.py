@@ -62,7 +62,8 @@ def test_ctx_create_rejects_bad_shapes():
     for cfg in (qasr_attn.AttnCfg(16, 8, 64, 28, 1e-6, 16384),   # head_dim
                 qasr_attn.AttnCfg(16, 16, 128, 28, 1e-6, 16384),  # REP 1
                 qasr_attn.AttnCfg(16, 8, 128, 0, 1e-6, 16384),    # layers
-                qasr_attn.AttnCfg(16, 8, 128, 28, 1e-6, 0)):      # max_seq
+                qasr_attn.AttnCfg(16, 8, 128, 28, 1e-6, 0),       # max_seq
+                qasr_attn.AttnCfg(16, 8, 128, 28, 1e-6, (1 << 24) + 1)):  # max_seq past 2^24
         rc = lib.qasr_ctx_create(ctypes.byref(cfg), 0, ctypes.byref(h))
         assert rc == qasr_attn.QASR_EINVAL
         assert lib.qasr_last_error()
