@@ -340,6 +340,7 @@ __global__ __launch_bounds__(kArgTilesThreads) void argmax_tiles_kernel(const fl
 // gate|up rows.
 constexpr int kOutF16 = 0, kOutAcc = 1, kOutF32 = 2, kOutGlu = 3;
 constexpr int kSkinnyRows = 16;
+constexpr int kSharedMinRows = 8;  // fewer rows: their loads are mostly out of range, nothing to share
 // Fused RMSNorm in front of a skinny projection: hidden sizes up to 8 x this
 // (one 8-element chunk per thread of rms_norm_kernel's 256).
 constexpr int kNormMaxChunks = 256;
@@ -675,9 +676,15 @@ __global__ __launch_bounds__(KS * 64) void skinny_gemm_kernel(SkinnyArgs p) {
                 if (4 * g + i < M) y_pre[i] = ((const f16*)p.Y)[(int64_t)(4 * g + i) * N + n0 + r];
         }
     }
+    // With 8 or more rows the second stage is requested after the folded
+    // norm's inputs have arrived: requested together, they queued behind the
+    // weight stages (16-slot step 1838 -> 1813 us).  One row keeps both
+    // stages first (0.6B one-slot step 964 against 967 us).
+    const bool norm_first = NORM && M >= kSharedMinRows;
     load_stage(0, s0);
+    if (norm_first) inv = np.finish(p, s_gain, s_part, wave, lane, r);
     load_stage(1, s1);
-    if constexpr (NORM) inv = np.finish(p, s_gain, s_part, wave, lane, r);
+    if (NORM && !norm_first) inv = np.finish(p, s_gain, s_part, wave, lane, r);
     int st = 0;
     for (; st + 2 < nst; st += 2) {
         __builtin_amdgcn_sched_barrier(0);
@@ -843,7 +850,6 @@ __global__ __launch_bounds__(kLdsWaves * 64) void skinny_lds_kernel(SkinnyArgs p
 // different bank groups.  The results equal skinny_gemm_kernel's bit for bit.
 constexpr int kSharedMaxK = 3072;  // K per workgroup (the K range of one group)
 constexpr int kSharedPad = 8;      // halves of padding per activation row
-constexpr int kSharedMinRows = 8;  // fewer rows: their loads are mostly out of range, nothing to share
 
 template <int KS, int TPW, int KMAX, bool W8, int OUT, bool NORM>
 __global__ __launch_bounds__(KS * TPW * 64) void skinny_shared_kernel(SkinnyArgs p) {
@@ -905,22 +911,34 @@ __global__ __launch_bounds__(KS * TPW * 64) void skinny_shared_kernel(SkinnyArgs
     }
     NormPrologue<NW> np;
     if constexpr (NORM) np.issue(p, wave, lane);
-    Stage s0, s1;
-    load_stage(0, s0);
-    load_stage(1, s1);
     // The workgroup's activation rows: piece q = threadIdx.x + i NT is row
     // q % 16 (= r, this lane's row: NT is a multiple of 16), chunk q / 16 of 8
     // values; rows past M read as zeros.  Up to 8 pieces per thread and round.
+    // The first round is requested before the weight stages and the second
+    // stage after the rows are staged: requests return in order, so rows
+    // requested behind both stages would wait for them.
     const int nchunk = kg / 8, npieces = kSkinnyRows * nchunk;
-    float inv = 0.0f;
-    if constexpr (NORM) inv = np.finish(p, s_gain, s_part, wave, lane, r);
-    for (int base = 0; base < npieces; base += 8 * NT) {
-        uint4 x[8];
+    auto load_pieces = [&](int base, uint4 (&x)[8]) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int q = base + threadIdx.x + i * NT, c = q >> 4;
             x[i] = (q < npieces && r < M) ? *(const uint4*)(p.X + (int64_t)r * K + kbase + 8 * c)
                                           : make_uint4(0, 0, 0, 0);
+        }
+    };
+    uint4 x0[8];
+    load_pieces(0, x0);
+    Stage s0, s1;
+    load_stage(0, s0);
+    float inv = 0.0f;
+    if constexpr (NORM) inv = np.finish(p, s_gain, s_part, wave, lane, r);
+    for (int base = 0; base < npieces; base += 8 * NT) {
+        uint4 x[8];
+        if (base == 0) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = x0[i];
+        } else {
+            load_pieces(base, x);
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -936,6 +954,7 @@ __global__ __launch_bounds__(KS * TPW * 64) void skinny_shared_kernel(SkinnyArgs
             *(uint4*)&s_act[r * AROW + 8 * c] = v.u;
         }
     }
+    load_stage(1, s1);
     __syncthreads();
 
     qasr::float4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1089,9 +1108,11 @@ __global__ __launch_bounds__(KS * 64) void skinny_multi_kernel(SkinnyArgs p) {
     Stage s0, s1;
     NormPrologue<KS> np;
     if constexpr (NORM) np.issue(p, wave, lane);
+    // The second stage is requested after the folded norm's inputs have
+    // arrived: requested together, they queued behind the weight stages.
     load_stage(0, s0);
-    load_stage(1, s1);
     if constexpr (NORM) inv = np.finish(p, s_gain, s_part, wave, lane, r);
+    load_stage(1, s1);
     int st = 0;
     for (; st + 2 < nst; st += 2) {
         __builtin_amdgcn_sched_barrier(0);
