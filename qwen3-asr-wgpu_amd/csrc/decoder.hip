@@ -353,7 +353,8 @@ constexpr int kSc1 = 16;              // buffer cache policy: device-coherent (s
 constexpr int kSkinnyMaxTiles = 512;  // column tiles of a split (groups > 1) projection
 constexpr int kSkinnyMaxGroups = 12;
 constexpr int kSkinnyTargetWgs = 512;
-constexpr int kSkinnySplitWgs = 256;  // a split projection: one workgroup per CU
+constexpr int kSkinnySplitWgs = 256;
+constexpr int kSkinnySplitMinK = 3072;  // shortest K cut across workgroups  // a split projection: one workgroup per CU
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
@@ -1256,10 +1257,19 @@ SkinnyShape skinny_base_shape(qasr_decoder* d, int rows, int n_out, int k, bool 
     }
     const int tiles = n_out / 16;
     if (tiles >= kSkinnyTargetWgs) return SkinnyShape{k % (4 * kSkinnyPair) ? 0 : 4, 1};
-    if (k >= 4096)
+    // K of 3072 or more is cut across workgroups (the down_proj of both shapes):
+    // two groups reach 256 workgroups at the 1.7B shape; the 0.6B's 64 tiles
+    // take three (192; one-slot step 956 against 962 us unsplit).  K = 2048
+    // stays whole (16-slot step 1810 against 1847 us split).
+    if (k >= kSkinnySplitMinK) {
+        int best = 0;
         for (int g : {2, 3, 4, 6, 8, 12})
-            if (k % (4 * g * kSkinnyPair) == 0 && (tiles * g >= kSkinnySplitWgs || g == 12))
-                return SkinnyShape{4, g};
+            if (k % (4 * g * kSkinnyPair) == 0) {
+                best = g;
+                if (tiles * g >= kSkinnySplitWgs) break;
+            }
+        if (best) return SkinnyShape{4, best};
+    }
     for (int ks : {12, 8, 4})
         if (k % (ks * kSkinnyPair) == 0) return SkinnyShape{ks, 1};
     return SkinnyShape{};
