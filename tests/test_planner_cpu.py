@@ -74,11 +74,11 @@ def test_decode_plan_bench_configs():
     chunk, base = qasr_attn.plan_decode([8193], NKVH, 256)
     assert chunk == [288] and base == [0, 8 * 29]  # config 4: 29 chunks of 288 keys
     chunk, base = qasr_attn.plan_decode([512], NKVH, 256)
-    assert chunk == [128] and base == [0, 32]  # config 1: 128-key minimum chunk
+    assert chunk == [64] and base == [0, 64]  # config 1: 64-key minimum chunk
     # below two minimum chunks an entry stays whole: one chunk of whole passes
     chunk, base = qasr_attn.plan_decode([1, 2, 31, 32, 33, 255, 256, 257], NKVH, 256)
-    assert chunk == [32, 32, 32, 32, 64, 128, 128, 128]
-    assert base == [0, 8, 16, 24, 32, 40, 56, 72, 96]
+    assert chunk == [32, 32, 32, 32, 64, 64, 64, 64]
+    assert base == [0, 8, 16, 24, 32, 40, 72, 104, 144]
     # a batch at the budget (64 entries x 8 kv heads) splits only its longest entries
     lens = [100] * 63 + [4000]
     chunk, base = qasr_attn.plan_decode(lens, NKVH, 256)
