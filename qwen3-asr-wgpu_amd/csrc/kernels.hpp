@@ -48,7 +48,7 @@ constexpr int kDecodeTileKeys = 32;   // keys per wave pass
 constexpr int kDecodeMaxChunksPerEntry = 256;
 constexpr int kDecodeMinChunk = 64;    // keys (one slot at 511: 7.24 us against 7.54 at 128, 7.88 at 32)
 constexpr int kDecodeMergeBatch = 32;  // partials the merging workgroup requests per round trip
-constexpr int kDecodeMaxSplit = kDecodeMergeBatch;  // chunks per entry by default (one merge batch)
+constexpr int kDecodeMaxSplit = 16;  // chunks per entry by default (config 4: 12.28 us against 12.55 at 32)
 constexpr int kDecodeMaxItems = 8192;   // >= 4096 target + kMaxBatch * nkvh rounding slack
 
 // Split-K workspace of one launch: per workgroup the unnormalised partial

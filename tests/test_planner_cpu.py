@@ -72,7 +72,7 @@ def test_decode_plan_bench_configs():
     full = sum(NKVH * (L // 960) for L in lens3p if L > 960)
     assert full >= 128  # most workgroups stream a full chunk until the end
     chunk, base = qasr_attn.plan_decode([8193], NKVH, 256)
-    assert chunk == [288] and base == [0, 8 * 29]  # config 4: 29 chunks of 288 keys
+    assert chunk == [544] and base == [0, 8 * 16]  # config 4: 16 chunks of 544 keys
     chunk, base = qasr_attn.plan_decode([512], NKVH, 256)
     assert chunk == [64] and base == [0, 64]  # config 1: 64-key minimum chunk
     # below two minimum chunks an entry stays whole: one chunk of whole passes
