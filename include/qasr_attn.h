@@ -342,13 +342,15 @@ int qasr_mfma_probe(qasr_ctx* ctx, int mode, int wgs, int waves, int mfma_iters,
  *
  * Decode (qasr_decode_attn / qasr_decode_step): `batch` (1..64) entries
  * attending lens[b] >= 1 keys, `nkvh` kv heads, a device of `cus` compute
- * units; the QASR_DECODE_WGS / _MIN_CHUNK / _MAX_SPLIT environment knobs
- * apply.  chunk_out[b]: keys per workgroup of entry b (a multiple of 32);
- * wg_base_out[0..batch]: entry b's workgroups are wg_base_out[b] ..
- * wg_base_out[b+1]-1 (nkvh * ceil(lens[b] / chunk_out[b]) of them).
+ * units; the QASR_DECODE_WGS / _GRANULE / _MAX_GRANULES environment knobs
+ * apply.  gran_out[b]: keys per granule of entry b (a multiple of 128 and a
+ * function of lens[b] alone: the entry's output bits do not depend on its
+ * batch mates); run_out[b]: granules per workgroup; wg_base_out[0..batch]:
+ * entry b's workgroups are wg_base_out[b] .. wg_base_out[b+1]-1
+ * (nkvh * ceil(ceil(lens[b] / gran_out[b]) / run_out[b]) of them).
  * lens[b] in [1, 1 << 24]. */
-int qasr_plan_decode(int batch, const int32_t* lens, int nkvh, int cus, int32_t* chunk_out,
-                     int32_t* wg_base_out);
+int qasr_plan_decode(int batch, const int32_t* lens, int nkvh, int cus, int32_t* gran_out,
+                     int32_t* run_out, int32_t* wg_base_out);
 
 /* Prefill (qasr_prefill_attn, one launch of 1..4096 rows at kv_start):
  * *rows_per_block (64, or 32 for unsplit short key ranges), *nrb row

@@ -152,6 +152,10 @@ __device__ __forceinline__ void stores_done_barrier() {
 __device__ __forceinline__ uint32_t ticket_add(uint32_t* p) {
     return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Arrival of n partials at once; returns the count before them.
+__device__ __forceinline__ uint32_t ticket_add_n(uint32_t* p, uint32_t n) {
+    return __hip_atomic_fetch_add(p, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ void ticket_reset(uint32_t* p) {
     __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

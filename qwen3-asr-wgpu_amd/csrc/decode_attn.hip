@@ -6,36 +6,47 @@
 // 1932-2025 and 3348-3451).  Semantics: src/cpu_decoder.rs:292-365 with one
 // query row, i.e. softmax(q.k_t * scale) . v over keys t < cur_len.
 //
+// Granules and runs.  An entry's keys are cut into granules whose size is a
+// function of the entry's own length only (the host's plan: a multiple of 256
+// keys, at most kDecodeMaxGranules of them).  Each granule yields one partial
+// (max, sum, unnormalised output per q head), and the partials of an entry
+// are merged in granule order.  So the bits of an entry's output depend on
+// its length and its keys, never on its batch mates: the reference's
+// `--batch N` output is byte-identical to `--batch 1` (src/decoder.rs:
+// 1930-1931, README "byte-identical"), and so is this kernel's.  What the
+// batch changes is only which workgroup runs which granules: a workgroup
+// takes a run of consecutive granules of one (entry, kv head), so the host
+// can spread any batch over about one workgroup per CU.
+//
 // Work decomposition (one launch for the whole batch):
-//   workgroup = (batch entry b, kv head, chunk of keys), W waves.  Chunk sizes
-//   are planned per entry on the host so every workgroup streams about the
-//   same number of keys whatever the ragged lengths.
+//   workgroup = (batch entry b, kv head, run of granules), 4 waves.
 //   Both q heads of the kv head (GQA 2:1) are computed from one K/V read.
-//   A wave pass covers 32 contiguous keys (wave w of a workgroup pass takes
-//   keys t0 + 32*w .. +32, so the workgroup's requests of one pass form one
-//   contiguous run): 8 dwordx4 buffer loads of K and 8 of V per lane, each
-//   instruction reading 1 KiB contiguous (4 keys x 256 B, lane l -> key l/16,
-//   dims (l%16)*8..+8), so every instruction is fully coalesced.  (Spreading
-//   a wave's loads over the workgroup pass in 4-key groups, or giving each
-//   wave one contiguous share of the chunk, both measured slower.)
-//   The buffer resources end at the chunk's last key, so the hardware range
-//   check returns zeros past it (those scores are masked).
+//   A workgroup pass covers 128 contiguous keys, wave w taking keys 32w..+32:
+//   8 dwordx4 buffer loads of K and 8 of V per lane, each instruction
+//   reading 1 KiB contiguous (4 keys x 256 B, lane l -> key l/16, dims
+//   (l%16)*8..+8), so every instruction is fully coalesced.  The buffer
+//   resources end at the run's last key, so the hardware range check returns
+//   zeros past it (those scores are masked).
 //   q.k: v_dot2_f32_f16 on the lane's 8 dims, then a transposing 16-lane DPP
 //   reduction that leaves each lane with one (key, head) score.  Softmax is
 //   online per (16-lane row, head) in the exp2 domain; the row's 16
 //   probabilities reach the V layout through LDS and P.V accumulates in f32
-//   (v_fma_mix on packed f16).  The 4W rows of the workgroup merge through
-//   one LDS pass.
-//   When an entry needs more than one chunk, each workgroup publishes its
-//   partial (max, sum, unnormalised output) with device-scope stores and the
-//   last one to arrive (ticket) merges them, issuing all its loads at once:
-//   no second launch and no L2-wide cache maintenance.
+//   (v_fma_mix on packed f16).  At each granule's end the 16 rows of the
+//   workgroup merge through one LDS pass (double buffered, one barrier) into
+//   the granule's partial, which stays in LDS, and the rows start over.
+//   After the run: an entry with one granule writes its output; a (entry,
+//   kv head) whose granules all ran in this workgroup merges them from LDS;
+//   otherwise the run's partials are published with device-scope stores and
+//   the last workgroup to arrive (ticket) merges all of them, issuing its
+//   loads at once: no second launch and no L2-wide cache maintenance.  Both
+//   merges combine the same values in the same order.
 //
 // Fused variant (stage (a) + (b)): the workgroup recomputes its two q heads
 // from the raw qkv row (bit-identical to the stage-(a) kernel); the workgroup
-// owning the last chunk also ropes the new K row, appends K and V to the cache
-// and substitutes them for the cache load of that key.  The first K/V pass is
-// issued before this prologue so its latency overlaps it.
+// owning the last granule also ropes the new K row, appends K and V to the
+// cache and substitutes them for the cache load of that key.  The first K/V
+// pass is requested before the workgroup waits for its query inputs, so the
+// prologue runs under that pass's latency.
 
 #include <type_traits>
 
@@ -54,6 +65,10 @@ constexpr int kSc1 = 16;  // buffer cache policy: sc1 (device-coherent, as agent
 // once per launch, and streaming it with the default policy measured 7-9%
 // slower (config 3: 23.3 against 21.7 us; 16 x 2048 keys: 29.2 against 26.5).
 constexpr int kNt = 2;
+constexpr int W = kDecodeWaves;
+constexpr int kWgKeys = W * kDecodeTileKeys;  // keys per workgroup pass
+static_assert(2 * kWgKeys == kDecodeGranuleQuantum, "a granule is an even number of workgroup passes");
+constexpr int kMaxG = kDecodeMaxGranules;
 
 __device__ __forceinline__ float dot8(const H8& a, const H8& b) {
     float s = 0.0f;
@@ -81,7 +96,7 @@ __device__ __forceinline__ void load_pass(__amdgpu_buffer_rsrc_t r, int t0, int 
     }
 }
 
-template <bool FUSED, int W>
+template <bool FUSED>
 __global__ __launch_bounds__(W * 64)
 __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kernel(
     CacheGeom g, int layer, DecodePlan P, const f16* __restrict__ qin,
@@ -93,12 +108,16 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     __shared__ H8 s_vnew[16];
     __shared__ __attribute__((aligned(16))) f16 s_raw[4][kHeadDim];  // q0, q1, k, v raw heads
     __shared__ __attribute__((aligned(16))) f16 s_tab[4][kHeadDim];  // q gain, k gain, cos, sin
-    __shared__ __attribute__((aligned(16))) float s_sq[3][kHeadDim];  // squares of q0, q1, k
     __shared__ float s_inv[3];
     __shared__ float s_p[W][64];
-    __shared__ float s_wm[4 * W][2];
-    __shared__ float s_wl[4 * W][2];
-    __shared__ float s_wa[4 * W][2][kHeadDim];
+    // Row states at a granule's end (double buffered: one barrier per granule).
+    __shared__ float s_wm[2][4 * W][2];
+    __shared__ float s_wl[2][4 * W][2];
+    __shared__ float s_wa[2][4 * W][2][kHeadDim];
+    // Granule partials of this workgroup's run.
+    __shared__ float s_pm[kMaxG][2];
+    __shared__ float s_pl[kMaxG][2];
+    __shared__ float s_pa[kMaxG][2][kHeadDim];
     __shared__ int s_last;
 
     const int wg = blockIdx.x;
@@ -113,77 +132,72 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     static_assert(kMaxBatch <= 64, "one lane per entry");
     const int b = __popcll(__ballot(lane + 1 < P.batch && P.wg_base[lane + 1] <= wg));
     const int L = P.len[b];
-    const int chunk = P.chunk[b];
-    const int nch = (L + chunk - 1) / chunk;
+    const int G = P.gran[b];
+    const int run = P.run[b];
+    const int ngr = (L + G - 1) / G;        // granules of the entry (per kv head)
+    const int nw = (ngr + run - 1) / run;   // workgroups per kv head
     const int rel = wg - P.wg_base[b];
-    const int kvh = rel / nch;
-    const int c = rel - kvh * nch;
-    const int key0 = c * chunk;
-    const int key1 = min(key0 + chunk, L);
+    const int kvh = rel / nw;
+    const int r = rel - kvh * nw;
+    const int g0 = r * run;
+    const int g1 = min(g0 + run, ngr);
+    const int key0 = g0 * G;
+    const int key1 = min(g1 * G, L);
     const int nkeys = key1 - key0;
+    const int ppg = G / kWgKeys;                    // passes per granule
+    const int npass = (nkeys + 2 * kWgKeys - 1) / (2 * kWgKeys) * 2;  // even
     const int nqh = P.nqh;
     const int h0 = kvh * kRep;
     f16* Kc = g.base + P.slot[b] * g.slot_stride + layer * g.layer_stride + kvh * g.head_stride;
     f16* Vc = Kc + g.kv_stride;
-    // Resources start at the chunk's first key and end at its last.
+    // Resources start at the run's first key and end at its last.
     const int rbytes = nkeys * (kHeadDim * 2);
     const __amdgpu_buffer_rsrc_t kres = make_rsrc(Kc + (int64_t)key0 * kHeadDim, rbytes);
     const __amdgpu_buffer_rsrc_t vres = make_rsrc(Vc + (int64_t)key0 * kHeadDim, rbytes);
-    constexpr int kWgKeys = W * kDecodeTileKeys;  // keys per workgroup pass
-    const int tw = wave * kDecodeTileKeys;         // this wave's first key in a pass
+    const int tw = wave * kDecodeTileKeys;  // this wave's first key in a pass
 
-    // The query inputs (the raw qkv heads, or q itself) are requested first and
-    // the first K/V pass right after them, so the K/V stream starts without
-    // waiting for a round trip; the prologue runs while the pass is in flight.
+    // The query inputs (the raw qkv heads and the gain / cos / sin rows, or q
+    // itself) come in by direct global -> LDS copies, requested first; the
+    // first K/V pass is requested right after them, and only then does the
+    // workgroup wait for the copies (by count: they are older than the pass),
+    // so the K/V stream starts without waiting for a round trip and the
+    // prologue runs while the first pass is in flight.  The passes are issued
+    // in order (scheduling barriers): the loop waits for the older pass by
+    // count while the newer one stays in flight.
     const int pos = L - 1;
-    const bool owner = FUSED && (c == nch - 1);
-    H8 q0, q1;
+    const bool owner = FUSED && (r == nw - 1);
     if constexpr (FUSED) {
         const int64_t tot = (int64_t)(nqh + 2 * g.nkvh) * kHeadDim;
         const f16* qkv_row = qin + b * tot;
-        if (tid < 64) {
-            const int which = tid >> 4;
+        if (wave == 0) {  // lane l: head l/16 (q0, q1, k, v), 16-byte piece l%16
+            const int which = lane >> 4;
             const int hoff = which < 2 ? (h0 + which) : which == 2 ? (nqh + kvh) : (nqh + g.nkvh + kvh);
-            H8 x;
-            x.u = *(const uint4*)(qkv_row + hoff * kHeadDim + seg * 8);
-            *(uint4*)&s_raw[which][seg * 8] = x.u;
-            if (which < 3) {  // f16 squares are exact in f32
-                float4 lo, hi;
-                lo.x = h2f(x.e[0]) * h2f(x.e[0]);
-                lo.y = h2f(x.e[1]) * h2f(x.e[1]);
-                lo.z = h2f(x.e[2]) * h2f(x.e[2]);
-                lo.w = h2f(x.e[3]) * h2f(x.e[3]);
-                hi.x = h2f(x.e[4]) * h2f(x.e[4]);
-                hi.y = h2f(x.e[5]) * h2f(x.e[5]);
-                hi.z = h2f(x.e[6]) * h2f(x.e[6]);
-                hi.w = h2f(x.e[7]) * h2f(x.e[7]);
-                *(float4*)&s_sq[which][seg * 8] = lo;
-                *(float4*)&s_sq[which][seg * 8 + 4] = hi;
-            }
-        } else if (tid < 128) {
-            const int which = (tid >> 4) & 3;
-            const f16* p = which == 0 ? q_gain
-                         : which == 1 ? k_gain
-                         : which == 2 ? cos_tab + (int64_t)pos * kHeadDim
-                                      : sin_tab + (int64_t)pos * kHeadDim;
-            *(uint4*)&s_tab[which][seg * 8] = *(const uint4*)(p + seg * 8);
+            dma16(make_rsrc_words(qkv_row, (int)(tot * 2)), hoff * (kHeadDim * 2) + seg * 16,
+                  lds_addr(&s_raw[0][0]));
+        } else if (wave == 1 && lane < 16) {
+            dma16(make_rsrc_words(q_gain, kHeadDim * 2), seg * 16, lds_addr(&s_tab[0][0]));
+            dma16(make_rsrc_words(k_gain, kHeadDim * 2), seg * 16, lds_addr(&s_tab[1][0]));
+            dma16(make_rsrc_words(cos_tab + (int64_t)pos * kHeadDim, kHeadDim * 2), seg * 16,
+                  lds_addr(&s_tab[2][0]));
+            dma16(make_rsrc_words(sin_tab + (int64_t)pos * kHeadDim, kHeadDim * 2), seg * 16,
+                  lds_addr(&s_tab[3][0]));
         }
-    } else {
-        const f16* qb = qin + (int64_t)b * nqh * kHeadDim + h0 * kHeadDim + seg * 8;
-        q0.u = *(const uint4*)qb;
-        q1.u = *(const uint4*)(qb + kHeadDim);
+    } else if (wave == 0 && lane < 32) {  // lane l: q head l/16, 16-byte piece l%16
+        const f16* qb = qin + (int64_t)b * nqh * kHeadDim + h0 * kHeadDim;
+        dma16(make_rsrc_words(qb, 2 * kHeadDim * 2), lane * 16, lds_addr(&s_q[0][0]));
     }
 
-    // Two pass buffers per wave: while one pass is computed the next one's
-    // loads are in flight.  Passes past the chunk fall outside the buffer
-    // range: their loads return zeros without touching memory.
     H8 ka[8], va[8], kb[8], vb[8];
     load_pass(kres, tw, row, seg, ka);
     load_pass(vres, tw, row, seg, va);
+    __builtin_amdgcn_sched_barrier(0);
+    // This wave's copies are older than the 16 pass loads just issued.
+    __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16)
+    __syncthreads();
 
+    H8 q0, q1;
     if constexpr (FUSED) {
-        __syncthreads();
-        if (tid < 3 && (tid < 2 || owner)) s_inv[tid] = head_inv_rms_squares(s_sq[tid], P.eps);
+        if (tid < 3 && (tid < 2 || owner)) s_inv[tid] = head_inv_rms_serial(s_raw[tid], P.eps);
         __syncthreads();
         if (tid < 256) {
             const int h = tid >> 7, j = tid & 127;
@@ -201,12 +215,14 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
             }
         }
         __syncthreads();
-        q0 = s_q[0][seg];
-        q1 = s_q[1][seg];
     }
+    q0 = s_q[0][seg];
+    q1 = s_q[1][seg];
 
+    __builtin_amdgcn_sched_barrier(0);
     load_pass(kres, tw + kWgKeys, row, seg, kb);
     load_pass(vres, tw + kWgKeys, row, seg, vb);
+    __builtin_amdgcn_sched_barrier(0);
 
     // Per 16-lane row: running (max, sum) of the head given by the lane's
     // parity (replicated over the 8 lanes of that parity), and the lane's 8
@@ -218,7 +234,7 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     const bool odd = seg & 1;
     float* s_pw = &s_p[wave][0];
     const float sl2 = P.scale_log2;
-    const int new_rel = pos - key0;  // the appended key, relative to the chunk (owner only)
+    const int new_rel = pos - key0;  // the appended key, relative to the run (owner only)
 
     auto process = [&](H8 (&kr)[8], H8 (&vr)[8], int t0) {
         if constexpr (FUSED) {
@@ -284,72 +300,116 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
         __builtin_amdgcn_wave_barrier();
     };
 
-    for (int t0 = tw; t0 < nkeys; t0 += 2 * kWgKeys) {
+    // One thread per (head, dim): h, j.  Partial records of this (entry, kv
+    // head): part0 + granule.
+    const int h = tid >> 7, j = tid & 127;
+    f16* ob = out + (int64_t)b * nqh * kHeadDim + h0 * kHeadDim;
+    const int64_t part0 = (int64_t)P.part_base[b] + (int64_t)kvh * ngr;
+
+    // End of granule gi (relative to the run): the 16 rows merge through LDS
+    // in row order into the granule's (M, sum, unnormalised output), kept in
+    // LDS until the run ends; then the rows start over.  Nothing here touches
+    // global memory, so the K/V stream's loads stay the only ones in flight.
+    auto finalize = [&](int gi) {
+        const int buf = gi & 1;
+        const int rr = wave * 4 + row;
+        if (seg < 2) {  // lane 0 of the row holds head 0's (m, l), lane 1 head 1's
+            s_wm[buf][rr][seg] = m_run;
+            s_wl[buf][rr][seg] = l_run;
+        }
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            s_wa[buf][rr][0][seg * 8 + d] = a0[d];
+            s_wa[buf][rr][1][seg * 8 + d] = a1[d];
+        }
+        __syncthreads();
+        float M = kNegInf;
+#pragma unroll
+        for (int q = 0; q < 4 * W; ++q) M = fmaxf(M, s_wm[buf][q][h]);
+        float Ls = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4 * W; ++q) {
+            const float mr = s_wm[buf][q][h];
+            const float f = mr == kNegInf ? 0.0f : fast_exp2(mr - M);
+            Ls = fmaf(s_wl[buf][q][h], f, Ls);
+            A = fmaf(s_wa[buf][q][h][j], f, A);
+        }
+        s_pa[gi][h][j] = A;
+        if (j == 0) {
+            s_pm[gi][h] = M;
+            s_pl[gi][h] = Ls;
+        }
+        m_run = kNegInf;
+        l_run = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) a0[d] = a1[d] = 0.0f;
+    };
+
+    // Workgroup passes p = 0, 1, ..: wave keys 128 p + tw .. +32, two per
+    // iteration (a granule is an even number of passes, and an odd last pass
+    // is followed by an empty one).  Every wave processes every pass: keys
+    // past the run are masked, which leaves a row's state exactly as it was.
+    // Only an entry's last granule can end inside a pass, and it is always
+    // the last of its run.  The loop has one path, so the compiler keeps the
+    // next pass's loads in flight while the current one is computed.
+    for (int p = 0; p < npass; p += 2) {
+        const int t0 = p * kWgKeys + tw;
         process(ka, va, t0);
         __builtin_amdgcn_sched_barrier(0);
         load_pass(kres, t0 + 2 * kWgKeys, row, seg, ka);
         load_pass(vres, t0 + 2 * kWgKeys, row, seg, va);
-        if (t0 + kWgKeys < nkeys) process(kb, vb, t0 + kWgKeys);
+        process(kb, vb, t0 + kWgKeys);
         __builtin_amdgcn_sched_barrier(0);
         load_pass(kres, t0 + 3 * kWgKeys, row, seg, kb);
         load_pass(vres, t0 + 3 * kWgKeys, row, seg, vb);
+        if ((p + 2) % ppg == 0 || p + 2 >= npass) finalize(p / ppg);
     }
-
-    // Merge the 4W rows of the workgroup through LDS: every row holds the
-    // (max, sum) of the head of the lane's parity and 8 dims of both heads.
-    {
-        const int r = wave * 4 + row;
-        if (seg < 2) {  // lane 0 of the row holds head 0's (m, l), lane 1 head 1's
-            s_wm[r][seg] = m_run;
-            s_wl[r][seg] = l_run;
-        }
-#pragma unroll
-        for (int d = 0; d < 8; ++d) {
-            s_wa[r][0][seg * 8 + d] = a0[d];
-            s_wa[r][1][seg * 8 + d] = a1[d];
-        }
-    }
+    const int mine = g1 - g0;  // granules of this run, partials in s_p*[0 .. mine)
     __syncthreads();
-    if (tid >= 256) return;  // 256 threads: one per (head, dim)
-    const int h = tid >> 7, j = tid & 127;
-    float M = kNegInf;
-#pragma unroll
-    for (int r = 0; r < 4 * W; ++r) M = fmaxf(M, s_wm[r][h]);
-    float Ls = 0.0f, A = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 4 * W; ++r) {
-        const float mr = s_wm[r][h];
-        const float f = mr == kNegInf ? 0.0f : fast_exp2(mr - M);
-        Ls = fmaf(s_wl[r][h], f, Ls);
-        A = fmaf(s_wa[r][h][j], f, A);
-    }
-    f16* ob = out + (int64_t)b * nqh * kHeadDim + h0 * kHeadDim;
-    if (nch == 1) {
-        ob[h * kHeadDim + j] = f2h(A / Ls);
+    if (ngr == 1) {
+        ob[h * kHeadDim + j] = f2h(s_pa[0][h][j] / s_pl[0][h]);
         return;
     }
 
-    store_dev(&ws_acc[(int64_t)wg * (2 * kHeadDim) + h * kHeadDim + j], A);
-    if (j == 0) {
-        store_dev(&ws_ml[(int64_t)wg * 4 + h], M);
-        store_dev(&ws_ml[(int64_t)wg * 4 + 2 + h], Ls);
+    // Merge of the ngr granule partials in granule order: M = max of the
+    // granule maxima, then sum_i 2^(m_i - M) * (l_i, acc_i).  Every granule
+    // holds at least one real key, so every m_i is finite.  The LDS and the
+    // workspace paths below do the same arithmetic in the same order.
+    if (nw == 1) {
+        float M = s_pm[0][h];
+        for (int i = 1; i < ngr; ++i) M = fmaxf(M, s_pm[i][h]);
+        float lsum = 0.0f, acc = 0.0f;
+        for (int i = 0; i < ngr; ++i) {
+            const float wgt = fast_exp2(s_pm[i][h] - M);
+            lsum = fmaf(s_pl[i][h], wgt, lsum);
+            acc = fmaf(s_pa[i][h][j], wgt, acc);
+        }
+        ob[h * kHeadDim + j] = f2h(acc / lsum);
+        return;
     }
-    stores_done_barrier();  // waves past thread 256 have exited: s_barrier counts live waves
+
+    // Publish this run's partials (device-scope stores), then the ticket.
+    for (int gi = 0; gi < mine; ++gi) {
+        const int64_t it = part0 + g0 + gi;
+        store_dev(&ws_acc[it * (2 * kHeadDim) + h * kHeadDim + j], s_pa[gi][h][j]);
+        if (j == 0) {
+            store_dev(&ws_ml[it * 4 + h], s_pm[gi][h]);
+            store_dev(&ws_ml[it * 4 + 2 + h], s_pl[gi][h]);
+        }
+    }
+    stores_done_barrier();
     uint32_t* ctr = &counters[b * g.nkvh + kvh];
-    if (tid == 0) s_last = (ticket_add(ctr) == (uint32_t)(nch - 1));
+    if (tid == 0) s_last = (ticket_add_n(ctr, (uint32_t)mine) + (uint32_t)mine == (uint32_t)ngr);
     __syncthreads();
     if (!s_last) return;
 
-    // Last arrival: merge the nch partials of (b, kv head) in chunk order:
-    // M = max of the chunk maxima, then sum_i 2^(m_i - M) * (l_i, acc_i).
-    // Every chunk holds at least one real key, so every m_i is finite.  Each
-    // thread requests the (m, l) of its head and its element of every chunk
-    // of a batch of 32 at once, as plain device-coherent (sc1) loads: a batch
-    // costs one memory round trip and the arithmetic has no branches.
-    const int64_t it0 = P.wg_base[b] + kvh * nch;
-    const __amdgpu_buffer_rsrc_t acc_res = make_rsrc(ws_acc + it0 * (2 * kHeadDim), nch * (2 * kHeadDim) * 4);
-    const __amdgpu_buffer_rsrc_t ml_res = make_rsrc(ws_ml + it0 * 4, nch * 16);
-    constexpr int kBatch = kDecodeMergeBatch;
+    // Last arrival: each thread requests the (m, l) of its head and its
+    // element of every granule at once, as plain device-coherent (sc1) loads
+    // into a batch of 4, 8, 16 or 32 slots sized to the granule count (unused
+    // slots read granule 0 and get weight 0): one memory round trip, and the
+    // arithmetic has no branches.
+    const __amdgpu_buffer_rsrc_t acc_res = make_rsrc(ws_acc + part0 * (2 * kHeadDim), ngr * (2 * kHeadDim) * 4);
+    const __amdgpu_buffer_rsrc_t ml_res = make_rsrc(ws_ml + part0 * 4, ngr * 16);
     auto ld_ml = [&](int i, int k) {  // k: 0 = m, 2 = l
         return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ml_res, (i * 4 + k + h) * 4, 0, kSc1));
     };
@@ -358,103 +418,60 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
                                              acc_res, (i * (2 * kHeadDim) + h * kHeadDim + j) * 4, 0, kSc1));
     };
     float lsum = 0.0f, acc = 0.0f;
-    // One round trip for N >= nch chunks (N a compile-time batch, so only
-    // about as many loads are issued as there are chunks).
     auto merge_one_batch = [&](auto n_tag) {
         constexpr int N = decltype(n_tag)::value;
         float mv[N], lv[N], xv[N];
 #pragma unroll
         for (int u = 0; u < N; ++u) {
-            const int i = u < nch ? u : 0;
+            const int i = u < ngr ? u : 0;
             mv[u] = ld_ml(i, 0);
             lv[u] = ld_ml(i, 2);
             xv[u] = ld_acc(i);
         }
         float M = mv[0];
 #pragma unroll
-        for (int u = 1; u < N; ++u) M = fmaxf(M, mv[u]);  // repeats of chunk 0 change nothing
+        for (int u = 1; u < N; ++u) M = fmaxf(M, mv[u]);  // repeats of granule 0 change nothing
 #pragma unroll
         for (int u = 0; u < N; ++u) {
-            const float wgt = u < nch ? fast_exp2(mv[u] - M) : 0.0f;
-            lsum = fmaf(lv[u], wgt, lsum);
-            acc = fmaf(xv[u], wgt, acc);
-        }
-    };
-    if (nch <= 4) {
-        merge_one_batch(std::integral_constant<int, 4>{});
-    } else if (nch <= 8) {
-        merge_one_batch(std::integral_constant<int, 8>{});
-    } else if (nch <= 16) {
-        merge_one_batch(std::integral_constant<int, 16>{});
-    } else if (nch <= kBatch) {
-        merge_one_batch(std::integral_constant<int, kBatch>{});
-    } else {
-        float M = kNegInf;
-        for (int i0 = 0; i0 < nch; i0 += kBatch) {
-            float mv[kBatch];
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) mv[u] = ld_ml(i0 + u < nch ? i0 + u : i0, 0);
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) M = fmaxf(M, mv[u]);
-        }
-        for (int i0 = 0; i0 < nch; i0 += kBatch) {
-            float mv[kBatch], lv[kBatch], xv[kBatch];
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const int i = i0 + u < nch ? i0 + u : i0;
-                mv[u] = ld_ml(i, 0);
-                lv[u] = ld_ml(i, 2);
-                xv[u] = ld_acc(i);
-            }
-#pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const float wgt = i0 + u < nch ? fast_exp2(mv[u] - M) : 0.0f;
+            if (u < ngr) {
+                const float wgt = fast_exp2(mv[u] - M);
                 lsum = fmaf(lv[u], wgt, lsum);
                 acc = fmaf(xv[u], wgt, acc);
             }
         }
+    };
+    static_assert(kMaxG == 32, "merge batches");
+    if (ngr <= 4) {
+        merge_one_batch(std::integral_constant<int, 4>{});
+    } else if (ngr <= 8) {
+        merge_one_batch(std::integral_constant<int, 8>{});
+    } else if (ngr <= 16) {
+        merge_one_batch(std::integral_constant<int, 16>{});
+    } else {
+        merge_one_batch(std::integral_constant<int, 32>{});
     }
     ob[h * kHeadDim + j] = f2h(acc / lsum);
     if (tid == 0) ticket_reset(ctr);
 }
 
-template <bool FUSED>
-hipError_t launch_w(int waves, const dim3& grid, hipStream_t stream, const CacheGeom& g,
-                    int layer, const DecodePlan& P, const f16* qin, const f16* q_gain,
-                    const f16* k_gain, const f16* cos_tab, const f16* sin_tab, f16* out,
-                    const DecodeWs& ws) {
-    switch (waves) {
-        case 4:
-            hipLaunchKernelGGL((decode_attn_kernel<FUSED, 4>), grid, dim3(4 * 64), 0, stream, g,
-                               layer, P, qin, q_gain, k_gain, cos_tab, sin_tab, out, ws.acc,
-                               ws.ml, ws.counters);
-            break;
-        case 8:
-            hipLaunchKernelGGL((decode_attn_kernel<FUSED, 8>), grid, dim3(8 * 64), 0, stream, g,
-                               layer, P, qin, q_gain, k_gain, cos_tab, sin_tab, out, ws.acc,
-                               ws.ml, ws.counters);
-            break;
-        default:
-            return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
 }  // namespace
 
-hipError_t launch_decode_attn(bool fused, int waves, const CacheGeom& g, int layer,
-                              const DecodePlan& P, int total_wgs, const f16* q_or_qkv,
-                              const f16* q_gain, const f16* k_gain, const f16* cos_tab,
-                              const f16* sin_tab, f16* out, const DecodeWs& ws,
-                              hipStream_t stream) {
+hipError_t launch_decode_attn(bool fused, const CacheGeom& g, int layer, const DecodePlan& P,
+                              int total_wgs, const f16* q_or_qkv, const f16* q_gain,
+                              const f16* k_gain, const f16* cos_tab, const f16* sin_tab, f16* out,
+                              const DecodeWs& ws, hipStream_t stream) {
     if (total_wgs <= 0) return hipSuccess;
-    if (total_wgs > ws.items) return hipErrorInvalidValue;
-    const dim3 grid(total_wgs);
+    if (P.part_base[P.batch] > ws.items) return hipErrorInvalidValue;
+    const dim3 grid(total_wgs), block(W * 64);
     if (fused)
-        return launch_w<true>(waves, grid, stream, g, layer, P, q_or_qkv, q_gain, k_gain, cos_tab,
-                              sin_tab, out, ws);
-    return launch_w<false>(waves, grid, stream, g, layer, P, q_or_qkv, q_gain, k_gain, cos_tab,
-                           sin_tab, out, ws);
+        hipLaunchKernelGGL((decode_attn_kernel<true>), grid, block, 0, stream, g, layer, P,
+                           q_or_qkv, q_gain, k_gain, cos_tab, sin_tab, out, ws.acc, ws.ml,
+                           ws.counters);
+    else
+        hipLaunchKernelGGL((decode_attn_kernel<false>), grid, block, 0, stream, g, layer, P,
+                           q_or_qkv, q_gain, k_gain, cos_tab, sin_tab, out, ws.acc, ws.ml,
+                           ws.counters);
+    return hipGetLastError();
 }
 
 }  // namespace qasr

@@ -47,15 +47,12 @@ namespace {
 constexpr int kNormThreads = 256;
 constexpr int kArgmaxThreads = 256;
 constexpr int kArgmaxChunks = 32;  // workgroups per logits row in the first argmax pass
-constexpr int kHeadRows = 128;     // rows per logits GEMM + argmax (bounds the logits scratch)
+constexpr int kHeadRows = 16;      // rows per logits GEMM + argmax: one skinny launch (kSkinnyRows)
 constexpr size_t kBlasWorkspace = size_t(64) << 20;
 constexpr int kMaxPrefillSegs = 64;  // segments of one batched prefill call
 // Rows of one call (decode batch or prefill): bounds the activation
 // workspace (about 61 KB per row at the 1.7B shape, 1 GB at the limit).
 constexpr int kMaxDecoderRows = 16384;
-// With QASR_PREFILL_GEMM=own, projections of at least this many rows
-// (prefill) take gemm_f16_kernel (gemm.hip) instead of rocBLAS.
-constexpr int kOwnGemmMinRows = 128;
 
 // ---- block reductions (wave64 shuffles, then one LDS pass) ---------------
 __device__ __forceinline__ float wave_sum(float v) {
@@ -1157,7 +1154,8 @@ struct qasr_decoder {
     bool fuse = true;              // QASR_DECODER_FUSE=0: no fused epilogues (same results)
     int lds_gemm = 1;              // QASR_SKINNY_LDS: 0 older kernel only, 2 LDS kernel wherever it fits
     int lds_tpw = 0, lds_groups = 0;  // QASR_SKINNY_TPW / _GROUPS: shape overrides (0 = planner)
-    bool own_gemm = false;            // QASR_PREFILL_GEMM=own: gemm_f16_kernel for the prefill projections
+    bool own_gemm = true;             // QASR_PREFILL_GEMM=blas: rocBLAS for the prefill projections instead
+    bool prefill = false;             // inside a prefill's layers: every projection takes the GEMM
     int shared_tiles = 3;             // QASR_SKINNY_SHARED: skinny_shared_kernel tiles per workgroup (0 off)
     int shared_min_tiles = 512;       // QASR_SKINNY_SHARED_MIN_TILES: narrower outputs keep skinny_gemm_kernel
     bool argmax_tiles = true;         // QASR_ARGMAX_TILES=0: the two-pass argmax over the logits
@@ -1250,7 +1248,7 @@ SkinnyShape lds_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8) {
 }
 
 SkinnyShape skinny_base_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8, bool allow_lds) {
-    if (d->force_blas || rows > kSkinnyRows || n_out % 16) return SkinnyShape{};
+    if (d->force_blas || d->prefill || rows > kSkinnyRows || n_out % 16) return SkinnyShape{};
     if (d->lds_gemm && allow_lds) {
         const SkinnyShape sh = lds_shape(d, rows, n_out, k, w8);
         if (sh.nks) return sh;
@@ -1307,18 +1305,24 @@ SkinnyShape skinny_shape(qasr_decoder* d, int rows, int n_out, int k, bool w8 = 
     // CU -- the 1.7B gate|up's 768 tiles take three (256 workgroups: 14.1 us
     // against 15.6 with four on 192), the logits' 9,496 four (126.9 against
     // 130.5 us with three).  QASR_SKINNY_MULTI=T forces T (0: off).
+    // The choice is made for kSkinnyRows rows whatever the batch's row count
+    // (up to kSkinnyRows): the kernels' K slicing, and so every row's bits,
+    // must not depend on how many other rows share the launch (the
+    // reference's --batch N == --batch 1, decoder.rs:686-693).
+    if (rows > kSkinnyRows) return SkinnyShape{};
+    const int sr = kSkinnyRows;
     const int tiles = n_out / 16, cus = std::max(d->ctx->cus, 1);
     const int tw = d->multi_tiles < 0 ? std::min(4, std::max(2, (tiles + cus - 1) / cus)) : d->multi_tiles;
-    const bool multi_ok = !w8 && tw > 1 && rows >= kSharedMinRows && n_out / 16 >= d->shared_min_tiles &&
+    const bool multi_ok = !w8 && tw > 1 && sr >= kSharedMinRows && n_out / 16 >= d->shared_min_tiles &&
                           d->lds_gemm < 2;
-    SkinnyShape sh = skinny_base_shape(d, rows, n_out, k, w8, !multi_ok);
-    const bool wide = sh.ks && !sh.nks && rows >= kSharedMinRows && n_out / 16 >= d->shared_min_tiles;
+    SkinnyShape sh = skinny_base_shape(d, sr, n_out, k, w8, !multi_ok);
+    const bool wide = sh.ks && !sh.nks && sr >= kSharedMinRows && n_out / 16 >= d->shared_min_tiles;
     if (wide && !w8 && tw > 1 && (sh.ks == 4 || sh.ks == 8) && (tw >= 2 && tw <= 4)) {
         sh.multi_tiles = tw;
         sh.multi_ks = sh.ks;
         return sh;
     }
-    sh.shared_tiles = shared_tiles(d, sh, rows, n_out, k);
+    sh.shared_tiles = shared_tiles(d, sh, sr, n_out, k);
     return sh;
 }
 
@@ -1463,7 +1467,7 @@ int gemm_f16(qasr_decoder* d, int rows, int n_out, int k, const void* W, const f
         HIP_TRY(hipGetLastError(), "dequantisation launch");
         W = d->wdq;
     }
-    if (d->own_gemm && rows >= kOwnGemmMinRows && qasr::gemm_f16_fits(rows, n_out, k)) {
+    if (d->own_gemm && qasr::gemm_f16_fits(rows, n_out, k)) {
         HIP_TRY(qasr::launch_gemm_f16(x, (const f16*)W, y, rows, n_out, k, accumulate, d->ctx->cus,
                                       d->stream),
                 "projection GEMM launch");
@@ -1651,7 +1655,7 @@ int bind_stream(qasr_decoder* d, void* stream) {
     const char* gp = std::getenv("QASR_SKINNY_GROUPS");
     d->lds_groups = gp ? std::atoi(gp) : 0;
     const char* pg = std::getenv("QASR_PREFILL_GEMM");
-    d->own_gemm = pg && std::string(pg) == "own";
+    d->own_gemm = !(pg && std::string(pg) == "blas");
     const char* sh = std::getenv("QASR_SKINNY_SHARED");
     d->shared_tiles = sh ? std::atoi(sh) : 3;
     const char* mt = std::getenv("QASR_SKINNY_MULTI");
@@ -1716,17 +1720,28 @@ int prefill_segments(qasr_decoder* dec, qasr_kv* kv, const qasr_segment* segs, i
     HIP_TRY(hipMemcpyAsync(dec->x, hidden_dev, (size_t)rows * hs * 2, hipMemcpyDeviceToDevice, st),
             "prefill input copy");
     dec->ss_valid = false;
-    for (int l = 0; l < a.num_hidden_layers; ++l) {
-        const qasr_layer_weights& L = dec->layers[l];
-        rc = normed_proj(dec, rows, qkvdim, L.qkv_proj, dec->x, L.input_norm, dec->qkv, L.qkv_scale);
-        if (rc) return rc;
-        rc = qasr_qk_norm_rope_append(dec->ctx, kv, l, segs, nseg, dec->qkv, L.q_norm, L.k_norm,
-                                      dec->qw, stream);
-        if (rc) return rc;
-        rc = qasr_prefill_attn_batch(dec->ctx, kv, l, segs, nseg, dec->qw, dec->attn, stream);
-        if (rc) return rc;
-        rc = layer_tail(dec, L, rows, st);
-        if (rc) return rc;
+    // The layers' projections all take the GEMM, whatever the row count:
+    // its per-element K order does not depend on how many rows (prompts)
+    // share the launch, so a prompt's bits are those of its lone prefill.
+    struct PrefillMode {
+        qasr_decoder* d;
+        explicit PrefillMode(qasr_decoder* dd) : d(dd) { d->prefill = true; }
+        ~PrefillMode() { d->prefill = false; }
+    };
+    {
+        PrefillMode mode(dec);
+        for (int l = 0; l < a.num_hidden_layers; ++l) {
+            const qasr_layer_weights& L = dec->layers[l];
+            rc = normed_proj(dec, rows, qkvdim, L.qkv_proj, dec->x, L.input_norm, dec->qkv, L.qkv_scale);
+            if (rc) return rc;
+            rc = qasr_qk_norm_rope_append(dec->ctx, kv, l, segs, nseg, dec->qkv, L.q_norm, L.k_norm,
+                                          dec->qw, stream);
+            if (rc) return rc;
+            rc = qasr_prefill_attn_batch(dec->ctx, kv, l, segs, nseg, dec->qw, dec->attn, stream);
+            if (rc) return rc;
+            rc = layer_tail(dec, L, rows, st);
+            if (rc) return rc;
+        }
     }
     if (nseg == 1) return head(dec, dec->x + (int64_t)(rows - 1) * hs, 1, next_dev, logits_dev, st);
     // Last rows into the gate|up scratch ([max_rows][2 inter], free after the
@@ -1740,6 +1755,31 @@ int prefill_segments(qasr_decoder* dec, qasr_kv* kv, const qasr_segment* segs, i
     hipLaunchKernelGGL(gather_rows_kernel, dim3(nseg), dim3(256), 0, st, dec->x, hs, last, dec->gu);
     HIP_TRY(hipGetLastError(), "row gather launch");
     return head(dec, dec->gu, nseg, next_dev, logits_dev, st);
+}
+
+// One decode step of `batch` (<= kSkinnyRows) rows, arguments checked.
+int step_rows(qasr_decoder* dec, qasr_kv* kv, int batch, const int32_t* slots, const int32_t* pos,
+              const int32_t* tokens_dev, int32_t* next_dev, float* logits_dev, hipStream_t st) {
+    const qasr_attn_cfg& a = dec->ctx->cfg;
+    const int hs = dec->cfg.hidden_size;
+    const int qkvdim = (a.num_attention_heads + 2 * a.num_key_value_heads) * a.head_dim;
+    // Chunk sums for a fused first norm when a skinny batch can use them.
+    dec->ss_valid = dec->fuse && batch <= kSkinnyRows && hs <= kNormMaxK;
+    hipLaunchKernelGGL(embed_rows_kernel, dim3(batch), dim3(256), 0, st, dec->embed, tokens_dev,
+                       dec->cfg.vocab_size, hs, dec->x, dec->ss_valid ? dec->ss : nullptr);
+    HIP_TRY(hipGetLastError(), "embedding launch");
+    for (int l = 0; l < a.num_hidden_layers; ++l) {
+        const qasr_layer_weights& L = dec->layers[l];
+        int rc = normed_proj(dec, batch, qkvdim, L.qkv_proj, dec->x, L.input_norm, dec->qkv,
+                             L.qkv_scale);
+        if (rc) return rc;
+        rc = qasr_decode_step(dec->ctx, kv, l, batch, slots, pos, dec->qkv, L.q_norm, L.k_norm,
+                              dec->attn, st);
+        if (rc) return rc;
+        rc = layer_tail(dec, L, batch, st);
+        if (rc) return rc;
+    }
+    return head(dec, dec->x, batch, next_dev, logits_dev, st);
 }
 
 }  // namespace
@@ -1850,35 +1890,46 @@ int qasr_decoder_step(qasr_decoder* dec, qasr_kv* kv, int batch, const int32_t* 
                       const int32_t* pos, const int32_t* tokens_dev, int32_t* next_dev,
                       float* logits_dev, void* stream) {
     if (!dec || !kv) return fail(QASR_EINVAL, "null decoder or KV pool");
+    if (kv->ctx != dec->ctx) return fail(QASR_EINVAL, "KV pool belongs to another context");
     if (batch < 0 || batch > dec->cfg.max_rows)
         return fail(QASR_EINVAL, "batch %d outside [0, max_rows %d]", batch, dec->cfg.max_rows);
     if (batch == 0) return QASR_OK;
     if (!pos || !tokens_dev || !next_dev) return fail(QASR_EINVAL, "null argument");
-    DeviceScope ds(dec->ctx->device);
+    const qasr_ctx* ctx = dec->ctx;
+    if (!ctx->cos) return fail(QASR_ESTATE, "RoPE tables not set (qasr_set_rope_tables)");
+    // Every entry is checked before the first launch.
+    std::vector<int32_t> sl(batch);
+    std::vector<char> seen(kv->slots, 0);
+    for (int b = 0; b < batch; ++b) {
+        sl[b] = slots ? slots[b] : b;
+        if (sl[b] < 0 || sl[b] >= kv->slots)
+            return fail(QASR_EINVAL, "entry %d: slot %d outside [0, %d)", b, sl[b], kv->slots);
+        if (seen[sl[b]]++) return fail(QASR_EINVAL, "entry %d: slot %d appears twice", b, sl[b]);
+        if (pos[b] < 0) return fail(QASR_EINVAL, "entry %d: negative position", b);
+        if (pos[b] >= kv->cap)
+            return fail(QASR_ERANGE, "entry %d: position %d beyond KV capacity %d", b, pos[b], kv->cap);
+        if (pos[b] >= ctx->cfg.max_seq)
+            return fail(QASR_ERANGE, "entry %d: decode past max_seq %d", b, ctx->cfg.max_seq);
+        if (pos[b] >= ctx->rope_rows)
+            return fail(QASR_ERANGE, "entry %d: position %d beyond the %d RoPE table rows", b,
+                        pos[b], ctx->rope_rows);
+    }
+    DeviceScope ds(ctx->device);
     if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
-    const hipStream_t st = (hipStream_t)stream;
     int rc = bind_stream(dec, stream);
     if (rc) return rc;
-    const qasr_attn_cfg& a = dec->ctx->cfg;
-    const int hs = dec->cfg.hidden_size;
-    const int qkvdim = (a.num_attention_heads + 2 * a.num_key_value_heads) * a.head_dim;
-    // Chunk sums for a fused first norm when a skinny batch can use them.
-    dec->ss_valid = dec->fuse && batch <= kSkinnyRows && hs <= kNormMaxK;
-    hipLaunchKernelGGL(embed_rows_kernel, dim3(batch), dim3(256), 0, st, dec->embed, tokens_dev,
-                       dec->cfg.vocab_size, hs, dec->x, dec->ss_valid ? dec->ss : nullptr);
-    HIP_TRY(hipGetLastError(), "embedding launch");
-    for (int l = 0; l < a.num_hidden_layers; ++l) {
-        const qasr_layer_weights& L = dec->layers[l];
-        rc = normed_proj(dec, batch, qkvdim, L.qkv_proj, dec->x, L.input_norm, dec->qkv,
-                         L.qkv_scale);
-        if (rc) return rc;
-        rc = qasr_decode_step(dec->ctx, kv, l, batch, slots, pos, dec->qkv, L.q_norm, L.k_norm,
-                              dec->attn, stream);
-        if (rc) return rc;
-        rc = layer_tail(dec, L, batch, st);
+    // Batches past kSkinnyRows rows run as consecutive groups of at most
+    // kSkinnyRows rows: every projection then runs the kernels of a lone
+    // slot's step, so each slot's bits are those of its step alone (the
+    // reference's --batch N == --batch 1).  The weights are read once per group.
+    const int64_t vocab = dec->cfg.vocab_size;
+    for (int b0 = 0; b0 < batch; b0 += kSkinnyRows) {
+        const int nb = std::min(kSkinnyRows, batch - b0);
+        rc = step_rows(dec, kv, nb, sl.data() + b0, pos + b0, tokens_dev + b0, next_dev + b0,
+                       logits_dev ? logits_dev + b0 * vocab : nullptr, (hipStream_t)stream);
         if (rc) return rc;
     }
-    return head(dec, dec->x, batch, next_dev, logits_dev, st);
+    return QASR_OK;
 }
 
 int qasr_decoder_prefill(qasr_decoder* dec, qasr_kv* kv, int slot, int kv_start, int s,

@@ -29,8 +29,12 @@ struct SegPlan {
     int32_t row_base[kMaxBatch + 1];  // prefix sum of rows; row_base[nseg] = total
 };
 
-// Stage (b) plan: one workgroup per (batch entry, kv head, chunk of keys).
-// Workgroups of entry b are wg_base[b] .. wg_base[b+1]-1, kv-head major.
+// Stage (b) plan.  Entry b's keys are cut into granules of gran[b] keys (a
+// multiple of kDecodeGranuleQuantum, a function of len[b] only, at most
+// kDecodeMaxGranules of them); a workgroup runs `run[b]` consecutive granules
+// of one kv head.  Workgroups of entry b are wg_base[b] .. wg_base[b+1]-1,
+// kv-head major; the partial record of (entry b, kv head h, granule i) is
+// part_base[b] + h * ceil(len[b] / gran[b]) + i.
 struct DecodePlan {
     int32_t batch;
     int32_t nqh;
@@ -38,20 +42,21 @@ struct DecodePlan {
     float eps;
     int32_t slot[kMaxBatch];
     int32_t len[kMaxBatch];    // keys attended; the fused step appends key len-1
-    int32_t chunk[kMaxBatch];  // keys per workgroup of this entry
+    int32_t gran[kMaxBatch];   // keys per granule
+    int32_t run[kMaxBatch];    // granules per workgroup
     int32_t wg_base[kMaxBatch + 1];
+    int32_t part_base[kMaxBatch + 1];
 };
 
-constexpr int kDecodeWaves = 4;       // default workgroup size (waves)
+constexpr int kDecodeWaves = 4;       // workgroup size (waves)
 constexpr int kDecodeWavesPerEU = 2;  // occupancy target: <= 256 VGPRs (two pass buffers)
 constexpr int kDecodeTileKeys = 32;   // keys per wave pass
-constexpr int kDecodeMaxChunksPerEntry = 256;
-constexpr int kDecodeMinChunk = 64;    // keys (one slot at 511: 7.24 us against 7.54 at 128, 7.88 at 32)
-constexpr int kDecodeMergeBatch = 32;  // partials the merging workgroup requests per round trip
-constexpr int kDecodeMaxSplit = 16;  // chunks per entry by default (config 4: 12.28 us against 12.55 at 32)
-constexpr int kDecodeMaxItems = 8192;   // >= 4096 target + kMaxBatch * nkvh rounding slack
+constexpr int kDecodeWgKeys = kDecodeWaves * kDecodeTileKeys;  // keys per workgroup pass
+constexpr int kDecodeGranuleQuantum = 2 * kDecodeWgKeys;        // granules are multiples of this
+constexpr int kDecodeMaxGranules = 32;  // granules per entry: the merge reads them in one round trip
+constexpr int kDecodeMinGranule = 256;  // keys: the smallest granule of a default plan
 
-// Split-K workspace of one launch: per workgroup the unnormalised partial
+// Split-K workspace of one launch: per granule partial the unnormalised
 // output of both q heads (2 x 128 f32) and (max, sum) per head, plus one
 // arrival counter per (batch entry, kv head).  Counters start at zero and the
 // merging workgroup puts them back to zero.
@@ -67,12 +72,10 @@ hipError_t launch_norm_rope_append(const CacheGeom& g, int layer, const SegPlan&
                                    const f16* cos_tab, const f16* sin_tab, f16* q_out,
                                    hipStream_t stream);
 
-// waves: workgroup size in waves (4 or 8).
-hipError_t launch_decode_attn(bool fused, int waves, const CacheGeom& g, int layer,
-                              const DecodePlan& P, int total_wgs, const f16* q_or_qkv,
-                              const f16* q_gain, const f16* k_gain, const f16* cos_tab,
-                              const f16* sin_tab, f16* out, const DecodeWs& ws,
-                              hipStream_t stream);
+hipError_t launch_decode_attn(bool fused, const CacheGeom& g, int layer, const DecodePlan& P,
+                              int total_wgs, const f16* q_or_qkv, const f16* q_gain,
+                              const f16* k_gain, const f16* cos_tab, const f16* sin_tab, f16* out,
+                              const DecodeWs& ws, hipStream_t stream);
 
 struct PrefillArgs {
     const f16* q;   // [s][nqh*128], roped
@@ -87,26 +90,31 @@ struct PrefillArgs {
     float scale_log2;
 };
 
-// Stage (c) plan: row blocks of 64 rows (32 for unsplit short key ranges);
-// row block rb's key tiles (128 keys) are split into ceil(tiles / tps) pieces.  Items of a kv head are laid out
-// rb-major: item = kvh*items_per_kvh + sp_base[rb] + split.
-constexpr int kMaxRowBlocks = 64;  // 4096 rows per launch
+// Stage (c).  A prefill is cut into pieces of at most kMaxRowBlocks * 64
+// consecutive rows of one segment.  A piece's plan is a function of its rows
+// and first position only (choose_prefill_plan on the host): row blocks of 64
+// rows (32 for unsplit short key ranges), and each row block's 128-key tiles
+// split into pieces of `tps` tiles.  So a prompt's bits do not depend on what
+// else the launch carries: the one-segment entry point and the batched one
+// run the same items.
+constexpr int kMaxRowBlocks = 64;  // row blocks of one piece (4096 rows)
 constexpr int kPrefillRows = 64;
 struct PrefillPlan {
     int32_t rows_per_block;  // kPrefillRows, or kPrefillRows / 2 for unsplit short key ranges
     int32_t nrb;
     int32_t tps;
     int32_t items_per_kvh;
-    int32_t sp_base[kMaxRowBlocks + 1];
+    int32_t sp_base[kMaxRowBlocks + 1];  // row block rb's items of a kv head: sp_base[rb] ..
 };
 
 // Split workspace: per item 4 waves x (64 accumulator elements x 64 lanes of
-// unnormalised O, element-major; then m and l per lane); one counter per
-// (kv head, row block), zero at rest.
+// unnormalised O, element-major; then m and l per lane) -- a 32-row item uses
+// half of it; one arrival counter per (row block of the launch, kv head),
+// zero at rest.
 struct PrefillWs {
     float* o;
     float* ml;
-    uint32_t* counters;  // [nkvh * kMaxRowBlocks]
+    uint32_t* counters;  // [kMaxLaunchRowBlocks * nkvh]
     int64_t items;
 };
 constexpr int kPrefillWaves = 4;      // waves that own rows (2 q heads x 2 x 32 rows)
@@ -117,25 +125,36 @@ constexpr int64_t kPrefillWaveMl = 2 * 64;       // m and l of each lane
 constexpr int64_t kPrefillItemFloats = kPrefillWaves * kPrefillWaveFloats;
 constexpr int64_t kPrefillItemMl = kPrefillWaves * kPrefillWaveMl;
 
-// Several segments in one launch (no key splits): segment i's rows are q/out
-// rows row_base[i] .. +rows[i] at positions kv_start[i] ..; its K/V blocks
-// start kv_off[i] elements past PrefillArgs::k / ::v; its items (kv head
-// minor, then row block) are item_base[i] .. item_base[i+1]-1.
-constexpr int kMaxPrefillSegs = 64;
+// One launch: up to kMaxPrefillPieces pieces of one row block size.  Piece
+// i: rows[i] q/out rows from row_base[i] at positions kv_start[i] ..; its K/V
+// blocks start kv_off[i] elements past PrefillArgs::k / ::v; nrb[i] row
+// blocks and tps[i] tiles per split; sp[sp_off(i) + rb] (sp_off(i) =
+// rb_base[i] + i) is row block rb's first item within a kv head and
+// sp[sp_off(i) + nrb[i]] the items per kv head.  Its workgroups are
+// item_base[i] .. item_base[i+1]-1 (kv head minor, then row block, then
+// split); its partial records part_base[i] + kvh * items_per_kvh + item; the
+// arrival counter of (row block rb, kv head h) is (rb_base[i] + rb) * nkvh + h.
+constexpr int kMaxPrefillPieces = 64;
+constexpr int kMaxLaunchRowBlocks = 192;
 struct PrefillSegs {
     int32_t n;
-    int32_t item_base[kMaxPrefillSegs + 1];
-    int32_t kv_start[kMaxPrefillSegs];
-    int32_t rows[kMaxPrefillSegs];
-    int32_t row_base[kMaxPrefillSegs];
-    int64_t kv_off[kMaxPrefillSegs];
+    int32_t item_base[kMaxPrefillPieces + 1];
+    int32_t part_base[kMaxPrefillPieces];
+    int32_t rb_base[kMaxPrefillPieces];
+    int32_t nrb[kMaxPrefillPieces];
+    int32_t tps[kMaxPrefillPieces];
+    int32_t kv_start[kMaxPrefillPieces];
+    int32_t rows[kMaxPrefillPieces];
+    int32_t row_base[kMaxPrefillPieces];
+    int64_t kv_off[kMaxPrefillPieces];
+    int32_t sp[kMaxLaunchRowBlocks + kMaxPrefillPieces];
 };
 
 PrefillPlan plan_prefill(int s, int kv_start, int nkvh, int tiles_per_split,
                          int rows_per_block = kPrefillRows);
-hipError_t launch_prefill_attn_segs(const PrefillArgs& a, const PrefillSegs& S, hipStream_t stream);
-hipError_t launch_prefill_attn(const PrefillArgs& a, const PrefillPlan& P, const PrefillWs& ws,
-                               hipStream_t stream);
+// rows_per_block: 64 or 32, the block size every piece of S was planned with.
+hipError_t launch_prefill_attn(const PrefillArgs& a, int rows_per_block, const PrefillSegs& S,
+                               const PrefillWs& ws, hipStream_t stream);
 
 // Prefill projections (gemm.hip): C[M][N] = f16(A[M][K] . B[N][K]^T (+ C)),
 // f32 accumulation, row-major, leading dimensions K, K and N, 16-byte

@@ -254,15 +254,15 @@ __device__ __forceinline__ void step_pv(Wave& w, const f16* vt, const half8v (&p
 }
 
 // Merge of the nsp split-K partials of one wave's 32 rows (lane = query row),
-// for the accumulator elements of dim blocks 2*HALF and 2*HALF+1 (element
-// chunks 4*HALF .. 4*HALF+3 of 8): returns the merged row sum and leaves the
-// merged, unnormalised output in those two blocks of o.  The partials are
-// combined in index order whichever workgroup arrives last, so the result is
+// for accumulator element chunks C0 .. C0+NC-1 (chunk k = elements 8k .. 8k+7
+// = o[k / 2][8 (k % 2) .. +8]): returns the merged row sum and leaves the
+// merged, unnormalised output in those chunks of o.  The partials are
+// combined in split order whichever workgroup arrives last, so the result is
 // bitwise reproducible.  Pass 1: the row max M (16 m values requested per
 // memory round trip).  Pass 2: partials in groups of G, their (m, l) and, per
 // 8-element chunk, the G x 8 accumulator values requested together.  Unused
 // slots of a group read partial 0's record and drop it.
-template <int G, int HALF>
+template <int G, int C0, int NC>
 __device__ __forceinline__ float merge_partials(const float* mlw, const float* ow, int nsp,
                                                 float16v (&o)[4]) {
     float M = kNegInf;
@@ -278,9 +278,9 @@ __device__ __forceinline__ float merge_partials(const float* mlw, const float* o
         for (int u = 0; u < 16; ++u) M = fmaxf(M, mm[u]);
     }
     float Ls = 0.0f;
-    float acc[4][8];
+    float acc[NC][8];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[c][e] = 0.0f;
     for (int i0 = 0; i0 < nsp; i0 += G) {
@@ -294,13 +294,13 @@ __device__ __forceinline__ float merge_partials(const float* mlw, const float* o
             Ls = fmaf(i < nsp ? li : 0.0f, w[u], Ls);
         }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {  // element chunk 4*half + c
+        for (int c = 0; c < NC; ++c) {
             float x[G][8];
 #pragma unroll
             for (int u = 0; u < G; ++u) {
                 const int i = i0 + u;
                 const float* src =
-                    ow + (int64_t)(i < nsp ? i : 0) * kPrefillItemFloats + (4 * HALF + c) * 8 * 64;
+                    ow + (int64_t)(i < nsp ? i : 0) * kPrefillItemFloats + (C0 + c) * 8 * 64;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const float v = load_dev(src + e * 64);
@@ -314,36 +314,39 @@ __device__ __forceinline__ float merge_partials(const float* mlw, const float* o
             __builtin_amdgcn_sched_barrier(0);  // keep the next chunk's loads after this one
         }
     }
-    // Element chunk 4*HALF + c is o[2*HALF + c/2][8*(c%2) .. +8].
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[2 * HALF + (c >> 1)][8 * (c & 1) + e] = acc[c][e];
+        for (int e = 0; e < 8; ++e) o[(C0 + c) >> 1][8 * ((C0 + c) & 1) + e] = acc[c][e];
     return Ls;
 }
 
 // Kernel state the epilogue needs.
+// rec: this item's partial record; rec0: the record of split 0 of its (row
+// block, kv head) (the splits' records follow it); ctr: their arrival counter.
 struct EpiArgs {
     const PrefillArgs& a;
-    const PrefillPlan& P;
     float* ws_o;
     float* ws_ml;
-    uint32_t* counters;
+    uint32_t* ctr;
     f16* K0;
     f16* K1;
     f16* V0;
     f16* V1;
     f16* Q;
-    int item, kvh, rb, nsp, rw, r, head;
+    int64_t rec, rec0;
+    int nsp, rw, r, head;
     bool row_ok;
     int g, lane, tid;
 };
 
-// Epilogue of a 32-row block (four key groups of 32 keys per row wave, no
-// split): wave (rw, KG) finishes dim block KG.  Each wave leaves its other
-// three blocks (16 accumulator elements x 64 lanes, element-major) and its
-// (m, l) in LDS -- the tile buffers and the free half of the Q block -- and
-// combines the four partials of its block in key-group order.
+// Epilogue of a 32-row block (four key groups of 32 keys per row wave):
+// wave (rw, KG) finishes dim block KG.  Each wave leaves its other three
+// blocks (16 accumulator elements x 64 lanes, element-major) and its (m, l)
+// in LDS -- the tile buffers and the free half of the Q block -- and
+// combines the four partials of its block in key-group order.  A split key
+// range then publishes the combined block (and KG 0 its (m, l)) and the last
+// item to arrive merges the splits of its block.
 template <int KG>
 __device__ __forceinline__ void epilogue4(Wave& w, const EpiArgs& e) {
     const int lane = e.lane, rw = e.rw;
@@ -381,16 +384,46 @@ __device__ __forceinline__ void epilogue4(Wave& w, const EpiArgs& e) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[i] = fmaf(j == KG ? w.o[KG][i] : src[i * 64 + lane], aj, o[i]);
     }
-    if (!e.row_ok) return;
-    const float inv = 1.0f / L;
     f16* orow = e.a.out + (int64_t)e.r * (e.a.nqh * kHeadDim) + e.head * kHeadDim;
+    auto write_out = [&](const float16v& ob, float l) {
+        if (!e.row_ok) return;
+        const float inv = 1.0f / l;
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-        half4v h4;
+        for (int q4 = 0; q4 < 4; ++q4) {
+            half4v h4;
 #pragma unroll
-        for (int x = 0; x < 4; ++x) h4[x] = (f16)(o[q4 * 4 + x] * inv);
-        *(half4v*)(orow + KG * 32 + 8 * q4 + 4 * e.g) = h4;
+            for (int x = 0; x < 4; ++x) h4[x] = (f16)(ob[q4 * 4 + x] * inv);
+            *(half4v*)(orow + KG * 32 + 8 * q4 + 4 * e.g) = h4;
+        }
+    };
+    if (e.nsp == 1) {
+        write_out(o, L);
+        return;
     }
+    // Publish dim block KG of row wave rw (element-major, as the 64-row
+    // epilogue's records), (m, l) from key group 0; then the ticket.
+    {
+        float* po = e.ws_o + e.rec * kPrefillItemFloats + rw * kPrefillWaveFloats;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) store_dev(po + (KG * 16 + i) * 64 + lane, o[i]);
+        if (KG == 0) {
+            float* pml = e.ws_ml + e.rec * kPrefillItemMl + rw * kPrefillWaveMl;
+            store_dev(pml + lane, M);
+            store_dev(pml + 64 + lane, L);
+        }
+    }
+    int& s_last = *reinterpret_cast<int*>(e.V0 + kTileHalves - 8);
+    stores_done_barrier();
+    if (e.tid == 0) s_last = (ticket_add(e.ctr) == (uint32_t)(e.nsp - 1));
+    __syncthreads();
+    if (!s_last) return;
+    const float* mlw = e.ws_ml + e.rec0 * kPrefillItemMl + rw * kPrefillWaveMl + lane;
+    const float* ow = e.ws_o + e.rec0 * kPrefillItemFloats + rw * kPrefillWaveFloats + lane;
+    float16v om[4];
+    const float Ls = e.nsp <= 2 ? merge_partials<2, 2 * KG, 2>(mlw, ow, e.nsp, om)
+                                : merge_partials<8, 2 * KG, 2>(mlw, ow, e.nsp, om);
+    write_out(om[KG], Ls);
+    if (e.tid == 0) ticket_reset(e.ctr);
 }
 
 // Epilogue of the wave of key group KG: wave (rw, KG) keeps dim blocks 2*KG
@@ -455,43 +488,41 @@ __device__ __forceinline__ void epilogue(Wave& w, const EpiArgs& e) {
     // storing its 32; then (m, l) per lane.  Published with device-scope
     // stores (see stores_done_barrier).
     {
-        float* po = e.ws_o + (int64_t)e.item * kPrefillItemFloats + rw * kPrefillWaveFloats;
+        float* po = e.ws_o + e.rec * kPrefillItemFloats + rw * kPrefillWaveFloats;
 #pragma unroll
         for (int d = 0; d < 2; ++d)
 #pragma unroll
             for (int i = 0; i < 16; ++i) store_dev(po + ((kMine + d) * 16 + i) * 64 + lane, o[kMine + d][i]);
         if (KG == 0) {
-            float* pml = e.ws_ml + (int64_t)e.item * kPrefillItemMl + rw * kPrefillWaveMl;
+            float* pml = e.ws_ml + e.rec * kPrefillItemMl + rw * kPrefillWaveMl;
             store_dev(pml + lane, w.m);
             store_dev(pml + 64 + lane, w.l);
         }
     }
     stores_done_barrier();
-    uint32_t* ctr = &e.counters[e.kvh * e.P.nrb + e.rb];
-    if (e.tid == 0) s_last = (ticket_add(ctr) == (uint32_t)(e.nsp - 1));
+    if (e.tid == 0) s_last = (ticket_add(e.ctr) == (uint32_t)(e.nsp - 1));
     __syncthreads();
     if (!s_last) return;
 
     // Last arrival: merge the nsp partials of this (kv head, row block); each
     // wave merges its half of its row wave's 32 rows.
-    const int it0 = e.kvh * e.P.items_per_kvh + e.P.sp_base[e.rb];
-    const float* mlw = e.ws_ml + (int64_t)it0 * kPrefillItemMl + rw * kPrefillWaveMl + lane;
-    const float* ow = e.ws_o + (int64_t)it0 * kPrefillItemFloats + rw * kPrefillWaveFloats + lane;
-    const float Ls = e.nsp <= 2 ? merge_partials<2, KG>(mlw, ow, e.nsp, o)
-                                : merge_partials<8, KG>(mlw, ow, e.nsp, o);
+    const float* mlw = e.ws_ml + e.rec0 * kPrefillItemMl + rw * kPrefillWaveMl + lane;
+    const float* ow = e.ws_o + e.rec0 * kPrefillItemFloats + rw * kPrefillWaveFloats + lane;
+    const float Ls = e.nsp <= 2 ? merge_partials<2, 4 * KG, 4>(mlw, ow, e.nsp, o)
+                                : merge_partials<8, 4 * KG, 4>(mlw, ow, e.nsp, o);
     write_out(Ls);
-    if (e.tid == 0) ticket_reset(ctr);
+    if (e.tid == 0) ticket_reset(e.ctr);
 }
 
 // NKG = 2: 64-row blocks, row wave rw = wave & 3 (2 q heads x 2 x 32 rows),
 // key group kg = wave >> 2 taking keys 64 kg .. +64 of every tile.  NKG = 4
-// (unsplit short key ranges): 32-row blocks, rw = wave & 1 (the 2 q heads),
-// kg = wave >> 1 taking keys 32 kg .. +32 -- half the work per workgroup and
+// (short key ranges): 32-row blocks, rw = wave & 1 (the 2 q heads), kg =
+// wave >> 1 taking keys 32 kg .. +32 -- half the work per workgroup and
 // twice the workgroups.
-template <bool MULTI, int NKG>
+template <int NKG>
 __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
-    PrefillArgs a, PrefillPlan P, PrefillSegs S, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, uint32_t* __restrict__ counters) {
+    PrefillArgs a, PrefillSegs S, float* __restrict__ ws_o, float* __restrict__ ws_ml,
+    uint32_t* __restrict__ counters) {
     // 160 KB: K and V tiles, double buffered, and the Q block.
     __shared__ __attribute__((aligned(16))) f16 K0[kTileHalves];
     __shared__ __attribute__((aligned(16))) f16 K1[kTileHalves];
@@ -505,51 +536,38 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     constexpr int RB = 16 * kRowWaves;        // rows per block: 64 or 32
     constexpr int GK = kTileKeys / NKG;       // keys per key group and tile: 64 or 32
     constexpr int NB = GK / 32;               // 32-key MFMA blocks per step
-    static_assert(!MULTI || NKG == 2, "segment launches use 64-row blocks");
     const int wave = tid >> 6;       // 0..7: copy slot
     const int rw = wave % kRowWaves; // row wave
     const int kg = wave / kRowWaves; // key group
     const int n = lane & 31;  // query column within the wave's 32 rows
     const int g = lane >> 5;  // k-slot group of the MFMA operands
 
-    int kvh, item, rb, sp, nsp, tps;
-    if constexpr (MULTI) {
-        // Segment = number of later segment starts at or before this item
-        // (one lane per segment, a ballot); then kv head minor, row block.
-        static_assert(kMaxPrefillSegs <= 64, "one lane per segment");
-        const int seg = __popcll(__ballot(lane + 1 < S.n && S.item_base[lane + 1] <= (int)blockIdx.x));
-        const int local = blockIdx.x - S.item_base[seg];
-        kvh = local % a.nkvh;
-        rb = local / a.nkvh;
-        item = 0;  // no split: the workspace is not used
-        sp = 0;
-        nsp = 1;
-        tps = kMaxRowBlocks * kRowsPerBlock;  // every tile of the row block
-        a.s = S.rows[seg];
-        a.kv_start = S.kv_start[seg];
-        a.q += (int64_t)S.row_base[seg] * a.nqh * kHeadDim;
-        a.out += (int64_t)S.row_base[seg] * a.nqh * kHeadDim;
-        a.k += S.kv_off[seg];
-        a.v += S.kv_off[seg];
-    } else {
-        kvh = blockIdx.x % a.nkvh;
-        const int rem = blockIdx.x / a.nkvh;
-        item = kvh * P.items_per_kvh + rem;  // canonical index (workspace)
-        rb = 0;
-        int lo = 0, hi = P.nrb - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (P.sp_base[mid] <= rem) lo = mid; else hi = mid - 1;
-        }
-        rb = lo;
-        sp = rem - P.sp_base[rb];
-        nsp = P.sp_base[rb + 1] - P.sp_base[rb];
-        tps = P.tps;
-    }
+    // Piece = number of later piece starts at or before this workgroup (one
+    // lane per piece, a ballot); then kv head minor, and the row block from
+    // the piece's item table (one lane per row block, a ballot).
+    static_assert(kMaxPrefillPieces <= 64 && kMaxRowBlocks <= 64, "one lane per piece / row block");
+    const int pc = __popcll(__ballot(lane + 1 < S.n && S.item_base[lane + 1] <= (int)blockIdx.x));
+    const int local = blockIdx.x - S.item_base[pc];
+    const int kvh = local % a.nkvh;
+    const int rem = local / a.nkvh;
+    const int* sp = S.sp + S.rb_base[pc] + pc;
+    const int nrb = S.nrb[pc];
+    const int rb = __popcll(__ballot(lane + 1 < nrb && sp[lane + 1] <= rem));
+    const int split = rem - sp[rb];
+    const int nsp = sp[rb + 1] - sp[rb];
+    const int tps = S.tps[pc];
+    const int64_t rec0 = (int64_t)S.part_base[pc] + (int64_t)kvh * sp[nrb] + sp[rb];
+    uint32_t* ctr = counters + (int64_t)(S.rb_base[pc] + rb) * a.nkvh + kvh;
+    a.s = S.rows[pc];
+    a.kv_start = S.kv_start[pc];
+    a.q += (int64_t)S.row_base[pc] * a.nqh * kHeadDim;
+    a.out += (int64_t)S.row_base[pc] * a.nqh * kHeadDim;
+    a.k += S.kv_off[pc];
+    a.v += S.kv_off[pc];
     const int row0 = rb * RB;
     const int kend = a.kv_start + min(row0 + RB, a.s);  // keys < kend
     const int ntiles = (kend + kTileKeys - 1) / kTileKeys;
-    const int t_begin = sp * tps;
+    const int t_begin = split * tps;
     const int t_end = min(t_begin + tps, ntiles);
 
     const int head = kvh * kRep + (rw & 1);
@@ -648,7 +666,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     // The two key groups of a row wave combine through LDS (the tile buffers
     // are free now); from here on both waves of a pair share the epilogue
     // work half and half.
-    EpiArgs e{a, P, ws_o, ws_ml, counters, K0, K1, V0, V1, Qs, item, kvh, rb, nsp, rw, r, head, row_ok, g, lane, tid};
+    EpiArgs e{a, ws_o, ws_ml, ctr, K0, K1, V0, V1, Qs, rec0 + split, rec0, nsp, rw, r, head, row_ok, g, lane, tid};
     if constexpr (NKG == 2) {
         if (kg == 0)
             epilogue<0>(w, e);
@@ -682,31 +700,23 @@ PrefillPlan plan_prefill(int s, int kv_start, int nkvh, int tiles_per_split, int
     return P;
 }
 
-hipError_t launch_prefill_attn(const PrefillArgs& a, const PrefillPlan& P, const PrefillWs& ws,
-                               hipStream_t stream) {
-    const int items = P.items_per_kvh * a.nkvh;
-    if (items <= 0) return hipSuccess;
-    if (items > ws.items || P.nrb > kMaxRowBlocks) return hipErrorInvalidValue;
-    if (P.rows_per_block == kRowsPerBlock / 2) {
-        // 32-row blocks: unsplit items only (their epilogue has no merge).
-        if (P.items_per_kvh != P.nrb) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((prefill_attn_kernel<false, 4>), dim3(items), dim3(kThreads), 0, stream,
-                           a, P, PrefillSegs{}, ws.o, ws.ml, ws.counters);
-    } else if (P.rows_per_block == kRowsPerBlock) {
-        hipLaunchKernelGGL((prefill_attn_kernel<false, 2>), dim3(items), dim3(kThreads), 0, stream,
-                           a, P, PrefillSegs{}, ws.o, ws.ml, ws.counters);
-    } else {
-        return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
-hipError_t launch_prefill_attn_segs(const PrefillArgs& a, const PrefillSegs& S, hipStream_t stream) {
-    if (S.n <= 0 || S.n > kMaxPrefillSegs) return hipErrorInvalidValue;
+hipError_t launch_prefill_attn(const PrefillArgs& a, int rows_per_block, const PrefillSegs& S,
+                               const PrefillWs& ws, hipStream_t stream) {
+    if (S.n <= 0 || S.n > kMaxPrefillPieces) return hipErrorInvalidValue;
     const int items = S.item_base[S.n];
     if (items <= 0) return hipSuccess;
-    hipLaunchKernelGGL((prefill_attn_kernel<true, 2>), dim3(items), dim3(kThreads), 0, stream, a,
-                       PrefillPlan{}, S, nullptr, nullptr, nullptr);
+    const int last = S.n - 1;
+    const int rbs = S.rb_base[last] + S.nrb[last];
+    const int64_t recs = (int64_t)S.part_base[last] + (int64_t)a.nkvh * S.sp[S.rb_base[last] + last + S.nrb[last]];
+    if (rbs > kMaxLaunchRowBlocks || recs > ws.items) return hipErrorInvalidValue;
+    if (rows_per_block == kRowsPerBlock / 2)
+        hipLaunchKernelGGL((prefill_attn_kernel<4>), dim3(items), dim3(kThreads), 0, stream, a, S,
+                           ws.o, ws.ml, ws.counters);
+    else if (rows_per_block == kRowsPerBlock)
+        hipLaunchKernelGGL((prefill_attn_kernel<2>), dim3(items), dim3(kThreads), 0, stream, a, S,
+                           ws.o, ws.ml, ws.counters);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

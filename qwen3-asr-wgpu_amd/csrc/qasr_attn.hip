@@ -18,6 +18,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <limits>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -113,11 +114,11 @@ void free_prefill_ws(qasr_kv* kv) {
     kv->pws_items = 0;
 }
 
-// Decode workspace: one partial per workgroup of a launch (the planner keeps a
-// launch under kDecodeMaxItems workgroups) and one ticket per (entry, kv head).
+// Decode workspace: one partial per granule of a launch (at most kMaxBatch
+// entries x nkvh x kDecodeMaxGranules) and one ticket per (entry, kv head).
 int alloc_decode_ws(qasr_kv* kv) {
     const int nkvh = kv->ctx->cfg.num_key_value_heads;
-    const int64_t items = qasr::kDecodeMaxItems;
+    const int64_t items = (int64_t)qasr::kMaxBatch * nkvh * qasr::kDecodeMaxGranules;
     HIP_TRY(hipMalloc(&kv->dws_acc, items * 2 * qasr::kHeadDim * sizeof(float)), "decode workspace");
     HIP_TRY(hipMalloc(&kv->dws_ml, items * 4 * sizeof(float)), "decode workspace");
     const size_t cbytes = (size_t)qasr::kMaxBatch * nkvh * sizeof(uint32_t);
@@ -136,78 +137,100 @@ int ensure_prefill_ws(qasr_kv* kv, int64_t items) {
             "prefill workspace");
     HIP_TRY(hipMalloc(&kv->pws_ml, items * qasr::kPrefillItemMl * sizeof(float)),
             "prefill workspace");
-    const size_t cbytes = (size_t)nkvh * qasr::kMaxRowBlocks * sizeof(uint32_t);
+    const size_t cbytes = (size_t)nkvh * qasr::kMaxLaunchRowBlocks * sizeof(uint32_t);
     HIP_TRY(hipMalloc(&kv->pws_ctr, cbytes), "prefill counters");
     HIP_TRY(hipMemset(kv->pws_ctr, 0, cbytes), "prefill counters");
     kv->pws_items = items;
     return QASR_OK;
 }
 
-// Decode launch plan: a fixed number of workgroups (QASR_DECODE_WGS, default
-// one per CU), each streaming one chunk of one entry's keys for one kv head.
-// One CU streams at most ~45-70 GB/s (a bare stream measures the same), so
-// a CU cannot speed up when others finish: the launch ends at full HBM
-// rate only while enough CUs are still streaming.  So when the batch leaves
-// room to split (entries x kv heads below the budget), every entry is cut
-// into chunks of one common size C -- the smallest multiple of 32 keys that
-// fits the budget (and at least QASR_DECODE_MIN_CHUNK keys, at most
-// QASR_DECODE_MAX_SPLIT chunks per entry) -- plus a shorter last chunk, and
-// entries shorter than C stay whole.  Most workgroups then carry C keys and
-// stream until the end (config 3: 20.1 against 21.0 us for equal chunks
-// within each entry, the plan before).  Batches at or past the budget split
-// their longest entries while a chunk exceeds 1.5x the average keys per
-// workgroup; the extra workgroups run as the first ones finish.
-int chunk_of(int L, int n) {
-    const int c = (L + n - 1) / n;
-    return (c + qasr::kDecodeTileKeys - 1) / qasr::kDecodeTileKeys * qasr::kDecodeTileKeys;
+// Decode launch plan, in two parts.
+//
+// 1. Granules: entry b's keys are cut into granules of G(len[b]) keys, the
+//    smallest multiple of 256 (two workgroup passes) that is at least
+//    QASR_DECODE_GRANULE (default 256) keys and leaves at most
+//    QASR_DECODE_MAX_GRANULES (default and limit 32) granules.  Every granule
+//    yields one partial and the partials merge in granule order, so an
+//    entry's output bits are a function of its own length and keys: batch
+//    composition, slot order and the device's CU count never change them
+//    (the reference's --batch N == --batch 1, decoder.rs:1930-1931).
+// 2. Runs: which workgroup runs which granules.  A workgroup takes `run`
+//    consecutive granules of one (entry, kv head).  One CU streams at most
+//    ~50-75 GB/s, so a launch runs at HBM rate only while most CUs stream:
+//    the plan aims at QASR_DECODE_WGS workgroups (default one per CU) that
+//    carry about the same number of keys.  When the batch leaves room
+//    (entries x kv heads below the budget), the smallest per-workgroup key
+//    budget C (a multiple of 256) is found for which runs of floor(C / G)
+//    granules (at least one) fit the budget.  Batches at or past the budget
+//    start from one workgroup per (entry, kv head) and split the run with
+//    the most keys while it exceeds 1.5x the average keys per workgroup; the
+//    extra workgroups run as the first ones finish.
+int granule_keys(int L, int gmin, int gmax) {
+    const int64_t want = std::max<int64_t>(gmin, ((int64_t)L + gmax - 1) / gmax);
+    const int64_t q = qasr::kDecodeGranuleQuantum;
+    return (int)((want + q - 1) / q * q);
 }
 
-void plan_decode_chunks(qasr::DecodePlan& P, int nkvh, int cus) {
-    const int target = std::max(1, std::min(env_int("QASR_DECODE_WGS", cus), 4096));
-    const int min_chunk = std::max(32, env_int("QASR_DECODE_MIN_CHUNK", qasr::kDecodeMinChunk));
-    const int max_split = std::max(1, std::min(env_int("QASR_DECODE_MAX_SPLIT", qasr::kDecodeMaxSplit),
-                                               qasr::kDecodeMaxChunksPerEntry));
-    int n[qasr::kMaxBatch];  // chunks per entry (greedy plan)
-    int wgs = 0;
+int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Keys of one workgroup's run at most: its K/V buffer ranges stay below 1 GB.
+constexpr int kMaxRunKeys = 1 << 22;
+
+void plan_decode_granules(qasr::DecodePlan& P, int nkvh, int cus) {
+    const int target = std::max(1, std::min(env_int("QASR_DECODE_WGS", cus), 8192));
+    const int gmin = std::max(qasr::kDecodeGranuleQuantum, env_int("QASR_DECODE_GRANULE", qasr::kDecodeMinGranule));
+    const int gmax = std::max(1, std::min(env_int("QASR_DECODE_MAX_GRANULES", qasr::kDecodeMaxGranules),
+                                          qasr::kDecodeMaxGranules));
+    int ngr[qasr::kMaxBatch], run[qasr::kMaxBatch];
+    int64_t keys = 0;
+    int pairs = 0;
     for (int i = 0; i < P.batch; ++i) {
-        n[i] = 1;
-        wgs += nkvh;
+        P.gran[i] = granule_keys(P.len[i], gmin, gmax);
+        ngr[i] = ceil_div(P.len[i], P.gran[i]);
+        run[i] = std::max(1, std::min(ngr[i], kMaxRunKeys / P.gran[i]));
+        keys += (int64_t)nkvh * P.len[i];
+        pairs += nkvh;
     }
-    int common = 0;  // C of the common-size plan, 0 for the greedy plan
-    if (wgs < target) {
-        int c = chunk_of(min_chunk, 1);
-        for (int i = 0; i < P.batch; ++i) c = std::max(c, chunk_of(P.len[i], max_split));
-        auto items = [&](int cc) {
+    if (pairs < target) {
+        auto runs_for = [&](int64_t c, int i) {
+            return (int)std::max<int64_t>(1, std::min<int64_t>(run[i], c / P.gran[i]));
+        };
+        auto wgs_for = [&](int64_t c) {
             int64_t t = 0;
-            for (int i = 0; i < P.batch; ++i) t += (int64_t)nkvh * ((P.len[i] + cc - 1) / cc);
+            for (int i = 0; i < P.batch; ++i) t += (int64_t)nkvh * ceil_div(ngr[i], runs_for(c, i));
             return t;
         };
-        while (items(c) > target) c += qasr::kDecodeTileKeys;
-        common = c;
+        int64_t c = qasr::kDecodeGranuleQuantum;
+        int64_t cmax = 0;
+        for (int i = 0; i < P.batch; ++i) cmax = std::max<int64_t>(cmax, (int64_t)ngr[i] * P.gran[i]);
+        while (c < cmax && wgs_for(c) > target) c += qasr::kDecodeGranuleQuantum;
+        for (int i = 0; i < P.batch; ++i) run[i] = runs_for(c, i);
     } else {
-        int64_t keys = 0;
-        for (int i = 0; i < P.batch; ++i) keys += (int64_t)nkvh * P.len[i];
-        while (wgs + nkvh <= qasr::kDecodeMaxItems / 2) {
-            int best = -1, best_chunk = 0;
-            for (int i = 0; i < P.batch; ++i) {
-                const int c = chunk_of(P.len[i], n[i]);
-                if (n[i] < max_split && chunk_of(P.len[i], n[i] + 1) >= min_chunk &&
-                    c > best_chunk) {
+        int wgs = 0;
+        for (int i = 0; i < P.batch; ++i) wgs += nkvh * ceil_div(ngr[i], run[i]);
+        const int max_wgs = 4 * std::max(target, pairs);
+        auto run_keys = [&](int i) { return std::min<int64_t>((int64_t)run[i] * P.gran[i], P.len[i]); };
+        while (wgs + nkvh <= max_wgs) {
+            int best = -1;
+            int64_t best_keys = 0;
+            for (int i = 0; i < P.batch; ++i)
+                if (run[i] > 1 && run_keys(i) > best_keys) {
                     best = i;
-                    best_chunk = c;
+                    best_keys = run_keys(i);
                 }
-            }
-            if (best < 0 || 2 * (int64_t)best_chunk * wgs <= 3 * keys) break;
-            ++n[best];
-            wgs += nkvh;
+            if (best < 0 || 2 * best_keys * wgs <= 3 * keys) break;
+            const int nw = ceil_div(ngr[best], run[best]);
+            const int r = std::min(run[best] - 1, ceil_div(ngr[best], nw + 1));  // run shrinks every time
+            wgs += nkvh * (ceil_div(ngr[best], r) - nw);
+            run[best] = r;
         }
     }
     P.wg_base[0] = 0;
+    P.part_base[0] = 0;
     for (int i = 0; i < P.batch; ++i) {
-        const int L = P.len[i];
-        const int chunk = common ? std::min(common, chunk_of(L, 1)) : chunk_of(L, n[i]);
-        P.chunk[i] = chunk;
-        P.wg_base[i + 1] = P.wg_base[i] + nkvh * ((L + chunk - 1) / chunk);
+        P.run[i] = run[i];
+        P.wg_base[i + 1] = P.wg_base[i] + nkvh * ceil_div(ngr[i], run[i]);
+        P.part_base[i + 1] = P.part_base[i] + nkvh * ngr[i];
     }
 }
 
@@ -240,11 +263,10 @@ int run_decode(bool fused, qasr_ctx* ctx, qasr_kv* kv, int layer, int batch, con
             P.slot[i] = slots ? slots[b0 + i] : b0 + i;
             P.len[i] = lens[b0 + i];
         }
-        plan_decode_chunks(P, nkvh, ctx->cus);
+        plan_decode_granules(P, nkvh, ctx->cus);
         const f16* qp = (const f16*)qin + b0 * in_row;
         f16* op = (f16*)out + b0 * out_row;
-        const int waves = env_int("QASR_DECODE_WAVES", qasr::kDecodeWaves);
-        hipError_t e = qasr::launch_decode_attn(fused, waves, g, layer, P, P.wg_base[nb], qp,
+        hipError_t e = qasr::launch_decode_attn(fused, g, layer, P, P.wg_base[nb], qp,
                                                 (const f16*)q_gain, (const f16*)k_gain, ctx->cos,
                                                 ctx->sin, op, ws, (hipStream_t)stream);
         if (e != hipSuccess) return hip_fail(e, "decode attention launch");
@@ -252,20 +274,20 @@ int run_decode(bool fused, qasr_ctx* ctx, qasr_kv* kv, int layer, int batch, con
     return QASR_OK;
 }
 
-// ---- prefill: planning shared by the allocating and the no-allocation entry
+// ---- prefill: planning shared by every prefill entry point ----------------
 
 // Split workspace of qasr_prefill_attn_noalloc, for callers that cannot
 // allocate (HIP graph capture, serving loops, harnesses that forbid it): a
 // file-scope device array, one copy per GPU, alive until the process ends.
-// Partials of at most kScratchItems work items (17.3 MB) plus the arrival
+// Partials of at most kScratchItems work items (34 MB) plus the arrival
 // counters.  Host code reaches it only through the address resolved per
 // device by hipGetSymbolAddress (scratch_ptr); the array's name is a host
 // stand-in, not a device address.
-constexpr int64_t kScratchItems = 256;
+constexpr int64_t kScratchItems = 512;
 constexpr int kScratchMaxKvHeads = 16;  // nkvh <= 16 (qasr_ctx_create's head limit)
 constexpr int64_t kScratchO = kScratchItems * qasr::kPrefillItemFloats;
 constexpr int64_t kScratchMl = kScratchItems * qasr::kPrefillItemMl;
-constexpr int64_t kScratchCounters = (int64_t)kScratchMaxKvHeads * qasr::kMaxRowBlocks;
+constexpr int64_t kScratchCounters = (int64_t)kScratchMaxKvHeads * qasr::kMaxLaunchRowBlocks;
 static __device__ __align__(256) float scratch[kScratchO + kScratchMl + kScratchCounters];
 
 constexpr int kMaxDevices = 64;
@@ -295,20 +317,24 @@ __global__ void zero_u32_kernel(uint32_t* p, int n) {
     if (i < n) p[i] = 0u;
 }
 
-// Longest prefill one qasr_prefill_attn_noalloc call takes: every row block
-// of the launch must have at least one work item in the scratch array.
+// Longest prefill one qasr_prefill_attn_noalloc call takes.  A default plan
+// of r rows has at most 256 + nkvh * ceil(r / 64) work items (tiles per split
+// are chosen for about 256 items; each row block adds at most one by
+// rounding), so up to this many rows every default plan fits the scratch
+// array, and the no-allocation call runs exactly qasr_prefill_attn's items.
 int noalloc_max_rows(int nkvh) {
-    return qasr::kPrefillRows * (int)std::min<int64_t>(qasr::kMaxRowBlocks, kScratchItems / nkvh);
+    const int64_t rbs = std::min<int64_t>(qasr::kMaxRowBlocks, (kScratchItems - 256) / nkvh);
+    return qasr::kPrefillRows * (int)rbs;
 }
 
-// The plan of one prefill launch of `rows` (<= kMaxRowBlocks * kPrefillRows)
-// rows at kv_start `ks`.  Tiles per split: about one workgroup per CU (256),
-// without splitting row blocks whose key range is short.  A split's merge
-// (publish, ticket, read back) is about three memory round trips, as long as
-// several latency-bound tiles: key ranges of up to kPrefillNoSplitTiles tiles
-// are never split.  Unsplit short ranges also take 32-row blocks: twice the
-// workgroups, half the work on the longest one.  A forced split count
-// (tps_forced > 0, QASR_PREFILL_TPS) keeps 64-row blocks.
+// The plan of one piece of `rows` (<= kMaxRowBlocks * kPrefillRows) rows at
+// kv_start `ks`, a function of (rows, ks, nkvh) alone.  Tiles per split:
+// about 256 work items, without splitting row blocks whose key range is
+// short.  A split's merge (publish, ticket, read back) is about three memory
+// round trips, as long as several latency-bound tiles: key ranges of up to
+// kPrefillNoSplitTiles tiles are never split.  Unsplit short ranges also take
+// 32-row blocks: twice the workgroups, half the work on the longest one.  A
+// forced split count (tps_forced > 0, QASR_PREFILL_TPS) keeps 64-row blocks.
 qasr::PrefillPlan choose_prefill_plan(int rows, int ks, int nkvh, int tps_forced) {
     const int nrb = (rows + qasr::kPrefillRows - 1) / qasr::kPrefillRows;
     const int max_tiles = (ks + rows + qasr::kPrefillTileKeys - 1) / qasr::kPrefillTileKeys;
@@ -327,89 +353,157 @@ qasr::PrefillPlan choose_prefill_plan(int rows, int ks, int nkvh, int tps_forced
     return qasr::plan_prefill(rows, ks, nkvh, tps, rb_rows);
 }
 
-int run_prefill(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, int s,
-                const void* q_dev, void* out_dev, void* stream, bool noalloc) {
+// One piece: up to kMaxRowBlocks * kPrefillRows rows of one segment.
+struct Piece {
+    int slot, ks, rows;
+    int64_t row_base;
+    qasr::PrefillPlan P;
+};
+
+// One launch: pieces [first, first + n) of a list, all of one row block size.
+struct PrefillLaunch {
+    qasr::PrefillSegs S;
+    int rows_per_block;
+    int64_t records;
+};
+
+// Causal prefill attention of nseg segments (rows concatenated in segment
+// order in q / out).  Every segment is cut into pieces of at most 4096 rows
+// and every piece planned by choose_prefill_plan, so a segment runs the same
+// work items (and so gets the same bits) whether it comes alone or with
+// others.  Pieces of one row block size are packed into launches of at most
+// kMaxPrefillPieces pieces, kMaxLaunchRowBlocks row blocks and `cap` partial
+// records.  Every check runs before the first launch.
+int run_prefill_segments(qasr_ctx* ctx, qasr_kv* kv, int layer, const qasr_segment* segs,
+                         int nseg, const void* q_dev, void* out_dev, void* stream, bool noalloc) {
     int rc = check_common(ctx, kv, layer);
     if (rc) return rc;
-    if (slot < 0 || slot >= kv->slots)
-        return fail(QASR_EINVAL, "slot %d outside [0, %d)", slot, kv->slots);
-    if (kv_start < 0 || s < 0) return fail(QASR_EINVAL, "negative kv_start / s");
-    if (s == 0) return QASR_OK;
-    if (!q_dev || !out_dev) return fail(QASR_EINVAL, "null device pointer");
-    const int64_t end = (int64_t)kv_start + s;
-    if (end > ctx->cfg.max_seq)
-        return fail(QASR_ERANGE, "prefill needs %lld positions, max_seq is %d", (long long)end,
-                    ctx->cfg.max_seq);
-    if (end > kv->cap)
-        return fail(QASR_ERANGE, "prefill needs %lld positions, KV capacity is %d",
-                    (long long)end, kv->cap);
+    if (nseg < 0 || (nseg > 0 && !segs)) return fail(QASR_EINVAL, "bad segment list");
     const qasr_attn_cfg& c = ctx->cfg;
     const int nqh = c.num_attention_heads, nkvh = c.num_key_value_heads;
+    int64_t total = 0;
+    for (int i = 0; i < nseg; ++i) {
+        const qasr_segment& g = segs[i];
+        if (g.slot < 0 || g.slot >= kv->slots)
+            return fail(QASR_EINVAL, "segment %d: slot %d outside [0, %d)", i, g.slot, kv->slots);
+        if (g.pos0 < 0 || g.rows < 0) return fail(QASR_EINVAL, "segment %d: negative kv_start/rows", i);
+        const int64_t end = (int64_t)g.pos0 + g.rows;
+        if (end > c.max_seq)
+            return fail(QASR_ERANGE, "segment %d: prefill needs %lld positions, max_seq is %d", i,
+                        (long long)end, c.max_seq);
+        if (end > kv->cap)
+            return fail(QASR_ERANGE, "segment %d: prefill needs %lld positions, KV capacity is %d",
+                        i, (long long)end, kv->cap);
+        total += g.rows;
+    }
+    if (total == 0) return QASR_OK;
+    if (!q_dev || !out_dev) return fail(QASR_EINVAL, "null device pointer");
     if (noalloc) {
         if (nkvh > kScratchMaxKvHeads)
             return fail(QASR_EINVAL, "%d kv heads: the no-allocation prefill takes at most %d",
                         nkvh, kScratchMaxKvHeads);
-        if (s > noalloc_max_rows(nkvh))
-            return fail(QASR_EINVAL, "%d rows: the no-allocation prefill takes at most %d rows per "
-                        "call (prefill longer prompts in chunks, kv_start > 0)", s,
+        if (total > noalloc_max_rows(nkvh))
+            return fail(QASR_EINVAL, "%lld rows: the no-allocation prefill takes at most %d rows per "
+                        "call (prefill longer prompts in chunks, kv_start > 0)", (long long)total,
                         noalloc_max_rows(nkvh));
         if (!ctx->scratch) return fail(QASR_ESTATE, "context has no prefill scratch address");
     }
+    const int tps_forced = env_int("QASR_PREFILL_TPS", 0);
+    const int piece_rows = qasr::kMaxRowBlocks * qasr::kPrefillRows;
+    std::vector<Piece> pieces;
+    int64_t r0 = 0;
+    for (int i = 0; i < nseg; ++i) {
+        for (int p0 = 0; p0 < segs[i].rows; p0 += piece_rows) {
+            Piece pc;
+            pc.slot = segs[i].slot;
+            pc.ks = segs[i].pos0 + p0;
+            pc.rows = std::min(piece_rows, segs[i].rows - p0);
+            pc.row_base = r0 + p0;
+            pc.P = choose_prefill_plan(pc.rows, pc.ks, nkvh, tps_forced);
+            pieces.push_back(pc);
+        }
+        r0 += segs[i].rows;
+    }
+    const qasr::CacheGeom g = geom(kv);
+    const int64_t cap = noalloc ? kScratchItems : std::numeric_limits<int64_t>::max();
+    std::vector<PrefillLaunch> launches;
+    for (const int rpb : {qasr::kPrefillRows, qasr::kPrefillRows / 2}) {
+        PrefillLaunch* L = nullptr;
+        for (const Piece& pc : pieces) {
+            if (pc.P.rows_per_block != rpb) continue;
+            const int64_t recs = (int64_t)nkvh * pc.P.items_per_kvh;
+            if (recs > cap)
+                return fail(QASR_EINVAL, "prefill plan of %lld items exceeds the scratch's %lld",
+                            (long long)recs, (long long)cap);
+            if (L) {
+                const qasr::PrefillSegs& S = L->S;
+                const int rbs = S.rb_base[S.n - 1] + S.nrb[S.n - 1];
+                if (S.n == qasr::kMaxPrefillPieces || rbs + pc.P.nrb > qasr::kMaxLaunchRowBlocks ||
+                    L->records + recs > cap)
+                    L = nullptr;
+            }
+            if (!L) {
+                launches.emplace_back();
+                L = &launches.back();
+                std::memset(&L->S, 0, sizeof L->S);
+                L->rows_per_block = rpb;
+                L->records = 0;
+            }
+            qasr::PrefillSegs& S = L->S;
+            const int i = S.n;
+            const int rb0 = i ? S.rb_base[i - 1] + S.nrb[i - 1] : 0;
+            S.rb_base[i] = rb0;
+            S.nrb[i] = pc.P.nrb;
+            S.tps[i] = pc.P.tps;
+            S.kv_start[i] = pc.ks;
+            S.rows[i] = pc.rows;
+            S.row_base[i] = (int32_t)pc.row_base;
+            S.kv_off[i] = (int64_t)pc.slot * g.slot_stride + (int64_t)layer * g.layer_stride;
+            S.part_base[i] = (int32_t)L->records;
+            for (int rb = 0; rb <= pc.P.nrb; ++rb) S.sp[rb0 + i + rb] = pc.P.sp_base[rb];
+            S.item_base[i + 1] = S.item_base[i] + (int32_t)recs;
+            S.n = i + 1;
+            L->records += recs;
+        }
+    }
+    if (total > INT32_MAX / (nqh * qasr::kHeadDim))
+        return fail(QASR_EINVAL, "%lld prefill rows exceed the row index range", (long long)total);
+    int64_t need = 0;
+    for (const PrefillLaunch& L : launches) need = std::max(need, L.records);
     DeviceScope ds(ctx->device);
     if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
-    const qasr::CacheGeom g = geom(kv);
-    const int64_t ld = (int64_t)nqh * qasr::kHeadDim;
-    const int rows_per_launch = qasr::kMaxRowBlocks * qasr::kPrefillRows;
-    const int tps_forced = env_int("QASR_PREFILL_TPS", 0);
-    qasr::PrefillWs fixed{};
+    qasr::PrefillWs ws{};
     if (noalloc) {
-        fixed.o = ctx->scratch;
-        fixed.ml = ctx->scratch + kScratchO;
-        fixed.counters = reinterpret_cast<uint32_t*>(ctx->scratch + kScratchO + kScratchMl);
-        fixed.items = kScratchItems;
+        ws.o = ctx->scratch;
+        ws.ml = ctx->scratch + kScratchO;
+        ws.counters = reinterpret_cast<uint32_t*>(ctx->scratch + kScratchO + kScratchMl);
+        ws.items = kScratchItems;
+    } else {
+        rc = ensure_prefill_ws(kv, need);
+        if (rc) return rc;
+        ws = qasr::PrefillWs{kv->pws_o, kv->pws_ml, kv->pws_ctr, kv->pws_items};
+    }
+    if (noalloc) {
         // The array keeps the last call's contents: the arrival counters
         // start this call at zero.
-        const int n = nkvh * qasr::kMaxRowBlocks;
+        const int n = nkvh * qasr::kMaxLaunchRowBlocks;
         hipLaunchKernelGGL(zero_u32_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream,
-                           fixed.counters, n);
+                           ws.counters, n);
         HIP_TRY(hipGetLastError(), "scratch counter clear");
     }
-    for (int r0 = 0; r0 < s; r0 += rows_per_launch) {
-        const int rows = std::min(rows_per_launch, s - r0);
-        const int ks = kv_start + r0;
-        const int max_tiles = (ks + rows + qasr::kPrefillTileKeys - 1) / qasr::kPrefillTileKeys;
-        qasr::PrefillPlan P = choose_prefill_plan(rows, ks, nkvh, tps_forced);
-        int tps = P.tps;
-        const int rb_rows = P.rows_per_block;
-        if (noalloc) {
-            // Coarser splits until the partials fit the scratch array; at
-            // tps = max_tiles every row block is one item (s is bounded so
-            // that this fits).
-            while ((int64_t)P.items_per_kvh * nkvh > kScratchItems && tps < max_tiles) {
-                tps = std::min(max_tiles, tps * 2);
-                P = qasr::plan_prefill(rows, ks, nkvh, tps, rb_rows);
-            }
-            if ((int64_t)P.items_per_kvh * nkvh > kScratchItems)
-                return fail(QASR_EINVAL, "prefill plan of %lld items exceeds the scratch's %lld",
-                            (long long)P.items_per_kvh * nkvh, (long long)kScratchItems);
-        } else {
-            rc = ensure_prefill_ws(kv, (int64_t)P.items_per_kvh * nkvh);
-            if (rc) return rc;
-        }
-        qasr::PrefillArgs a;
-        a.q = (const f16*)q_dev + r0 * ld;
-        a.out = (f16*)out_dev + r0 * ld;
-        a.k = g.base + slot * g.slot_stride + layer * g.layer_stride;
-        a.v = a.k + g.kv_stride;
-        a.head_stride = g.head_stride;
-        a.nqh = nqh;
-        a.nkvh = nkvh;
-        a.s = rows;
-        a.kv_start = ks;
-        a.scale_log2 = ctx->scale_log2;
-        const qasr::PrefillWs ws =
-            noalloc ? fixed : qasr::PrefillWs{kv->pws_o, kv->pws_ml, kv->pws_ctr, kv->pws_items};
-        hipError_t e = qasr::launch_prefill_attn(a, P, ws, (hipStream_t)stream);
+    qasr::PrefillArgs a;
+    a.q = (const f16*)q_dev;
+    a.out = (f16*)out_dev;
+    a.k = g.base;
+    a.v = g.base + g.kv_stride;
+    a.head_stride = g.head_stride;
+    a.nqh = nqh;
+    a.nkvh = nkvh;
+    a.s = 0;
+    a.kv_start = 0;
+    a.scale_log2 = ctx->scale_log2;
+    for (const PrefillLaunch& L : launches) {
+        const hipError_t e = qasr::launch_prefill_attn(a, L.rows_per_block, L.S, ws, (hipStream_t)stream);
         if (e != hipSuccess) return hip_fail(e, "prefill attention launch");
     }
     return QASR_OK;
@@ -776,95 +870,27 @@ int qasr_decode_step(qasr_ctx* ctx, qasr_kv* kv, int layer, int batch, const int
 
 int qasr_prefill_attn(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start, int s,
                       const void* q_dev, void* out_dev, void* stream) {
-    return run_prefill(ctx, kv, layer, slot, kv_start, s, q_dev, out_dev, stream, false);
+    const qasr_segment seg{slot, kv_start, s};
+    return run_prefill_segments(ctx, kv, layer, &seg, 1, q_dev, out_dev, stream, false);
 }
 
 int qasr_prefill_attn_noalloc(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_start,
                               int s, const void* q_dev, void* out_dev, void* stream) {
-    return run_prefill(ctx, kv, layer, slot, kv_start, s, q_dev, out_dev, stream, true);
+    const qasr_segment seg{slot, kv_start, s};
+    return run_prefill_segments(ctx, kv, layer, &seg, 1, q_dev, out_dev, stream, true);
 }
-
-// Longest key range (kv_start + rows) of a segment that a one-launch batched
-// prefill takes: each row block's keys are then one workgroup's work.
-constexpr int kPrefillOneLaunchKeys = 2048;
 
 int qasr_prefill_attn_batch(qasr_ctx* ctx, qasr_kv* kv, int layer, const qasr_segment* segs,
                             int nseg, const void* q_dev, void* out_dev, void* stream) {
-    int rc = check_common(ctx, kv, layer);
-    if (rc) return rc;
-    if (nseg < 0 || (nseg > 0 && !segs)) return fail(QASR_EINVAL, "bad segment list");
-    if (nseg == 0) return QASR_OK;
-    if (!q_dev || !out_dev) return fail(QASR_EINVAL, "null device pointer");
-    // Every segment checked before any launch.  One launch takes them all
-    // when each key range is short enough to be one workgroup's per row
-    // block (no split); otherwise one launch per segment, which splits long
-    // key ranges across workgroups.
-    bool one_launch = nseg > 1 && nseg <= qasr::kMaxPrefillSegs;
-    for (int i = 0; i < nseg; ++i) {
-        const qasr_segment& g = segs[i];
-        if (g.slot < 0 || g.slot >= kv->slots)
-            return fail(QASR_EINVAL, "segment %d: slot %d outside [0, %d)", i, g.slot, kv->slots);
-        if (g.pos0 < 0 || g.rows < 0) return fail(QASR_EINVAL, "segment %d: negative kv_start/rows", i);
-        const int64_t end = (int64_t)g.pos0 + g.rows;
-        if (end > ctx->cfg.max_seq)
-            return fail(QASR_ERANGE, "segment %d: prefill needs %lld positions, max_seq is %d", i,
-                        (long long)end, ctx->cfg.max_seq);
-        if (end > kv->cap)
-            return fail(QASR_ERANGE, "segment %d: prefill needs %lld positions, KV capacity is %d",
-                        i, (long long)end, kv->cap);
-        if (end > kPrefillOneLaunchKeys || g.rows > qasr::kMaxRowBlocks * qasr::kPrefillRows)
-            one_launch = false;
-    }
-    const int64_t ld = (int64_t)ctx->cfg.num_attention_heads * qasr::kHeadDim;
-    if (!one_launch) {
-        int64_t r0 = 0;
-        for (int i = 0; i < nseg; ++i) {
-            rc = qasr_prefill_attn(ctx, kv, layer, segs[i].slot, segs[i].pos0, segs[i].rows,
-                                   (const f16*)q_dev + r0 * ld, (f16*)out_dev + r0 * ld, stream);
-            if (rc) return rc;
-            r0 += segs[i].rows;
-        }
-        return QASR_OK;
-    }
-    DeviceScope ds(ctx->device);
-    if (ds.err != hipSuccess) return hip_fail(ds.err, "hipSetDevice");
-    const qasr_attn_cfg& c = ctx->cfg;
-    const qasr::CacheGeom g = geom(kv);
-    qasr::PrefillSegs S{};
-    S.n = nseg;
-    S.item_base[0] = 0;
-    int32_t r0 = 0;
-    for (int i = 0; i < nseg; ++i) {
-        const int nrb = (segs[i].rows + qasr::kPrefillRows - 1) / qasr::kPrefillRows;
-        S.item_base[i + 1] = S.item_base[i] + c.num_key_value_heads * nrb;
-        S.kv_start[i] = segs[i].pos0;
-        S.rows[i] = segs[i].rows;
-        S.row_base[i] = r0;
-        S.kv_off[i] = (int64_t)segs[i].slot * g.slot_stride + (int64_t)layer * g.layer_stride;
-        r0 += segs[i].rows;
-    }
-    qasr::PrefillArgs a;
-    a.q = (const f16*)q_dev;
-    a.out = (f16*)out_dev;
-    a.k = g.base;
-    a.v = g.base + g.kv_stride;
-    a.head_stride = g.head_stride;
-    a.nqh = c.num_attention_heads;
-    a.nkvh = c.num_key_value_heads;
-    a.s = 0;
-    a.kv_start = 0;
-    a.scale_log2 = ctx->scale_log2;
-    const hipError_t e = qasr::launch_prefill_attn_segs(a, S, (hipStream_t)stream);
-    if (e != hipSuccess) return hip_fail(e, "prefill attention launch");
-    return QASR_OK;
+    return run_prefill_segments(ctx, kv, layer, segs, nseg, q_dev, out_dev, stream, false);
 }
 
-int qasr_plan_decode(int batch, const int32_t* lens, int nkvh, int cus, int32_t* chunk_out,
-                     int32_t* wg_base_out) {
+int qasr_plan_decode(int batch, const int32_t* lens, int nkvh, int cus, int32_t* gran_out,
+                     int32_t* run_out, int32_t* wg_base_out) {
     if (batch < 1 || batch > qasr::kMaxBatch)
         return fail(QASR_EINVAL, "batch %d outside [1, %d]", batch, qasr::kMaxBatch);
     if (nkvh < 1 || nkvh > 64 || cus < 1) return fail(QASR_EINVAL, "nkvh %d / cus %d", nkvh, cus);
-    if (!lens || !chunk_out || !wg_base_out) return fail(QASR_EINVAL, "null pointer");
+    if (!lens || !gran_out || !run_out || !wg_base_out) return fail(QASR_EINVAL, "null pointer");
     qasr::DecodePlan P{};
     P.batch = batch;
     for (int b = 0; b < batch; ++b) {
@@ -872,8 +898,11 @@ int qasr_plan_decode(int batch, const int32_t* lens, int nkvh, int cus, int32_t*
             return fail(QASR_EINVAL, "entry %d attends %d keys (at most %d)", b, lens[b], kMaxPositions);
         P.len[b] = lens[b];
     }
-    plan_decode_chunks(P, nkvh, cus);
-    for (int b = 0; b < batch; ++b) chunk_out[b] = P.chunk[b];
+    plan_decode_granules(P, nkvh, cus);
+    for (int b = 0; b < batch; ++b) {
+        gran_out[b] = P.gran[b];
+        run_out[b] = P.run[b];
+    }
     for (int b = 0; b <= batch; ++b) wg_base_out[b] = P.wg_base[b];
     return QASR_OK;
 }

@@ -155,7 +155,7 @@ def load(path: str = LIB_PATH):
     L.qasr_mfma_probe.argtypes = [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                   ctypes.c_int, _vp, _vp, _vp]
     i32p = ctypes.POINTER(ctypes.c_int32)
-    L.qasr_plan_decode.argtypes = [ctypes.c_int, i32p, ctypes.c_int, ctypes.c_int, i32p, i32p]
+    L.qasr_plan_decode.argtypes = [ctypes.c_int, i32p, ctypes.c_int, ctypes.c_int, i32p, i32p, i32p]
     L.qasr_plan_prefill.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, i32p, i32p, i32p, i32p]
     _lib = L
     return L
@@ -563,15 +563,16 @@ def mfma_probe(ctx: Context, mode: int, wgs: int, waves: int, mfma_iters: int, v
 
 
 def plan_decode(lens, nkvh: int = 8, cus: int = 256):
-    """The decode split plan the library launches for entries attending
-    lens[b] keys (qasr_plan_decode; host only, no device): (chunk keys per
-    workgroup of each entry, workgroup bases [batch + 1])."""
+    """The decode plan the library launches for entries attending lens[b]
+    keys (qasr_plan_decode; host only, no device): (keys per granule of each
+    entry, granules per workgroup of each entry, workgroup bases [batch + 1])."""
     n = len(lens)
     arr = (ctypes.c_int32 * max(1, n))(*[int(x) for x in lens])
-    chunk = (ctypes.c_int32 * max(1, n))()
+    gran = (ctypes.c_int32 * max(1, n))()
+    run = (ctypes.c_int32 * max(1, n))()
     base = (ctypes.c_int32 * (n + 1))()
-    _check(load().qasr_plan_decode(n, arr, nkvh, cus, chunk, base))
-    return list(chunk[:n]), list(base)
+    _check(load().qasr_plan_decode(n, arr, nkvh, cus, gran, run, base))
+    return list(gran[:n]), list(run[:n]), list(base)
 
 
 def plan_prefill(rows: int, kv_start: int, nkvh: int = 8):

@@ -1,6 +1,6 @@
 // sanitize_planners.cpp -- host sanitizer driver for the library's launch
 // planners (qasr_plan_decode, qasr_plan_prefill).  Built by
-// `python qwen3-asr-wgpu_amd/sanitize_planners.py`: every source's host code
+// `python tests/sanitize_planners.py`: every source's host code
 // with AddressSanitizer and UndefinedBehaviorSanitizer (device code as
 // usual), linked into one executable with this file.  No device is touched:
 // the planners are host code.  It drives them over random batches, the edge
@@ -36,25 +36,29 @@ int uniform(int lo, int hi) { return lo + (int)(next_u64() % (uint64_t)(hi - lo 
 
 constexpr int kMaxPos = 1 << 24;
 
-// Every key of every entry in exactly one chunk; chunks are whole 32-key
-// passes; bases add up.
+// Every key of every entry in exactly one granule, granules whole
+// workgroup passes and at most 32 per entry, runs within the granules,
+// bases add up.
 void decode_case(const std::vector<int32_t>& lens, int nkvh, int cus) {
     const int n = (int)lens.size();
-    std::vector<int32_t> chunk(n + 1, -1), base(n + 2, -1);
-    const int rc = qasr_plan_decode(n, lens.data(), nkvh, cus, chunk.data(), base.data());
+    std::vector<int32_t> gran(n + 1, -1), run(n + 1, -1), base(n + 2, -1);
+    const int rc = qasr_plan_decode(n, lens.data(), nkvh, cus, gran.data(), run.data(), base.data());
     check(rc == QASR_OK, "qasr_plan_decode refused a valid batch", n, rc);
     if (rc != QASR_OK) return;
     check(base[0] == 0, "wg_base[0]", base[0]);
     for (int b = 0; b < n; ++b) {
-        const int64_t c = chunk[b], L = lens[b];
-        check(c >= 32 && c % 32 == 0, "chunk not whole passes", b, c);
-        if (c <= 0) continue;
-        const int64_t nch = (L + c - 1) / c;
-        check((nch - 1) * c < L && L <= nch * c, "chunks do not tile the entry", L, c);
-        check(nch <= 256, "chunks per entry", nch);
-        check((int64_t)base[b + 1] - base[b] == nkvh * nch, "wg_base step", b, base[b + 1] - base[b]);
+        const int64_t g = gran[b], L = lens[b], r = run[b];
+        check(g >= 256 && g % 256 == 0, "granule not whole pass pairs", b, g);
+        if (g <= 0) continue;
+        const int64_t ngr = (L + g - 1) / g;
+        check((ngr - 1) * g < L && L <= ngr * g, "granules do not tile the entry", L, g);
+        check(ngr <= 32, "granules per entry", ngr);
+        check(r >= 1 && r <= ngr && r * g <= (1 << 22) + g, "granules per workgroup", b, r);
+        if (r <= 0) continue;
+        check((int64_t)base[b + 1] - base[b] == nkvh * ((ngr + r - 1) / r), "wg_base step", b,
+              base[b + 1] - base[b]);
     }
-    check(chunk[n] == -1 && base[n + 1] == -1, "wrote past the outputs");
+    check(gran[n] == -1 && run[n] == -1 && base[n + 1] == -1, "wrote past the outputs");
 }
 
 // Row blocks cover the rows; every row block's key tiles are covered by its
@@ -81,20 +85,20 @@ void prefill_case(int rows, int kv_start, int nkvh) {
 }
 
 void refusals() {
-    int32_t lens[65], chunk[66], base[66];
+    int32_t lens[65], gran[66], run[66], base[66];
     for (int i = 0; i < 65; ++i) lens[i] = 100;
-    check(qasr_plan_decode(0, lens, 8, 256, chunk, base) == QASR_EINVAL, "batch 0 accepted");
-    check(qasr_plan_decode(65, lens, 8, 256, chunk, base) == QASR_EINVAL, "batch 65 accepted");
-    check(qasr_plan_decode(1, lens, 0, 256, chunk, base) == QASR_EINVAL, "nkvh 0 accepted");
-    check(qasr_plan_decode(1, lens, 65, 256, chunk, base) == QASR_EINVAL, "nkvh 65 accepted");
-    check(qasr_plan_decode(1, lens, 8, 0, chunk, base) == QASR_EINVAL, "cus 0 accepted");
-    check(qasr_plan_decode(1, nullptr, 8, 256, chunk, base) == QASR_EINVAL, "null lens accepted");
+    check(qasr_plan_decode(0, lens, 8, 256, gran, run, base) == QASR_EINVAL, "batch 0 accepted");
+    check(qasr_plan_decode(65, lens, 8, 256, gran, run, base) == QASR_EINVAL, "batch 65 accepted");
+    check(qasr_plan_decode(1, lens, 0, 256, gran, run, base) == QASR_EINVAL, "nkvh 0 accepted");
+    check(qasr_plan_decode(1, lens, 65, 256, gran, run, base) == QASR_EINVAL, "nkvh 65 accepted");
+    check(qasr_plan_decode(1, lens, 8, 0, gran, run, base) == QASR_EINVAL, "cus 0 accepted");
+    check(qasr_plan_decode(1, nullptr, 8, 256, gran, run, base) == QASR_EINVAL, "null lens accepted");
     lens[0] = 0;
-    check(qasr_plan_decode(1, lens, 8, 256, chunk, base) == QASR_EINVAL, "empty entry accepted");
+    check(qasr_plan_decode(1, lens, 8, 256, gran, run, base) == QASR_EINVAL, "empty entry accepted");
     lens[0] = kMaxPos + 1;
-    check(qasr_plan_decode(1, lens, 8, 256, chunk, base) == QASR_EINVAL, "2^24 + 1 keys accepted");
+    check(qasr_plan_decode(1, lens, 8, 256, gran, run, base) == QASR_EINVAL, "2^24 + 1 keys accepted");
     lens[0] = 2147483647;
-    check(qasr_plan_decode(1, lens, 8, 256, chunk, base) == QASR_EINVAL, "INT_MAX keys accepted");
+    check(qasr_plan_decode(1, lens, 8, 256, gran, run, base) == QASR_EINVAL, "INT_MAX keys accepted");
     int32_t rpb, nrb, tps, sp[65];
     check(qasr_plan_prefill(0, 0, 8, &rpb, &nrb, &tps, sp) == QASR_EINVAL, "0 rows accepted");
     check(qasr_plan_prefill(4097, 0, 8, &rpb, &nrb, &tps, sp) == QASR_EINVAL, "4097 rows accepted");
@@ -111,10 +115,10 @@ int main() {
     const char* knobs[][2] = {{nullptr, nullptr},
                               {"QASR_DECODE_WGS", "1"},
                               {"QASR_DECODE_WGS", "4096"},
-                              {"QASR_DECODE_MIN_CHUNK", "32"},
-                              {"QASR_DECODE_MIN_CHUNK", "100000"},
-                              {"QASR_DECODE_MAX_SPLIT", "1"},
-                              {"QASR_DECODE_MAX_SPLIT", "100000"},
+                              {"QASR_DECODE_GRANULE", "32"},
+                              {"QASR_DECODE_GRANULE", "100000"},
+                              {"QASR_DECODE_MAX_GRANULES", "1"},
+                              {"QASR_DECODE_MAX_GRANULES", "100000"},
                               {"QASR_DECODE_WGS", "-5"},
                               {"QASR_PREFILL_TPS", "1"},
                               {"QASR_PREFILL_TPS", "7"},

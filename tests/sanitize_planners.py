@@ -6,7 +6,7 @@ code as for the library), links them with sanitize_planners.cpp into
 _build/sanitize/sanitize_planners, and runs it: qasr_plan_decode and
 qasr_plan_prefill over random batches, argument edges, the environment knobs
 and the refusals, with the plans' invariants checked.  Host code only; no
-device is needed.  Usage: python qwen3-asr-wgpu_amd/sanitize_planners.py
+device is needed.  Usage: python tests/sanitize_planners.py
 """
 from __future__ import annotations
 
@@ -16,8 +16,9 @@ import shutil
 import subprocess
 import sys
 
-sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-from build import HERE, INCLUDE, OBJ, ROCM_LIB, _compile, sources  # noqa: E402
+TESTS = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(os.path.dirname(TESTS), "qwen3-asr-wgpu_amd"))
+from build import INCLUDE, OBJ, ROCM_LIB, _compile, sources  # noqa: E402
 
 SANITIZE_HOST = ["-g", "-fno-omit-frame-pointer",
                  "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
@@ -39,7 +40,7 @@ def build_sanitized() -> str:
     san = ["-fsanitize=address,undefined", "-fno-sanitize-recover=undefined"]
     steps = [
         [gxx, "-std=c++17", "-O1", "-g", *san, f"-I{INCLUDE}", "-c",
-         os.path.join(HERE, "sanitize_planners.cpp"), "-o", drv],
+         os.path.join(TESTS, "sanitize_planners.cpp"), "-o", drv],
         [gxx, *san, "-o", SAN_EXE, drv, *objs, f"-L{ROCM_LIB}", "-lamdhip64", "-lrocblas",
          f"-Wl,-rpath,{ROCM_LIB}"],
     ]

@@ -1,8 +1,9 @@
 """Stage (b) decode attention on the GPU against the oracle
 (cpu_decoder.rs:292-365 with one row; stage (a) per 398-423), at the BASELINE
 decode configs and at edge lengths, plus invariants: fused step == stage (a)
-then attention (bitwise), chunk-size independence, slot-permutation
-invariance, appended rows bit-exact."""
+then attention (bitwise), every granule and run plan within the bound, an
+entry's output bits independent of its batch mates, slot order and the
+workgroup budget (--batch N == --batch 1), appended rows bit-exact."""
 from __future__ import annotations
 
 import os
@@ -91,57 +92,117 @@ def test_config3_batch16_ragged_decode(O, gpu):
     g.close()
 
 
-# (minimum chunk keys, workgroup target): from the finest split the planner
-# allows (32-key chunks, up to 256 per entry) through the default plan to one
-# chunk per entry (no split-K, no merge), plus 8-wave workgroups.
-CHUNK_PLANS = [("32", "4096", "4"), ("64", "512", "4"), ("256", "512", "4"),
-               ("100000", "512", "4"), ("64", "512", "8")]
+# (minimum granule keys, workgroup budget, granules per entry at most): from
+# the finest granules (256 keys, one workgroup each) through the default plan
+# to one granule per entry (no merge), runs of many granules whose partials
+# are published for another workgroup's merge, and the greedy plan of a small
+# budget where most (entry, kv head) pairs run whole in one workgroup and
+# merge in LDS.
+GRANULE_PLANS = [("256", "4096", "32"), ("512", "256", "32"), ("256", "64", "32"),
+                 ("100000", "512", "32"), ("256", "8", "32"), ("256", "40", "6")]
 
 
-@pytest.mark.parametrize("min_chunk,wgs,waves", CHUNK_PLANS)
-def test_decode_chunk_sizes_and_unfused_equal_fused(O, gpu, min_chunk, wgs, waves, monkeypatch):
-    """Every split-K chunking matches the oracle; the unfused path
+@pytest.mark.parametrize("gran,wgs,gmax", GRANULE_PLANS)
+def test_decode_plans_and_unfused_equal_fused(O, gpu, gran, wgs, gmax, monkeypatch):
+    """Every granule and run plan matches the oracle; the unfused path
     (qasr_decode_attn on stage-(a) output) equals the fused step bitwise."""
     import qasr_attn
     from gpu_helpers import Gpu, dev, empty, host, say
 
     from oracle import Rng
 
-    monkeypatch.setenv("QASR_DECODE_MIN_CHUNK", min_chunk)
+    monkeypatch.setenv("QASR_DECODE_GRANULE", gran)
     monkeypatch.setenv("QASR_DECODE_WGS", wgs)
-    monkeypatch.setenv("QASR_DECODE_WAVES", waves)
-    chunk = f"{min_chunk}/{wgs}/w{waves}"
-    rng = Rng(SEED_BASE + 200 + int(min_chunk) % 1000 + int(waves))
+    monkeypatch.setenv("QASR_DECODE_MAX_GRANULES", gmax)
+    plan = f"{gran}/{wgs}/{gmax}"
+    rng = Rng(SEED_BASE + 200 + int(gran) % 1000 + int(wgs) % 97)
     lay = Layer(rng)
-    lengths = [1, 2, 127, 128, 129, 255, 256, 1023, 1024, 1500, 2047, 2048, 4095]
+    # 8000 keys: 32 granules of 256 (the merge's largest batch)
+    lengths = [1, 2, 127, 128, 129, 255, 256, 1023, 1024, 1500, 2047, 2048, 4095, 8000]
     cap = cap_for(max(lengths) + 1)
     n = len(lengths)
     g = Gpu(slots=n, cap=cap)
     refs = _setup(O, rng, lay, [L - 1 for L in lengths], cap, g)
+    say(f"decode plan {plan}: {qasr_attn.plan_decode(lengths, NKVH, 256)}")
     got_fused, rows, _ = _decode_step_check(O, rng, lay, g, refs, [L - 1 for L in lengths])
     # unfused: q from stage (a) (re-appending the same rows rewrites the same bits)
     q = g.append(0, lay, [(i, lengths[i] - 1, 1) for i in range(n)], rows)
     out = empty(n, QDIM)
-    say(f"decode_attn unfused chunk={chunk}")
+    say(f"decode_attn unfused plan={plan}")
     qasr_attn.decode_attn(g.ctx, g.kv, 0, lengths, dev(q), out)
     assert np.array_equal(host(out), got_fused)
     g.close()
 
 
-def test_decode_merge_past_16_chunks(O, gpu, monkeypatch):
-    """Up to 64 chunks per entry (QASR_DECODE_MAX_SPLIT=64, 32-key chunks):
-    the last arrival merges the partials in batches of 32, one round trip
-    each, in chunk order -- the same oracle bound and fused/unfused equality."""
-    monkeypatch.setenv("QASR_DECODE_MAX_SPLIT", "64")
-    test_decode_chunk_sizes_and_unfused_equal_fused(O, gpu, "32", "4096", "4", monkeypatch)
+def test_decode_output_independent_of_batch_mates(O, gpu, monkeypatch):
+    """--batch N == --batch 1 for attention: each entry decoded alone, inside
+    two different batches (other slots, other order) and under other
+    workgroup budgets gives the same bits, on the unfused and the fused path.
+    The granule plan depends on an entry's own length only; the batch and the
+    device change only which workgroup runs which granules."""
+    import qasr_attn
+    from gpu_helpers import Gpu, dev, empty, host, say
+
+    from oracle import Rng
+
+    rng = Rng(SEED_BASE + 960)
+    lay = Layer(rng)
+    lengths = [5, 300, 700, 1500, 2047, 2600, 3333, 7000, 129, 1024, 256, 3900]
+    n = len(lengths)
+    cap = cap_for(max(lengths) + 1)
+    g = Gpu(slots=n, cap=cap)
+    refs = _setup(O, rng, lay, [L - 1 for L in lengths], cap, g)
+    rows = rng.normal_f16((n, TOT))
+    q = g.append(0, lay, [(i, lengths[i] - 1, 1) for i in range(n)], rows)
+    qg, kg = g.gains(lay)
+
+    def attn(slots, wgs=None):
+        if wgs is None:
+            monkeypatch.delenv("QASR_DECODE_WGS", raising=False)
+        else:
+            monkeypatch.setenv("QASR_DECODE_WGS", str(wgs))
+        out = empty(len(slots), QDIM)
+        qasr_attn.decode_attn(g.ctx, g.kv, 0, [lengths[s] for s in slots], dev(q[slots]), out,
+                              slots=slots)
+        return host(out)
+
+    def step(slots, wgs=None):
+        if wgs is None:
+            monkeypatch.delenv("QASR_DECODE_WGS", raising=False)
+        else:
+            monkeypatch.setenv("QASR_DECODE_WGS", str(wgs))
+        out = empty(len(slots), QDIM)
+        qasr_attn.decode_step(g.ctx, g.kv, 0, [lengths[s] - 1 for s in slots], dev(rows[slots]),
+                              qg, kg, out, slots=slots)
+        return host(out)
+
+    batch_a = [3, 0, 7, 5]
+    batch_b = [11, 6, 2, 9, 4, 1, 10, 8, 3, 7, 0, 5]
+    say("decode batch invariance: alone, two batches, three budgets")
+    alone = {s: attn([s]) for s in range(n)}
+    for i in range(n):
+        _, want = refs[i].step(rows[i:i + 1], lengths[i] - 1)
+        assert_parity(alone[i], want, f"slot {i} alone")
+    for slots, wgs in [(batch_a, None), (batch_b, None), (batch_b, 64), (batch_a, 1000)]:
+        got = attn(slots, wgs)
+        for k, s in enumerate(slots):
+            assert np.array_equal(got[k:k + 1], alone[s]), (slots, wgs, s)
+    step_alone = {s: step([s]) for s in (3, 7, 11)}
+    for slots in (batch_a, batch_b):
+        got = step(slots, 100)
+        for k, s in enumerate(slots):
+            if s in step_alone:
+                assert np.array_equal(got[k:k + 1], step_alone[s]), (slots, s)
+            assert np.array_equal(got[k:k + 1], alone[s]), (slots, s)
+    g.close()
 
 
 def test_decode_partials_do_not_leak_between_launches(O, gpu, monkeypatch):
-    """Split-K partial slots are shared by every launch on a pool and handed
-    back unset by each launch's merger.  Steps that alternate planner settings
-    (so a slot serves a different entry, kv head and chunk each time, or no
-    split at all) each match the oracle, and a step repeated after them
-    reproduces its first output bitwise."""
+    """Split-K partial slots are shared by every launch on a pool and the
+    arrival counters are handed back at zero by each launch's merger.  Steps
+    that alternate planner settings (so a slot serves a different entry, kv
+    head and granule each time, or no split at all) each match the oracle,
+    and a step repeated after them reproduces its first output bitwise."""
     import qasr_attn
     from gpu_helpers import Gpu, dev, empty, host, say
 
@@ -168,14 +229,14 @@ def test_decode_partials_do_not_leak_between_launches(O, gpu, monkeypatch):
     for i in range(n):
         _, want = refs[i].step(rows0[i:i + 1], pos[i])
         assert_parity(first[i:i + 1], want, f"first step entry {i}")
-    for min_chunk, wgs, split in [("32", "4096", "64"), ("100000", "512", "32"),
-                                  ("64", "97", "32"), ("128", "256", "5")]:
-        monkeypatch.setenv("QASR_DECODE_MIN_CHUNK", min_chunk)
+    for gran, wgs, gmax in [("256", "4096", "32"), ("100000", "512", "32"),
+                            ("256", "97", "32"), ("768", "256", "5"), ("256", "20", "32")]:
+        monkeypatch.setenv("QASR_DECODE_GRANULE", gran)
         monkeypatch.setenv("QASR_DECODE_WGS", wgs)
-        monkeypatch.setenv("QASR_DECODE_MAX_SPLIT", split)
-        say(f"decode leak check: plan {min_chunk}/{wgs}/{split}")
+        monkeypatch.setenv("QASR_DECODE_MAX_GRANULES", gmax)
+        say(f"decode leak check: plan {gran}/{wgs}/{gmax}")
         _decode_step_check(O, rng, lay, g, refs, pos)
-    for var in ("QASR_DECODE_MIN_CHUNK", "QASR_DECODE_WGS", "QASR_DECODE_MAX_SPLIT"):
+    for var in ("QASR_DECODE_GRANULE", "QASR_DECODE_WGS", "QASR_DECODE_MAX_GRANULES"):
         monkeypatch.delenv(var)
     say("decode leak check: repeated first step")
     again = step_rows(rows0)

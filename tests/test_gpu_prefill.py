@@ -170,23 +170,29 @@ def _segments_setup(O, rng, lay, segments, cap):
     return g, refs, qkv, q
 
 
-def test_prefill_attn_batch_equals_per_segment_launches(O, gpu, monkeypatch):
-    """With the per-segment launches held to one split per row block
-    (QASR_PREFILL_TPS large; the one-launch path never splits), one launch
-    for all segments gives the per-segment launches' output bit for bit."""
+@pytest.mark.parametrize("tps", [None, "3"])
+def test_prefill_attn_batch_equals_single_segment_calls(O, gpu, tps, monkeypatch):
+    """--batch N == --batch 1 for prefill attention: one batched call over
+    segments whose plans differ (32-row unsplit blocks, 64-row blocks with
+    key splits, config 4's last chunk, a segment longer than one 4096-row
+    piece) gives every segment the bits of its own qasr_prefill_attn call,
+    under the default plans and under a forced split count."""
     import qasr_attn
     from gpu_helpers import dev, empty, host, say
 
     from oracle import Rng
 
-    monkeypatch.setenv("QASR_PREFILL_TPS", "100000")
-
+    if tps is None:
+        monkeypatch.delenv("QASR_PREFILL_TPS", raising=False)
+    else:
+        monkeypatch.setenv("QASR_PREFILL_TPS", tps)
     rng = Rng(SEED_BASE + 480)
     lay = Layer(rng)
-    segments = [(0, 0, 37), (1, 0, 200), (2, 100, 120), (3, 0, 1), (4, 190, 66)]
-    g, _, _, q = _segments_setup(O, rng, lay, segments, 512)
+    segments = [(0, 0, 37), (1, 0, 200), (2, 100, 120), (3, 0, 1), (4, 190, 66),
+                (5, 7680, 512), (6, 900, 4200)]
+    g, _, _, q = _segments_setup(O, rng, lay, segments, cap_for(7680 + 512))
     total = q.shape[0]
-    say(f"prefill_attn_batch over {segments}")
+    say(f"prefill_attn_batch over {segments} tps={tps}")
     out_b = empty(total, QDIM)
     qasr_attn.prefill_attn_batch(g.ctx, g.kv, 0, segments, dev(q), out_b)
     got = host(out_b)
@@ -200,8 +206,8 @@ def test_prefill_attn_batch_equals_per_segment_launches(O, gpu, monkeypatch):
 
 
 def test_prefill_attn_batch_long_segments_against_oracle(O, gpu):
-    """Key ranges up to 2048 in one launch (each row block's keys in one
-    workgroup) against the oracle, segment by segment."""
+    """Key ranges up to 2048 in one batched call (each segment on its own
+    plan, some with key splits) against the oracle, segment by segment."""
     import qasr_attn
     from gpu_helpers import dev, empty, host, say
 

@@ -3,12 +3,14 @@ prefill_multi, decoder.rs:3599-3700) and the slot scheduler (serving.py,
 inference.rs:707-764, 1944-2227) against this library's single-sequence
 path, on seeded random weights of the 0.6B decoder shape (3 layers).
 
-With at most 16 rows a projection runs the skinny GEMM, whose rows are
-independent, and a context of a few dozen keys is one decode chunk whatever
-the batch holds: there, batched and single paths must agree bitwise.  Longer
-prompts go through rocBLAS with a different row count and the decode plan
-depends on the batch, so there logits must agree to rounding and a greedy
-stream may part from the single path's only at a near-tie."""
+The reference's batched output is byte-identical to `--batch 1`
+(README "byte-identical"; decoder.rs:686-693, 1930-1931), and so is this
+library's: a prefill's projections run one GEMM whose per-element K order
+does not depend on the row count, its attention runs each prompt's own
+plan, a decode step's projections run the kernels of a lone slot's step
+(groups of at most 16 rows) and its attention cuts each slot's keys by the
+slot's own length.  So batched and single paths agree bitwise here: logits,
+KV rows and every token of every stream."""
 from __future__ import annotations
 
 import numpy as np
@@ -76,24 +78,67 @@ def test_prefill_batch_short_segments_bitwise(weights):
     b.close()
 
 
-def test_prefill_batch_long_segments_within_rounding(weights):
-    """474 rows (rocBLAS projections): logits within rounding of the single
-    prefills, equal tokens wherever the top-2 margin is clear."""
+def test_prefill_batch_long_segments_bitwise(weights):
+    """474 rows in one batched prefill (GEMM projections, attention split
+    plans per prompt): the same logits, tokens and KV rows, bit for bit, as
+    one prefill per slot."""
     lens = [100, 37, 260, 77]
     a, b, tok_a, tok_b, lg_a, lg_b = _prefill_both(weights, lens, SEED_BASE + 1120)
-    spread = float(np.std(lg_b))
-    diff = float(np.max(np.abs(lg_a - lg_b)))
-    assert diff <= 2e-2 * spread, (diff, spread)
-    for i in range(len(lens)):
-        top = np.partition(lg_b[i], -2)[-2:]
-        if top[1] - top[0] > 2 * diff:
-            assert tok_a[i] == tok_b[i]
+    assert tok_a == tok_b
+    assert np.array_equal(lg_a, lg_b)
     ka, kb = a.kv.tensor(), b.kv.tensor()
     for i, n in enumerate(lens):
-        d = (ka[i, :, :, :, :n].float() - kb[i, :, :, :, :n].float()).abs().max().item()
-        assert d <= 2e-2, f"slot {i}: KV differs by {d}"
+        assert ka[i, :, :, :, :n].equal(kb[i, :, :, :, :n]), f"slot {i} KV differs"
+    assert a.step() == b.step()
     a.close()
     b.close()
+
+
+def _quantized(W):
+    import torch
+
+    W8 = dict(W)
+    for key in list(W):
+        if isinstance(key, tuple) and key[1].endswith("_proj"):
+            w = W[key].float()
+            s = (w.abs().amax(dim=1) / 127.0).clamp_min(1e-8)
+            W8[key] = torch.round(w / s[:, None]).clamp(-128, 127).to(torch.int8)
+            W8[(key[0], key[1] + "_scale")] = s
+    return W8
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_decode_step_bits_independent_of_batch(weights, int8):
+    """A slot's decode steps alone, inside a batch of 5 and inside a batch
+    of 20 (two groups: 16 + 4 rows) give the same logits and tokens bit for
+    bit, step after step, for f16 and int8 weights; the prompt itself is
+    prefilled alone, in a batch of 5 and in a batch of 20."""
+    import torch
+
+    from gpu_helpers import say
+
+    W = _quantized(weights) if int8 else weights
+    shared = _prompt(SEED_BASE + 1180, 33)
+    others = [_prompt(SEED_BASE + 1181 + i, 5 + 7 * i) for i in range(19)]
+    runs = {}
+    for n in (1, 5, 20):
+        say(f"int8={int8}: slot 0 among {n} slots")
+        dec = _decoder(W, n)
+        lg = torch.empty((n, CFG["vocab"]), dtype=torch.float32, device="cuda")
+        if n == 1:
+            toks = [dec.prefill(shared, 0, slot=0, logits=lg[0])]
+        else:
+            toks = [dec.prefill_batch([(0, shared)] + [(i, others[i - 1]) for i in range(1, n)],
+                                      logits=lg)[0]]
+        lgs = [lg[0].cpu().numpy().copy()]
+        for _ in range(6):
+            toks.append(dec.step(logits=lg)[0])
+            lgs.append(lg[0].cpu().numpy().copy())
+        runs[n] = (toks, np.stack(lgs))
+        dec.close()
+    for n in (5, 20):
+        assert runs[n][0] == runs[1][0], n
+        assert np.array_equal(runs[n][1], runs[1][1]), n
 
 
 def test_prefill_batch_rejects_bad_segments(weights):
@@ -173,25 +218,32 @@ def test_scheduler_short_prompts_bitwise(weights):
     assert stopped_early >= 2
 
 
-def test_scheduler_long_prompts_part_only_at_near_ties(weights):
-    """Prompts of 40-300 rows at width 4 (rocBLAS prefill, batch-dependent
-    decode plans): a stream may part from the single path's only where the
-    single path's top-2 margin is within rounding (2% of the logit spread)."""
+def test_scheduler_long_prompts_bitwise(weights):
+    """Prompts of 40-300 rows at width 4 (GEMM prefills of several prompts at
+    once, decode over contexts of hundreds of keys): every segment's tokens
+    equal the single path's."""
     rng = np.random.default_rng(11)
     lens = [int(x) for x in rng.integers(40, 300, size=10)]
     max_news = [int(x) for x in rng.integers(8, 24, size=10)]
     single, plain, batched = _run_both(weights, lens, max_news, 4, SEED_BASE + 1150)
-    same = 0
     for g in range(len(lens)):
-        ids, margins, spread = single[g]
-        assert plain[g].ids == ids
-        got = batched[g].ids
-        if got == ids:
-            same += 1
-            continue
-        j = next(k for k in range(min(len(got), len(ids))) if got[k] != ids[k])
-        assert margins[j] < 2e-2 * spread, f"segment {g} parts at token {j}, margin {margins[j]}"
-    assert same >= len(lens) // 2
+        ids = single[g][0]
+        assert plain[g].ids == ids, g
+        assert batched[g].ids == ids, g
+
+
+def test_scheduler_width_past_16_bitwise(weights):
+    """Width 20 over 24 segments: decode steps of up to 20 rows (groups of 16
+    + 4) and prefills of up to 20 prompts; every segment's tokens equal the
+    single path's."""
+    rng = np.random.default_rng(12)
+    lens = [int(x) for x in rng.integers(3, 120, size=24)]
+    max_news = [int(x) for x in rng.integers(4, 14, size=24)]
+    single, plain, batched = _run_both(weights, lens, max_news, 20, SEED_BASE + 1155)
+    for g in range(len(lens)):
+        ids = single[g][0]
+        assert plain[g].ids == ids, g
+        assert batched[g].ids == ids, g
 
 
 def test_decoder_prefill_batch_abi_refuses_bad_segments(weights):
@@ -248,9 +300,9 @@ def test_pipelined_steps_equal_synchronous_steps(weights):
 
 
 def test_int8_prefill_batch_equals_dequantized_f16(weights):
-    """Int8 projections through the batched prefill (more than 16 rows: the
-    layer's matrix dequantised for rocBLAS) against f16 weights dequantised
-    on the host: identical tokens and logits, bitwise."""
+    """Int8 projections through the batched prefill (the layer's matrix
+    dequantised for the GEMM) against f16 weights dequantised on the host:
+    identical tokens and logits, bitwise."""
     import torch
 
     W8, Wdq = dict(weights), dict(weights)

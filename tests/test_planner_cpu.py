@@ -1,9 +1,10 @@
 """The library's launch planners on the host (qasr_plan_decode,
 qasr_plan_prefill; no device needed): every key of every entry falls in
-exactly one decode workgroup's chunk, chunks are whole 32-key passes, the
-workgroup bases add up, and every prefill row block's key tiles are covered
-by its splits -- over random batches, the knobs the GPU tests drive, the
-bench configurations the documentation cites, and the refusals."""
+exactly one decode granule and one workgroup's run, granule sizes depend on
+an entry's own length only (so its output bits do not depend on its batch
+mates), the workgroup bases add up, and every prefill row block's key tiles
+are covered by its splits -- over random batches, the knobs the GPU tests
+drive, the bench configurations the documentation cites, and the refusals."""
 from __future__ import annotations
 
 import numpy as np
@@ -29,22 +30,33 @@ def splitmix_lengths(seed: int, n: int, lo: int, hi: int):
     return out
 
 
-def check_decode_plan(lens, chunk, base, max_split=32, nkvh=NKVH):
+def granule(L: int, gmin: int = 256, gmax: int = 32) -> int:
+    """The granule rule, restated: the smallest multiple of 256 keys (two
+    workgroup passes) that is at least gmin and leaves at most gmax granules."""
+    want = max(gmin, -(-L // gmax))
+    return -(-want // 256) * 256
+
+
+def check_decode_plan(lens, plan, nkvh=NKVH, gmin=256, gmax=32):
+    gran, run, base = plan
     assert base[0] == 0
+    parts = 0
     for b, L in enumerate(lens):
-        c = chunk[b]
-        assert c >= 32 and c % 32 == 0, (b, c)
-        nch = -(-L // c)
-        # chunks [j c, min((j+1) c, L)) for j < nch: none empty, none past L
-        assert (nch - 1) * c < L <= nch * c
-        assert nch <= max_split
-        assert base[b + 1] - base[b] == nkvh * nch, (b, L, c)
-    assert base[-1] <= 8192
+        g, r = gran[b], run[b]
+        assert g == granule(L, gmin, gmax), (b, L, g)
+        ngr = -(-L // g)
+        # granules [i g, min((i+1) g, L)) for i < ngr: none empty, none past L
+        assert (ngr - 1) * g < L <= ngr * g and ngr <= 32
+        assert 1 <= r <= ngr
+        assert base[b + 1] - base[b] == nkvh * -(-ngr // r), (b, L, g, r)
+        parts += nkvh * ngr
+    assert parts <= 64 * nkvh * 32  # the workspace's partial records
 
 
 @pytest.fixture(autouse=True)
 def _no_knobs(monkeypatch):
-    for v in ("QASR_DECODE_WGS", "QASR_DECODE_MIN_CHUNK", "QASR_DECODE_MAX_SPLIT", "QASR_PREFILL_TPS"):
+    for v in ("QASR_DECODE_WGS", "QASR_DECODE_GRANULE", "QASR_DECODE_MAX_GRANULES",
+              "QASR_PREFILL_TPS"):
         monkeypatch.delenv(v, raising=False)
 
 
@@ -53,60 +65,64 @@ def test_decode_plan_covers_every_key_random_batches():
     for _ in range(300):
         n = int(rng.integers(1, 65))
         lens = [int(x) for x in rng.integers(1, 16385, size=n)]
-        chunk, base = qasr_attn.plan_decode(lens, NKVH, 256)
-        check_decode_plan(lens, chunk, base)
-        # the budget is one workgroup per CU unless the batch alone exceeds it
+        plan = qasr_attn.plan_decode(lens, NKVH, 256)
+        check_decode_plan(lens, plan)
+        base = plan[2]
         assert base[-1] >= NKVH * n
-        if NKVH * n < 256:
+        if NKVH * n < 256:  # the budget is one workgroup per CU unless the batch alone exceeds it
             assert base[-1] <= 256
 
 
+def test_decode_granules_do_not_depend_on_the_batch():
+    """An entry's granules alone equal its granules in any batch and on any
+    device: the property that makes --batch N byte-identical to --batch 1."""
+    rng = np.random.default_rng(11)
+    for _ in range(100):
+        n = int(rng.integers(2, 65))
+        lens = [int(x) for x in rng.integers(1, 16385, size=n)]
+        gran, _, _ = qasr_attn.plan_decode(lens, NKVH, int(rng.integers(1, 512)))
+        for b in range(0, n, 7):
+            alone, _, _ = qasr_attn.plan_decode([lens[b]], NKVH, 256)
+            assert alone[0] == gran[b]
+
+
 def test_decode_plan_bench_configs():
-    lens3 = splitmix_lengths(SPLITMIX_SEED_CONFIG3, 16, 400, 2400)
-    chunk, base = qasr_attn.plan_decode([L + 1 for L in lens3], NKVH, 256)
-    check_decode_plan([L + 1 for L in lens3], chunk, base)
-    assert base[-1] == 256 and max(chunk) == 960  # config 3: one workgroup per CU
-    # one common chunk size; only entries shorter than it stay whole
-    lens3p = [L + 1 for L in lens3]
-    assert all(c == 960 or c >= L for c, L in zip(chunk, lens3p))
-    full = sum(NKVH * (L // 960) for L in lens3p if L > 960)
-    assert full >= 128  # most workgroups stream a full chunk until the end
-    chunk, base = qasr_attn.plan_decode([8193], NKVH, 256)
-    assert chunk == [544] and base == [0, 8 * 16]  # config 4: 16 chunks of 544 keys
-    chunk, base = qasr_attn.plan_decode([512], NKVH, 256)
-    assert chunk == [64] and base == [0, 64]  # config 1: 64-key minimum chunk
-    # below two minimum chunks an entry stays whole: one chunk of whole passes
-    chunk, base = qasr_attn.plan_decode([1, 2, 31, 32, 33, 255, 256, 257], NKVH, 256)
-    assert chunk == [32, 32, 32, 32, 64, 64, 64, 64]
-    assert base == [0, 8, 16, 24, 32, 40, 72, 104, 144]
-    # a batch at the budget (64 entries x 8 kv heads) splits only its longest entries
+    lens3 = [L + 1 for L in splitmix_lengths(SPLITMIX_SEED_CONFIG3, 16, 400, 2400)]
+    gran, run, base = plan = qasr_attn.plan_decode(lens3, NKVH, 256)
+    check_decode_plan(lens3, plan)
+    assert gran == [256] * 16 and 240 <= base[-1] <= 256  # config 3: about one workgroup per CU
+    gran, run, base = plan = qasr_attn.plan_decode([8193], NKVH, 256)
+    assert gran == [512] and run == [1] and base == [0, 8 * 17]  # config 4: 17 granules
+    gran, run, base = qasr_attn.plan_decode([512], NKVH, 256)
+    assert gran == [256] and run == [1] and base == [0, 16]  # config 1: two granules
+    lens = [1, 2, 255, 256, 257, 4096, 8192]
+    gran, run, base = plan = qasr_attn.plan_decode(lens, NKVH, 256)
+    check_decode_plan(lens, plan)
+    assert gran == [256] * 7 and base[-1] <= 256
+    assert run[:4] == [1, 1, 1, 1]  # one granule each
+    # a batch past the budget (64 entries x 8 kv heads) splits only its longest entries
     lens = [100] * 63 + [4000]
-    chunk, base = qasr_attn.plan_decode(lens, NKVH, 256)
-    check_decode_plan(lens, chunk, base)
-    assert chunk[:63] == [128] * 63 and base[-1] > 512
+    gran, run, base = plan = qasr_attn.plan_decode(lens, NKVH, 256)
+    check_decode_plan(lens, plan)
+    assert base[:64] == [8 * i for i in range(64)] and base[-1] > 512
 
 
 def test_decode_plan_knobs(monkeypatch):
-    # the finest plan the merge tests force: past 32 chunks per entry
-    monkeypatch.setenv("QASR_DECODE_MAX_SPLIT", "64")
-    monkeypatch.setenv("QASR_DECODE_MIN_CHUNK", "32")
+    monkeypatch.setenv("QASR_DECODE_GRANULE", "768")
+    lens = [8193, 130, 1000]
+    plan = qasr_attn.plan_decode(lens, NKVH, 256)
+    check_decode_plan(lens, plan, gmin=768)
+    monkeypatch.setenv("QASR_DECODE_MAX_GRANULES", "4")
+    plan = qasr_attn.plan_decode(lens, NKVH, 256)
+    check_decode_plan(lens, plan, gmin=768, gmax=4)
+    monkeypatch.setenv("QASR_DECODE_WGS", "8")  # past the budget: the greedy plan
+    plan = qasr_attn.plan_decode(lens, NKVH, 256)
+    check_decode_plan(lens, plan, gmin=768, gmax=4)
+    plan = qasr_attn.plan_decode([3000, 3000], NKVH, 256)
+    assert plan[1] == [4, 4]  # equal entries stay whole: one workgroup per (entry, kv head)
     monkeypatch.setenv("QASR_DECODE_WGS", "4096")
-    chunk, base = qasr_attn.plan_decode([8193], NKVH, 256)
-    check_decode_plan([8193], chunk, base, max_split=64)
-    assert 32 < base[-1] // NKVH <= 64
-    monkeypatch.delenv("QASR_DECODE_WGS")
-    monkeypatch.setenv("QASR_DECODE_MAX_SPLIT", "32")
-    monkeypatch.setenv("QASR_DECODE_MIN_CHUNK", "100000")
-    lens = [1500, 700, 4095]
-    chunk, base = qasr_attn.plan_decode(lens, NKVH, 256)
-    check_decode_plan(lens, chunk, base)
-    assert base == [0, 8, 16, 24]  # one chunk per entry: no split, no merge
-    monkeypatch.delenv("QASR_DECODE_MIN_CHUNK")
-    monkeypatch.setenv("QASR_DECODE_WGS", "512")
-    lens3 = [L + 1 for L in splitmix_lengths(SPLITMIX_SEED_CONFIG3, 16, 400, 2400)]
-    chunk, base = qasr_attn.plan_decode(lens3, NKVH, 256)
-    check_decode_plan(lens3, chunk, base)
-    assert 256 < base[-1] <= 512
+    plan = qasr_attn.plan_decode(lens, NKVH, 256)
+    assert plan[1] == [1, 1, 1]
 
 
 def test_decode_plan_refusals():

@@ -13,7 +13,7 @@ import sys
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-SCRIPT = os.path.join(ROOT, "qwen3-asr-wgpu_amd", "sanitize_planners.py")
+SCRIPT = os.path.join(ROOT, "tests", "sanitize_planners.py")
 
 
 @pytest.mark.skipif(not (shutil.which("hipcc") or os.path.exists("/opt/rocm/bin/hipcc")),
@@ -21,7 +21,7 @@ SCRIPT = os.path.join(ROOT, "qwen3-asr-wgpu_amd", "sanitize_planners.py")
 @pytest.mark.skipif(not os.path.exists(SCRIPT), reason="sanitizer driver not in this tree")
 def test_planners_clean_under_asan_ubsan():
     env = dict(os.environ)
-    for v in ("QASR_DECODE_WGS", "QASR_DECODE_MIN_CHUNK", "QASR_DECODE_MAX_SPLIT", "QASR_PREFILL_TPS"):
+    for v in ("QASR_DECODE_WGS", "QASR_DECODE_GRANULE", "QASR_DECODE_MAX_GRANULES", "QASR_PREFILL_TPS"):
         env.pop(v, None)
     env["ASAN_OPTIONS"] = "detect_leaks=0:abort_on_error=0"
     r = subprocess.run([sys.executable, SCRIPT], capture_output=True, text=True, env=env, timeout=900)
