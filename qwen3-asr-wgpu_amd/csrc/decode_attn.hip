@@ -19,7 +19,7 @@
 // can spread any batch over about one workgroup per CU.
 //
 // Work decomposition (one launch for the whole batch):
-//   workgroup = (batch entry b, kv head, run of granules), 4 waves.
+//   workgroup = (batch entry b, run of granules, kv head), 4 waves.
 //   Both q heads of the kv head (GQA 2:1) are computed from one K/V read.
 //   A workgroup pass covers 128 contiguous keys, wave w taking keys 32w..+32:
 //   8 dwordx4 buffer loads of K and 8 of V per lane, each instruction
@@ -31,15 +31,17 @@
 //   reduction that leaves each lane with one (key, head) score.  Softmax is
 //   online per (16-lane row, head) in the exp2 domain; the row's 16
 //   probabilities reach the V layout through LDS and P.V accumulates in f32
-//   (v_fma_mix on packed f16).  At each granule's end the 16 rows of the
-//   workgroup merge through one LDS pass (double buffered, one barrier) into
-//   the granule's partial, which stays in LDS, and the rows start over.
-//   After the run: an entry with one granule writes its output; a (entry,
-//   kv head) whose granules all ran in this workgroup merges them from LDS;
-//   otherwise the run's partials are published with device-scope stores and
-//   the last workgroup to arrive (ticket) merges all of them, issuing its
-//   loads at once: no second launch and no L2-wide cache maintenance.  Both
-//   merges combine the same values in the same order.
+//   (v_fma_mix on packed f16).  At each granule's end each wave merges its
+//   4 rows through lane swaps (no LDS round trip, no workgroup barrier: the
+//   waves stream independently) into its wave partial, kept in LDS, and the
+//   rows start over.  After the run the 4 wave partials of each granule
+//   combine, in wave order, into the granule's partial: an entry with one
+//   granule writes its output; a (entry, kv head) whose granules all ran in
+//   this workgroup merges them there; otherwise the run's partials are
+//   published with device-scope stores and the last workgroup to arrive
+//   (ticket) merges all of them, issuing its loads at once: no second launch
+//   and no L2-wide cache maintenance.  Both merges combine the same values in
+//   the same order.
 //
 // Fused variant (stage (a) + (b)): the workgroup recomputes its two q heads
 // from the raw qkv row (bit-identical to the stage-(a) kernel); the workgroup
@@ -69,6 +71,22 @@ constexpr int W = kDecodeWaves;
 constexpr int kWgKeys = W * kDecodeTileKeys;  // keys per workgroup pass
 static_assert(2 * kWgKeys == kDecodeGranuleQuantum, "a granule is an even number of workgroup passes");
 constexpr int kMaxG = kDecodeMaxGranules;
+constexpr int kMaxRunG = kDecodeMaxRunGranules;
+
+// Lane swaps between rows (16-lane groups): pair_rows gives every lane the
+// value of the even (first) and odd (second) row of its row pair, halves the
+// value of the lower (first) and upper (second) 32 lanes, at the lane's
+// position in the row / half.
+__device__ __forceinline__ void pair_rows(float v, float& even, float& odd) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    even = __uint_as_float(r[0]);
+    odd = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void halves(float v, float& lo, float& hi) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    lo = __uint_as_float(r[0]);
+    hi = __uint_as_float(r[1]);
+}
 
 __device__ __forceinline__ float dot8(const H8& a, const H8& b) {
     float s = 0.0f;
@@ -110,14 +128,11 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     __shared__ __attribute__((aligned(16))) f16 s_tab[4][kHeadDim];  // q gain, k gain, cos, sin
     __shared__ float s_inv[3];
     __shared__ float s_p[W][64];
-    // Row states at a granule's end (double buffered: one barrier per granule).
-    __shared__ float s_wm[2][4 * W][2];
-    __shared__ float s_wl[2][4 * W][2];
-    __shared__ float s_wa[2][4 * W][2][kHeadDim];
-    // Granule partials of this workgroup's run.
-    __shared__ float s_pm[kMaxG][2];
-    __shared__ float s_pl[kMaxG][2];
-    __shared__ float s_pa[kMaxG][2][kHeadDim];
+    // Wave partials of the run's granules: (max, sum) per head and the
+    // unnormalised output of both heads.
+    __shared__ float s_wm[kMaxRunG][W][2];
+    __shared__ float s_wl[kMaxRunG][W][2];
+    __shared__ __attribute__((aligned(16))) float s_wa[kMaxRunG][W][2][kHeadDim];
     __shared__ int s_last;
 
     const int wg = blockIdx.x;
@@ -136,11 +151,14 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     const int run = P.run[b];
     const int ngr = (L + G - 1) / G;        // granules of the entry (per kv head)
     const int nw = (ngr + run - 1) / run;   // workgroups per kv head
+    // kv head minor: workgroup i runs on XCD i mod 8, so with 8 kv heads every
+    // XCD gets one run of each size.  Runs end at the entry's end: the last
+    // holds the (possibly short) last granule, the first any remainder.
     const int rel = wg - P.wg_base[b];
-    const int kvh = rel / nw;
-    const int r = rel - kvh * nw;
-    const int g0 = r * run;
-    const int g1 = min(g0 + run, ngr);
+    const int kvh = rel % g.nkvh;
+    const int r = rel / g.nkvh;
+    const int g1 = ngr - (nw - 1 - r) * run;
+    const int g0 = max(0, g1 - run);
     const int key0 = g0 * G;
     const int key1 = min(g1 * G, L);
     const int nkeys = key1 - key0;
@@ -197,7 +215,7 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
 
     H8 q0, q1;
     if constexpr (FUSED) {
-        if (tid < 3 && (tid < 2 || owner)) s_inv[tid] = head_inv_rms_serial(s_raw[tid], P.eps);
+        if (tid < 3 && (tid < 2 || owner)) s_inv[tid] = head_inv_rms_vec(s_raw[tid], P.eps);
         __syncthreads();
         if (tid < 256) {
             const int h = tid >> 7, j = tid & 127;
@@ -306,38 +324,69 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     f16* ob = out + (int64_t)b * nqh * kHeadDim + h0 * kHeadDim;
     const int64_t part0 = (int64_t)P.part_base[b] + (int64_t)kvh * ngr;
 
-    // End of granule gi (relative to the run): the 16 rows merge through LDS
-    // in row order into the granule's (M, sum, unnormalised output), kept in
-    // LDS until the run ends; then the rows start over.  Nothing here touches
-    // global memory, so the K/V stream's loads stay the only ones in flight.
-    auto finalize = [&](int gi) {
-        const int buf = gi & 1;
-        const int rr = wave * 4 + row;
-        if (seg < 2) {  // lane 0 of the row holds head 0's (m, l), lane 1 head 1's
-            s_wm[buf][rr][seg] = m_run;
-            s_wl[buf][rr][seg] = l_run;
-        }
+    // Partial merge a <- a (+) b of two row states (each lane: (m, l) of the
+    // head of its parity, 8 dims of both heads): M = max, then each side
+    // weighted by 2^(m - M) (0 for a side without keys).  The other head's
+    // weights come from the neighbouring lane.
+    auto combine = [&](float& m, float& l, float (&x0)[8], float (&x1)[8], float mb, float lb,
+                       const float (&y0)[8], const float (&y1)[8]) {
+        const float M = fmaxf(m, mb);
+        const float fa = m == kNegInf ? 0.0f : fast_exp2(m - M);
+        const float fb = mb == kNegInf ? 0.0f : fast_exp2(mb - M);
+        l = fmaf(lb, fb, l * fa);
+        m = M;
+        const float fax = dpp<kDppXor1>(fa), fbx = dpp<kDppXor1>(fb);
+        const float fa0 = odd ? fax : fa, fb0 = odd ? fbx : fb;
+        const float fa1 = odd ? fa : fax, fb1 = odd ? fb : fbx;
 #pragma unroll
         for (int d = 0; d < 8; ++d) {
-            s_wa[buf][rr][0][seg * 8 + d] = a0[d];
-            s_wa[buf][rr][1][seg * 8 + d] = a1[d];
+            x0[d] = fmaf(y0[d], fb0, x0[d] * fa0);
+            x1[d] = fmaf(y1[d], fb1, x1[d] * fa1);
         }
-        __syncthreads();
-        float M = kNegInf;
+    };
+
+    // End of granule gi (relative to the run), per wave and without waiting
+    // for the other waves: the wave's 4 rows merge as (row 0 (+) row 1) (+)
+    // (row 2 (+) row 3) through lane swaps, and row 0's lanes leave the wave's
+    // partial in LDS; then the rows start over.
+    auto finalize = [&](int gi) {
+        float m, l, x0[8], x1[8], mb, lb, y0[8], y1[8];
+        pair_rows(m_run, m, mb);
+        pair_rows(l_run, l, lb);
 #pragma unroll
-        for (int q = 0; q < 4 * W; ++q) M = fmaxf(M, s_wm[buf][q][h]);
-        float Ls = 0.0f, A = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4 * W; ++q) {
-            const float mr = s_wm[buf][q][h];
-            const float f = mr == kNegInf ? 0.0f : fast_exp2(mr - M);
-            Ls = fmaf(s_wl[buf][q][h], f, Ls);
-            A = fmaf(s_wa[buf][q][h][j], f, A);
+        for (int d = 0; d < 8; ++d) {
+            pair_rows(a0[d], x0[d], y0[d]);
+            pair_rows(a1[d], x1[d], y1[d]);
         }
-        s_pa[gi][h][j] = A;
-        if (j == 0) {
-            s_pm[gi][h] = M;
-            s_pl[gi][h] = Ls;
+        combine(m, l, x0, x1, mb, lb, y0, y1);
+        float n0, n1;
+        halves(m, n0, n1);
+        m = n0;
+        mb = n1;
+        halves(l, n0, n1);
+        l = n0;
+        lb = n1;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            halves(x0[d], n0, n1);
+            x0[d] = n0;
+            y0[d] = n1;
+            halves(x1[d], n0, n1);
+            x1[d] = n0;
+            y1[d] = n1;
+        }
+        combine(m, l, x0, x1, mb, lb, y0, y1);
+        if (lane < 16) {
+            float* w0 = &s_wa[gi][wave][0][seg * 8];
+            float* w1 = &s_wa[gi][wave][1][seg * 8];
+            *(float4*)w0 = make_float4(x0[0], x0[1], x0[2], x0[3]);
+            *(float4*)(w0 + 4) = make_float4(x0[4], x0[5], x0[6], x0[7]);
+            *(float4*)w1 = make_float4(x1[0], x1[1], x1[2], x1[3]);
+            *(float4*)(w1 + 4) = make_float4(x1[4], x1[5], x1[6], x1[7]);
+            if (lane < 2) {  // lane 0: head 0's (m, l), lane 1: head 1's
+                s_wm[gi][wave][lane] = m;
+                s_wl[gi][wave][lane] = l;
+            }
         }
         m_run = kNegInf;
         l_run = 0.0f;
@@ -350,8 +399,9 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     // is followed by an empty one).  Every wave processes every pass: keys
     // past the run are masked, which leaves a row's state exactly as it was.
     // Only an entry's last granule can end inside a pass, and it is always
-    // the last of its run.  The loop has one path, so the compiler keeps the
-    // next pass's loads in flight while the current one is computed.
+    // the last of its run.  The loop has one path and no workgroup barrier,
+    // so the compiler keeps the next pass's loads in flight while the current
+    // one is computed and the waves stream independently.
     for (int p = 0; p < npass; p += 2) {
         const int t0 = p * kWgKeys + tw;
         process(ka, va, t0);
@@ -364,37 +414,74 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
         load_pass(vres, t0 + 3 * kWgKeys, row, seg, vb);
         if ((p + 2) % ppg == 0 || p + 2 >= npass) finalize(p / ppg);
     }
-    const int mine = g1 - g0;  // granules of this run, partials in s_p*[0 .. mine)
+    const int mine = g1 - g0;  // granules of this run
     __syncthreads();
+
+    // Granule gi's partial (M, sum, unnormalised output of head h, dim j):
+    // its 4 wave partials in wave order, each weighted by 2^(m_w - M).
+    auto granule = [&](int gi, float& M, float& Lg, float& Ag) {
+        float mw[W];
+#pragma unroll
+        for (int w = 0; w < W; ++w) mw[w] = s_wm[gi][w][h];
+        M = mw[0];
+#pragma unroll
+        for (int w = 1; w < W; ++w) M = fmaxf(M, mw[w]);
+        Lg = 0.0f;
+        Ag = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float f = mw[w] == kNegInf ? 0.0f : fast_exp2(mw[w] - M);
+            Lg = fmaf(s_wl[gi][w][h], f, Lg);
+            Ag = fmaf(s_wa[gi][w][h][j], f, Ag);
+        }
+    };
     if (ngr == 1) {
-        ob[h * kHeadDim + j] = f2h(s_pa[0][h][j] / s_pl[0][h]);
+        float M, Lg, Ag;
+        granule(0, M, Lg, Ag);
+        ob[h * kHeadDim + j] = f2h(Ag / Lg);
         return;
     }
 
     // Merge of the ngr granule partials in granule order: M = max of the
     // granule maxima, then sum_i 2^(m_i - M) * (l_i, acc_i).  Every granule
     // holds at least one real key, so every m_i is finite.  The LDS and the
-    // workspace paths below do the same arithmetic in the same order.
+    // workspace paths below do the same arithmetic on the same values in the
+    // same order.
     if (nw == 1) {
-        float M = s_pm[0][h];
-        for (int i = 1; i < ngr; ++i) M = fmaxf(M, s_pm[i][h]);
+        float M = kNegInf;
+        for (int i = 0; i < ngr; ++i) {
+            float mi, li, ai;
+            granule(i, mi, li, ai);
+            M = i == 0 ? mi : fmaxf(M, mi);
+        }
         float lsum = 0.0f, acc = 0.0f;
         for (int i = 0; i < ngr; ++i) {
-            const float wgt = fast_exp2(s_pm[i][h] - M);
-            lsum = fmaf(s_pl[i][h], wgt, lsum);
-            acc = fmaf(s_pa[i][h][j], wgt, acc);
+            float mi, li, ai;
+            granule(i, mi, li, ai);
+            const float wgt = fast_exp2(mi - M);
+            lsum = fmaf(li, wgt, lsum);
+            acc = fmaf(ai, wgt, acc);
         }
         ob[h * kHeadDim + j] = f2h(acc / lsum);
         return;
     }
 
-    // Publish this run's partials (device-scope stores), then the ticket.
-    for (int gi = 0; gi < mine; ++gi) {
-        const int64_t it = part0 + g0 + gi;
-        store_dev(&ws_acc[it * (2 * kHeadDim) + h * kHeadDim + j], s_pa[gi][h][j]);
-        if (j == 0) {
-            store_dev(&ws_ml[it * 4 + h], s_pm[gi][h]);
-            store_dev(&ws_ml[it * 4 + 2 + h], s_pl[gi][h]);
+    // Publish this run's partials (device-scope stores), four granules'
+    // LDS reads at a time, then the ticket.
+    for (int g4 = 0; g4 < mine; g4 += 4) {
+        float mi[4], li[4], ai[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) granule(min(g4 + u, mine - 1), mi[u], li[u], ai[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (g4 + u < mine) {
+                const int64_t it = part0 + g0 + g4 + u;
+                store_dev(&ws_acc[it * (2 * kHeadDim) + h * kHeadDim + j], ai[u]);
+                if (j == 0) {
+                    store_dev(&ws_ml[it * 4 + h], mi[u]);
+                    store_dev(&ws_ml[it * 4 + 2 + h], li[u]);
+                }
+            }
         }
     }
     stores_done_barrier();

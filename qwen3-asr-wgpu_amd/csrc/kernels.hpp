@@ -32,8 +32,9 @@ struct SegPlan {
 // Stage (b) plan.  Entry b's keys are cut into granules of gran[b] keys (a
 // multiple of kDecodeGranuleQuantum, a function of len[b] only, at most
 // kDecodeMaxGranules of them); a workgroup runs `run[b]` consecutive granules
-// of one kv head.  Workgroups of entry b are wg_base[b] .. wg_base[b+1]-1,
-// kv-head major; the partial record of (entry b, kv head h, granule i) is
+// of one kv head, runs aligned to the entry's end (the first takes any
+// remainder).  Workgroups of entry b are wg_base[b] .. wg_base[b+1]-1, kv
+// head minor; the partial record of (entry b, kv head h, granule i) is
 // part_base[b] + h * ceil(len[b] / gran[b]) + i.
 struct DecodePlan {
     int32_t batch;
@@ -54,7 +55,7 @@ constexpr int kDecodeTileKeys = 32;   // keys per wave pass
 constexpr int kDecodeWgKeys = kDecodeWaves * kDecodeTileKeys;  // keys per workgroup pass
 constexpr int kDecodeGranuleQuantum = 2 * kDecodeWgKeys;        // granules are multiples of this
 constexpr int kDecodeMaxGranules = 32;  // granules per entry: the merge reads them in one round trip
-constexpr int kDecodeMinGranule = 256;  // keys: the smallest granule of a default plan
+constexpr int kDecodeMaxRunGranules = 16;  // granules of one workgroup's run (wave partials in LDS)
 
 // Split-K workspace of one launch: per granule partial the unnormalised
 // output of both q heads (2 x 128 f32) and (max, sum) per head, plus one

@@ -62,6 +62,26 @@ __device__ __forceinline__ float head_inv_rms_squares_all(const float* sq, float
     return 1.0f / sqrtf(sum2 / (float)kHeadDim + eps);
 }
 
+// The same chain read 16 bytes at a time (all 16 reads issued before the
+// adds): the squares are independent of each other, so only the 128
+// dependent adds in ascending j stay on the serial path -- same adds, same
+// order, same bits as head_inv_rms_serial.  `raw` is 16-byte aligned.
+__device__ __forceinline__ float head_inv_rms_vec(const f16* raw, float eps) {
+#pragma clang fp contract(off)
+    H8 v[kHeadDim / 8];
+#pragma unroll
+    for (int c = 0; c < kHeadDim / 8; ++c) v[c].u = *(const uint4*)(raw + 8 * c);
+    float sum2 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kHeadDim / 8; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float f = h2f(v[c].e[e]);
+            sum2 += f * f;
+        }
+    return 1.0f / sqrtf(sum2 / (float)kHeadDim + eps);
+}
+
 // One roped element j of a head whose raw values, gains and cos/sin rows are
 // given (all f16).  `inv` is the head's inverse RMS.
 __device__ __forceinline__ f16 rope_elem(const f16* raw, const f16* gain, const f16* cos_row,

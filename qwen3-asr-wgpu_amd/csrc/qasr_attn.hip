@@ -146,16 +146,18 @@ int ensure_prefill_ws(qasr_kv* kv, int64_t items) {
 
 // Decode launch plan, in two parts.
 //
-// 1. Granules: entry b's keys are cut into granules of G(len[b]) keys, the
-//    smallest multiple of 256 (two workgroup passes) that is at least
-//    QASR_DECODE_GRANULE (default 256) keys and leaves at most
-//    QASR_DECODE_MAX_GRANULES (default and limit 32) granules.  Every granule
+// 1. Granules: entry b's keys are cut into granules of G(len[b]) keys, a
+//    multiple of 256 (two workgroup passes) leaving at most
+//    QASR_DECODE_MAX_GRANULES (default and limit 32) granules: by default
+//    256 keys up to 1024 keys, 1024 up to 8192, then len / 32 (granule_keys);
+//    with QASR_DECODE_GRANULE = g, at least g keys.  Every granule
 //    yields one partial and the partials merge in granule order, so an
 //    entry's output bits are a function of its own length and keys: batch
 //    composition, slot order and the device's CU count never change them
 //    (the reference's --batch N == --batch 1, decoder.rs:1930-1931).
 // 2. Runs: which workgroup runs which granules.  A workgroup takes `run`
-//    consecutive granules of one (entry, kv head).  One CU streams at most
+//    consecutive granules (at most kDecodeMaxRunGranules) of one (entry, kv
+//    head).  One CU streams at most
 //    ~50-75 GB/s, so a launch runs at HBM rate only while most CUs stream:
 //    the plan aims at QASR_DECODE_WGS workgroups (default one per CU) that
 //    carry about the same number of keys.  When the batch leaves room
@@ -166,8 +168,21 @@ int ensure_prefill_ws(qasr_kv* kv, int64_t items) {
 //    the most keys while it exceeds 1.5x the average keys per workgroup; the
 //    extra workgroups run as the first ones finish.
 int granule_keys(int L, int gmin, int gmax) {
-    const int64_t want = std::max<int64_t>(gmin, ((int64_t)L + gmax - 1) / gmax);
     const int64_t q = qasr::kDecodeGranuleQuantum;
+    int64_t want;
+    if (gmin > 0) {
+        want = std::max<int64_t>(gmin, ((int64_t)L + gmax - 1) / gmax);
+    } else {
+        // Default rule.  A granule costs a per-wave merge inside the stream
+        // and a partial in the final merge, so entries of a batch want few,
+        // large granules (config 3, 16 slots of 400-2400 keys: 21.0 us per
+        // layer at 1024 keys, 22.4 at 512, 23.4 at 256); a lone entry wants
+        // enough granules to spread over the GPU (one slot at 512 keys: 9.4 us
+        // at 256, 10.6 at 1024; at 8193 keys: 13.6 us at 512, 17.8 at 1024).
+        // So: 256 keys up to 1024 keys, 1024 up to 8192, and beyond that as
+        // many granules as the merge takes (512 keys up to 16384).
+        want = L <= 1024 ? 256 : L <= 8192 ? 1024 : ((int64_t)L + gmax - 1) / gmax;
+    }
     return (int)((want + q - 1) / q * q);
 }
 
@@ -178,7 +193,8 @@ constexpr int kMaxRunKeys = 1 << 22;
 
 void plan_decode_granules(qasr::DecodePlan& P, int nkvh, int cus) {
     const int target = std::max(1, std::min(env_int("QASR_DECODE_WGS", cus), 8192));
-    const int gmin = std::max(qasr::kDecodeGranuleQuantum, env_int("QASR_DECODE_GRANULE", qasr::kDecodeMinGranule));
+    const int genv = env_int("QASR_DECODE_GRANULE", 0);  // > 0: max(this, len / max granules)
+    const int gmin = genv > 0 ? std::max(qasr::kDecodeGranuleQuantum, genv) : 0;
     const int gmax = std::max(1, std::min(env_int("QASR_DECODE_MAX_GRANULES", qasr::kDecodeMaxGranules),
                                           qasr::kDecodeMaxGranules));
     int ngr[qasr::kMaxBatch], run[qasr::kMaxBatch];
@@ -187,11 +203,14 @@ void plan_decode_granules(qasr::DecodePlan& P, int nkvh, int cus) {
     for (int i = 0; i < P.batch; ++i) {
         P.gran[i] = granule_keys(P.len[i], gmin, gmax);
         ngr[i] = ceil_div(P.len[i], P.gran[i]);
-        run[i] = std::max(1, std::min(ngr[i], kMaxRunKeys / P.gran[i]));
+        run[i] = std::max(1, std::min({ngr[i], kMaxRunKeys / P.gran[i], qasr::kDecodeMaxRunGranules}));
         keys += (int64_t)nkvh * P.len[i];
         pairs += nkvh;
     }
-    if (pairs < target) {
+    const bool split = env_int("QASR_DECODE_SPLIT", 1) != 0;  // 0: every (entry, kv head) whole
+    if (!split) {
+        // runs as long as a workgroup's LDS allows (kDecodeMaxRunGranules)
+    } else if (pairs < target) {
         auto runs_for = [&](int64_t c, int i) {
             return (int)std::max<int64_t>(1, std::min<int64_t>(run[i], c / P.gran[i]));
         };

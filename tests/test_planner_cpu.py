@@ -30,14 +30,19 @@ def splitmix_lengths(seed: int, n: int, lo: int, hi: int):
     return out
 
 
-def granule(L: int, gmin: int = 256, gmax: int = 32) -> int:
-    """The granule rule, restated: the smallest multiple of 256 keys (two
-    workgroup passes) that is at least gmin and leaves at most gmax granules."""
-    want = max(gmin, -(-L // gmax))
+def granule(L: int, gmin: int = 0, gmax: int = 32) -> int:
+    """The granule rule, restated: a multiple of 256 keys (two workgroup
+    passes); by default 256 keys up to 1024 keys, 1024 up to 8192 and
+    len / 32 beyond; with a forced gmin, the smallest multiple that is at
+    least gmin and leaves at most gmax granules."""
+    if gmin:
+        want = max(gmin, -(-L // gmax))
+    else:
+        want = 256 if L <= 1024 else 1024 if L <= 8192 else -(-L // gmax)
     return -(-want // 256) * 256
 
 
-def check_decode_plan(lens, plan, nkvh=NKVH, gmin=256, gmax=32):
+def check_decode_plan(lens, plan, nkvh=NKVH, gmin=0, gmax=32):
     gran, run, base = plan
     assert base[0] == 0
     parts = 0
@@ -47,7 +52,7 @@ def check_decode_plan(lens, plan, nkvh=NKVH, gmin=256, gmax=32):
         ngr = -(-L // g)
         # granules [i g, min((i+1) g, L)) for i < ngr: none empty, none past L
         assert (ngr - 1) * g < L <= ngr * g and ngr <= 32
-        assert 1 <= r <= ngr
+        assert 1 <= r <= min(ngr, 16)  # a run's wave partials fit the workgroup's LDS
         assert base[b + 1] - base[b] == nkvh * -(-ngr // r), (b, L, g, r)
         parts += nkvh * ngr
     assert parts <= 64 * nkvh * 32  # the workspace's partial records
@@ -69,8 +74,11 @@ def test_decode_plan_covers_every_key_random_batches():
         check_decode_plan(lens, plan)
         base = plan[2]
         assert base[-1] >= NKVH * n
-        if NKVH * n < 256:  # the budget is one workgroup per CU unless the batch alone exceeds it
-            assert base[-1] <= 256
+        # the budget is one workgroup per CU unless the batch alone exceeds it
+        # (or its runs would pass 16 granules)
+        floor = sum(NKVH * -(-(-(-L // granule(L))) // 16) for L in lens)
+        if NKVH * n < 256:
+            assert base[-1] <= max(256, floor)
 
 
 def test_decode_granules_do_not_depend_on_the_batch():
@@ -90,7 +98,8 @@ def test_decode_plan_bench_configs():
     lens3 = [L + 1 for L in splitmix_lengths(SPLITMIX_SEED_CONFIG3, 16, 400, 2400)]
     gran, run, base = plan = qasr_attn.plan_decode(lens3, NKVH, 256)
     check_decode_plan(lens3, plan)
-    assert gran == [256] * 16 and 240 <= base[-1] <= 256  # config 3: about one workgroup per CU
+    assert gran == [1024 if L > 1024 else 256 for L in lens3]
+    assert 240 <= base[-1] <= 256  # config 3: about one workgroup per CU
     gran, run, base = plan = qasr_attn.plan_decode([8193], NKVH, 256)
     assert gran == [512] and run == [1] and base == [0, 8 * 17]  # config 4: 17 granules
     gran, run, base = qasr_attn.plan_decode([512], NKVH, 256)
@@ -98,7 +107,7 @@ def test_decode_plan_bench_configs():
     lens = [1, 2, 255, 256, 257, 4096, 8192]
     gran, run, base = plan = qasr_attn.plan_decode(lens, NKVH, 256)
     check_decode_plan(lens, plan)
-    assert gran == [256] * 7 and base[-1] <= 256
+    assert gran == [256] * 5 + [1024] * 2 and base[-1] <= 256
     assert run[:4] == [1, 1, 1, 1]  # one granule each
     # a batch past the budget (64 entries x 8 kv heads) splits only its longest entries
     lens = [100] * 63 + [4000]
@@ -120,6 +129,10 @@ def test_decode_plan_knobs(monkeypatch):
     check_decode_plan(lens, plan, gmin=768, gmax=4)
     plan = qasr_attn.plan_decode([3000, 3000], NKVH, 256)
     assert plan[1] == [4, 4]  # equal entries stay whole: one workgroup per (entry, kv head)
+    monkeypatch.setenv("QASR_DECODE_GRANULE", "256")
+    monkeypatch.delenv("QASR_DECODE_MAX_GRANULES")
+    plan = qasr_attn.plan_decode([8000, 8000], NKVH, 256)
+    assert plan[1] == [16, 16]  # whole entries, but a run holds at most 16 granules
     monkeypatch.setenv("QASR_DECODE_WGS", "4096")
     plan = qasr_attn.plan_decode(lens, NKVH, 256)
     assert plan[1] == [1, 1, 1]
