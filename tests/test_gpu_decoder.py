@@ -5,19 +5,27 @@ oracle's TextDecoder), on seeded random weights of the Qwen3-ASR decoder
 shapes (no checkpoint exists offline).
 
 The two sides differ by rounding (GEMM summation order, tree sums in the
-norms): logits must agree to 2% of their spread at every step, and the greedy
-token streams must be identical at every step on these seeds
-(decoder_model.compare_greedy), at both decoder shapes.
+norms): logits must agree to 2% of their spread at every step.  The greedy
+comparison is teacher-forced: both sides take the CPU reference's previous
+token at every step, and every step's argmax must agree except at a near-tie
+(the CPU's top-2 margin below twice that step's logit difference), which is
+counted and recorded (decoder_model.compare_teacher_forced), over a
+pre-declared list of 8 seeds per test (16 distinct prompts for the 16-slot
+test), at both decoder shapes.
 """
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
-from decoder_model import CFG_0P6B, CFG_1P7B, compare_greedy, host_bits, synth_weights
+from decoder_model import (CFG_0P6B, CFG_1P7B, compare_teacher_forced, host_bits,
+                           synth_weights)
 from workloads import SEED_BASE
 
 pytestmark = pytest.mark.gpu
+
+# Pre-declared seed offsets of the teacher-forced greedy checks.
+SEEDS = (910, 930, 940, 950, 960, 970, 980, 990)
 
 
 def _prompt(seed: int, rows: int, hs: int):
@@ -41,78 +49,57 @@ def _logits(vocab):
     return torch.empty(vocab, dtype=torch.float32, device="cuda")
 
 
-def test_native_decoder_greedy_0p6b_single_slot(O, gpu):
-    """0.6B shape, 28 layers, full vocabulary: a 40-row prompt, 16 steps."""
+def _teacher_forced_single(O, cfg, wseed, label, s=40, steps=16):
+    """One set of weights; for each pre-declared seed a prompt of s rows and
+    `steps` teacher-forced steps, CPU reference decoder against the native
+    GPU decoder (one slot, re-prefilled from position 0 per seed)."""
     from gpu_helpers import say
 
-    cfg = dict(CFG_0P6B)
-    s, steps = 40, 16
-    W = synth_weights(cfg, SEED_BASE + 920, device="cuda")
+    W = synth_weights(cfg, SEED_BASE + wseed, device="cuda")
     Wh = host_bits(W)
-    hidden = _prompt(SEED_BASE + 921, s, cfg["hs"])
     cos, sin = O.text_rope_tables_f16(cfg["max_seq"])
-    say("native decoder 0.6B: CPU reference decoder")
-    cpu = O.TextDecoder(cfg, Wh, 1024, cos, sin)
-    cpu_out = [cpu.prefill(hidden.cpu().numpy().view(np.uint16), 0)]
-    for _ in range(steps):
-        cpu_out.append(cpu.step())
-    cpu.close()
-    del Wh
-
-    say("native decoder 0.6B: GPU")
     dec = _native(cfg, W, 1, 1024)
     lg = _logits(cfg["vocab"])
-    tok = dec.prefill(hidden, 0, logits=lg)
-    gpu_out = [(tok, lg.cpu().numpy())]
     lgb = lg.view(1, -1)
-    for _ in range(steps):
-        t = dec.step(logits=lgb)[0]
-        gpu_out.append((t, lgb[0].cpu().numpy()))
+    flips = 0
+    for seed in SEEDS:
+        hidden = _prompt(SEED_BASE + seed + 11, s, cfg["hs"])
+        say(f"native decoder {label} seed {seed}: CPU reference decoder")
+        cpu = O.TextDecoder(cfg, Wh, 1024, cos, sin)
+        cpu_out = [cpu.prefill(hidden.cpu().numpy().view(np.uint16), 0)]
+        for _ in range(steps):
+            cpu_out.append(cpu.step())
+        cpu.close()
+        say(f"native decoder {label} seed {seed}: GPU")
+        tok = dec.prefill(hidden, 0, logits=lg)
+        gpu_out = [(tok, lg.cpu().numpy())]
+        for k in range(steps):
+            dec.last[0] = cpu_out[k][0]  # teacher forcing
+            t = dec.step(logits=lgb)[0]
+            gpu_out.append((t, lgb[0].cpu().numpy()))
+        flips += compare_teacher_forced(cpu_out, gpu_out, f"native {label} seed {seed}")
     dec.close()
-    say(f"cpu tokens {[t for t, _ in cpu_out]}")
-    say(f"gpu tokens {[t for t, _ in gpu_out]}")
-    compare_greedy(cpu_out, gpu_out, "native 0.6B")
+    print(f"native {label}: {flips} near-tie disagreements over {len(SEEDS)} seeds x {steps + 1} steps")
 
 
-def test_native_decoder_greedy_1p7b_single_slot(O, gpu):
-    """1.7B shape, 28 layers, full vocabulary: a 40-row prompt, 16 steps;
-    identical token streams against the oracle's CPU decoder."""
-    from gpu_helpers import say
+def test_native_decoder_teacher_forced_0p6b_single_slot(O, gpu):
+    """0.6B shape, 28 layers, full vocabulary: per seed a 40-row prompt and
+    16 teacher-forced steps."""
+    _teacher_forced_single(O, dict(CFG_0P6B), 920, "0.6B")
 
-    cfg = dict(CFG_1P7B)
-    s, steps = 40, 16
-    W = synth_weights(cfg, SEED_BASE + 1300, device="cuda")
-    Wh = host_bits(W)
-    hidden = _prompt(SEED_BASE + 1301, s, cfg["hs"])
-    cos, sin = O.text_rope_tables_f16(cfg["max_seq"])
-    say("native decoder 1.7B: CPU reference decoder")
-    cpu = O.TextDecoder(cfg, Wh, 1024, cos, sin)
-    cpu_out = [cpu.prefill(hidden.cpu().numpy().view(np.uint16), 0)]
-    for _ in range(steps):
-        cpu_out.append(cpu.step())
-    cpu.close()
-    del Wh
 
-    say("native decoder 1.7B: GPU")
-    dec = _native(cfg, W, 1, 1024)
-    lg = _logits(cfg["vocab"])
-    tok = dec.prefill(hidden, 0, logits=lg)
-    gpu_out = [(tok, lg.cpu().numpy())]
-    lgb = lg.view(1, -1)
-    for _ in range(steps):
-        t = dec.step(logits=lgb)[0]
-        gpu_out.append((t, lgb[0].cpu().numpy()))
-    dec.close()
-    say(f"cpu tokens {[t for t, _ in cpu_out]}")
-    say(f"gpu tokens {[t for t, _ in gpu_out]}")
-    compare_greedy(cpu_out, gpu_out, "native 1.7B")
+def test_native_decoder_teacher_forced_1p7b_single_slot(O, gpu):
+    """1.7B shape, 28 layers, full vocabulary: per seed a 40-row prompt and
+    16 teacher-forced steps."""
+    _teacher_forced_single(O, dict(CFG_1P7B), 1300, "1.7B")
 
 
 def test_native_decoder_1p7b_16_slot_batched_steps(O, gpu):
     """1.7B shape, 28 layers, full vocabulary, 16 slots (--batch 16): each
-    slot's prompt (3-18 rows) is prefilled, then two steps run all 16 slots
-    in one batch (the skinny GEMM's 16-row case and 16-entry decode
-    attention).  Every slot's tokens equal its own CPU reference decoder's."""
+    slot's prompt (3-18 rows, 16 distinct prompt seeds) is prefilled, then
+    two teacher-forced steps run all 16 slots in one batch (the skinny GEMM's
+    16-row case and 16-entry decode attention), each slot against its own
+    CPU reference decoder."""
     import torch
 
     from gpu_helpers import say
@@ -143,31 +130,34 @@ def test_native_decoder_1p7b_16_slot_batched_steps(O, gpu):
         tok = dec.prefill(prompts[i], 0, slot=i, logits=lg)
         gpu_out.append([(tok, lg.cpu().numpy())])
     lgb = torch.empty((nslot, cfg["vocab"]), dtype=torch.float32, device="cuda")
-    for _ in range(steps):
+    for k in range(steps):
+        for i in range(nslot):
+            dec.last[i] = cpu_out[i][k][0]  # teacher forcing
         toks = dec.step(list(range(nslot)), logits=lgb)
         host = lgb.cpu().numpy()
         for i in range(nslot):
             gpu_out[i].append((toks[i], host[i]))
     dec.close()
     for i in range(nslot):
-        compare_greedy(cpu_out[i], gpu_out[i], f"native 1.7B slot {i}")
+        compare_teacher_forced(cpu_out[i], gpu_out[i], f"native 1.7B slot {i}")
 
 
-def test_native_decoder_two_slots_chunked_prefill(O, gpu):
+@pytest.mark.parametrize("seed", SEEDS)
+def test_native_decoder_two_slots_chunked_prefill(O, gpu, seed):
     """Two sequences, 2 layers of the 0.6B shape: prompts of 1100 and 700 rows
-    prefilled in 512-row calls (max_rows), then 12 batched steps of both
-    slots with split-K decode contexts."""
+    prefilled in 512-row calls (max_rows), then 12 teacher-forced batched
+    steps of both slots with split-K decode contexts."""
     from gpu_helpers import say
 
     cfg = dict(CFG_0P6B, layers=2)
     lens, steps = [1100, 700], 12
-    W = synth_weights(cfg, SEED_BASE + 930, device="cuda")
+    W = synth_weights(cfg, SEED_BASE + seed, device="cuda")
     Wh = host_bits(W)
     cos, sin = O.text_rope_tables_f16(cfg["max_seq"])
-    prompts = [_prompt(SEED_BASE + 931 + i, L, cfg["hs"]) for i, L in enumerate(lens)]
+    prompts = [_prompt(SEED_BASE + seed + 1 + i, L, cfg["hs"]) for i, L in enumerate(lens)]
     cpu_out = []
     for i, L in enumerate(lens):
-        say(f"native decoder batch: CPU reference, slot {i}")
+        say(f"native decoder batch seed {seed}: CPU reference, slot {i}")
         cpu = O.TextDecoder(cfg, Wh, 2048, cos, sin)
         h = prompts[i].cpu().numpy().view(np.uint16)
         for k0 in range(0, L, 512):
@@ -179,7 +169,7 @@ def test_native_decoder_two_slots_chunked_prefill(O, gpu):
         cpu.close()
     del Wh
 
-    say("native decoder batch: GPU")
+    say(f"native decoder batch seed {seed}: GPU")
     import torch
 
     dec = _native(cfg, W, 2, 1024, max_rows=512)
@@ -189,14 +179,16 @@ def test_native_decoder_two_slots_chunked_prefill(O, gpu):
         tok = dec.prefill(prompts[i], 0, slot=i, logits=lg)  # chunks of 512 rows inside
         gpu_out.append([(tok, lg.cpu().numpy())])
     lgb = torch.empty((2, cfg["vocab"]), dtype=torch.float32, device="cuda")
-    for _ in range(steps):
+    for k in range(steps):
+        for i in range(2):
+            dec.last[i] = cpu_out[i][k][0]  # teacher forcing
         toks = dec.step([0, 1], logits=lgb)
         for i in range(2):
             gpu_out[i].append((toks[i], lgb[i].cpu().numpy()))
     assert dec.kv.cap >= max(lens) + steps
     dec.close()
     for i in range(2):
-        compare_greedy(cpu_out[i], gpu_out[i], f"native slot {i}")
+        compare_teacher_forced(cpu_out[i], gpu_out[i], f"native seed {seed} slot {i}")
 
 
 def test_native_decoder_step_graph_replays_equal_eager(O, gpu):
