@@ -48,6 +48,11 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 __device__ __forceinline__ void dma16(u32x4v rsrc, int voff, uint32_t lds) {
     asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
 }
+// The same copy as a device-coherent (sc1) load: it reads what other
+// workgroups published with device-scope stores.
+__device__ __forceinline__ void dma16_sc1(u32x4v rsrc, int voff, uint32_t lds) {
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen sc1 lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds) : "memory");
+}
 
 // ---- DPP cross-lane moves inside a 16-lane row (no LDS traffic) ----------
 template <int CTRL>

@@ -132,8 +132,17 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     // unnormalised output of both heads.
     __shared__ float s_wm[kMaxRunG][W][2];
     __shared__ float s_wl[kMaxRunG][W][2];
-    __shared__ __attribute__((aligned(16))) float s_wa[kMaxRunG][W][2][kHeadDim];
+    // The run's wave partials (unnormalised output of both heads), and once
+    // they are published, the last arrival's copies of the pair's granule
+    // outputs: one buffer.
+    __shared__ __attribute__((aligned(16))) float s_big[kMaxG * 2 * kHeadDim];
+    static_assert(kMaxRunG * W <= kMaxG, "the wave partials fit the merge buffer");
+    float(*s_wa)[W][2][kHeadDim] = reinterpret_cast<float(*)[W][2][kHeadDim]>(s_big);
+    float(*s_x)[2 * kHeadDim] = reinterpret_cast<float(*)[2 * kHeadDim]>(s_big);
     __shared__ int s_last;
+    // The last arrival's copies of the granule partials: (m0, m1, l0, l1)
+    // and the unnormalised output of both heads per granule.
+    __shared__ __attribute__((aligned(16))) float s_ml[kMaxG][4];
 
     const int wg = blockIdx.x;
     const int tid = threadIdx.x;
@@ -490,52 +499,30 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     __syncthreads();
     if (!s_last) return;
 
-    // Last arrival: each thread requests the (m, l) of its head and its
-    // element of every granule at once, as plain device-coherent (sc1) loads
-    // into a batch of 4, 8, 16 or 32 slots sized to the granule count (unused
-    // slots read granule 0 and get weight 0): one memory round trip, and the
-    // arithmetic has no branches.
-    const __amdgpu_buffer_rsrc_t acc_res = make_rsrc(ws_acc + part0 * (2 * kHeadDim), ngr * (2 * kHeadDim) * 4);
-    const __amdgpu_buffer_rsrc_t ml_res = make_rsrc(ws_ml + part0 * 4, ngr * 16);
-    auto ld_ml = [&](int i, int k) {  // k: 0 = m, 2 = l
-        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ml_res, (i * 4 + k + h) * 4, 0, kSc1));
-    };
-    auto ld_acc = [&](int i) {
-        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                             acc_res, (i * (2 * kHeadDim) + h * kHeadDim + j) * 4, 0, kSc1));
-    };
+    // Last arrival: each granule's partial (its 1 KiB output record and its
+    // 16-byte (m0, m1, l0, l1) record) is copied into LDS by one wave, with
+    // device-coherent (sc1) direct global -> LDS loads, all requested at
+    // once: one memory round trip.  Then M = max of the granule maxima and
+    // the weighted sums in granule order, the same arithmetic on the same
+    // values as the in-workgroup merge.  (A plain loop: this code runs once
+    // per pair, from a cold instruction cache.)
+    {
+        const u32x4v acc_res = make_rsrc_words(ws_acc + part0 * (2 * kHeadDim), ngr * (2 * kHeadDim) * 4);
+        const u32x4v ml_res = make_rsrc_words(ws_ml + part0 * 4, ngr * 16);
+        for (int u = wave; u < ngr; u += W) {
+            dma16_sc1(acc_res, u * (2 * kHeadDim * 4) + lane * 16, lds_addr(&s_x[u][0]));
+            if (lane == 0) dma16_sc1(ml_res, u * 16, lds_addr(&s_ml[u][0]));
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies landed
+        __syncthreads();
+    }
+    float M = s_ml[0][h];
+    for (int u = 1; u < ngr; ++u) M = fmaxf(M, s_ml[u][h]);
     float lsum = 0.0f, acc = 0.0f;
-    auto merge_one_batch = [&](auto n_tag) {
-        constexpr int N = decltype(n_tag)::value;
-        float mv[N], lv[N], xv[N];
-#pragma unroll
-        for (int u = 0; u < N; ++u) {
-            const int i = u < ngr ? u : 0;
-            mv[u] = ld_ml(i, 0);
-            lv[u] = ld_ml(i, 2);
-            xv[u] = ld_acc(i);
-        }
-        float M = mv[0];
-#pragma unroll
-        for (int u = 1; u < N; ++u) M = fmaxf(M, mv[u]);  // repeats of granule 0 change nothing
-#pragma unroll
-        for (int u = 0; u < N; ++u) {
-            if (u < ngr) {
-                const float wgt = fast_exp2(mv[u] - M);
-                lsum = fmaf(lv[u], wgt, lsum);
-                acc = fmaf(xv[u], wgt, acc);
-            }
-        }
-    };
-    static_assert(kMaxG == 32, "merge batches");
-    if (ngr <= 4) {
-        merge_one_batch(std::integral_constant<int, 4>{});
-    } else if (ngr <= 8) {
-        merge_one_batch(std::integral_constant<int, 8>{});
-    } else if (ngr <= 16) {
-        merge_one_batch(std::integral_constant<int, 16>{});
-    } else {
-        merge_one_batch(std::integral_constant<int, 32>{});
+    for (int u = 0; u < ngr; ++u) {
+        const float wgt = fast_exp2(s_ml[u][h] - M);
+        lsum = fmaf(s_ml[u][2 + h], wgt, lsum);
+        acc = fmaf(s_x[u][h * kHeadDim + j], wgt, acc);
     }
     ob[h * kHeadDim + j] = f2h(acc / lsum);
     if (tid == 0) ticket_reset(ctr);

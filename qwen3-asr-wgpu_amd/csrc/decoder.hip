@@ -350,8 +350,8 @@ constexpr int kSc1 = 16;              // buffer cache policy: device-coherent (s
 constexpr int kSkinnyMaxTiles = 512;  // column tiles of a split (groups > 1) projection
 constexpr int kSkinnyMaxGroups = 12;
 constexpr int kSkinnyTargetWgs = 512;
-constexpr int kSkinnySplitWgs = 256;
-constexpr int kSkinnySplitMinK = 3072;  // shortest K cut across workgroups  // a split projection: one workgroup per CU
+constexpr int kSkinnySplitWgs = 256;    // a split projection: one workgroup per CU
+constexpr int kSkinnySplitMinK = 3072;  // shortest K cut across workgroups
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int64_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,

@@ -55,7 +55,7 @@ constexpr int kDecodeTileKeys = 32;   // keys per wave pass
 constexpr int kDecodeWgKeys = kDecodeWaves * kDecodeTileKeys;  // keys per workgroup pass
 constexpr int kDecodeGranuleQuantum = 2 * kDecodeWgKeys;        // granules are multiples of this
 constexpr int kDecodeMaxGranules = 32;  // granules per entry: the merge reads them in one round trip
-constexpr int kDecodeMaxRunGranules = 16;  // granules of one workgroup's run (wave partials in LDS)
+constexpr int kDecodeMaxRunGranules = 8;  // granules of one workgroup's run (wave partials in LDS)
 
 // Split-K workspace of one launch: per granule partial the unnormalised
 // output of both q heads (2 x 128 f32) and (max, sum) per head, plus one

@@ -53,7 +53,7 @@ void decode_case(const std::vector<int32_t>& lens, int nkvh, int cus) {
         const int64_t ngr = (L + g - 1) / g;
         check((ngr - 1) * g < L && L <= ngr * g, "granules do not tile the entry", L, g);
         check(ngr <= 32, "granules per entry", ngr);
-        check(r >= 1 && r <= ngr && r <= 16 && r * g <= (1 << 22) + g, "granules per workgroup", b, r);
+        check(r >= 1 && r <= ngr && r <= 8 && r * g <= (1 << 22) + g, "granules per workgroup", b, r);
         if (r <= 0) continue;
         check((int64_t)base[b + 1] - base[b] == nkvh * ((ngr + r - 1) / r), "wg_base step", b,
               base[b + 1] - base[b]);

@@ -52,7 +52,7 @@ def check_decode_plan(lens, plan, nkvh=NKVH, gmin=0, gmax=32):
         ngr = -(-L // g)
         # granules [i g, min((i+1) g, L)) for i < ngr: none empty, none past L
         assert (ngr - 1) * g < L <= ngr * g and ngr <= 32
-        assert 1 <= r <= min(ngr, 16)  # a run's wave partials fit the workgroup's LDS
+        assert 1 <= r <= min(ngr, 8)  # a run's wave partials fit the workgroup's LDS
         assert base[b + 1] - base[b] == nkvh * -(-ngr // r), (b, L, g, r)
         parts += nkvh * ngr
     assert parts <= 64 * nkvh * 32  # the workspace's partial records
@@ -75,8 +75,8 @@ def test_decode_plan_covers_every_key_random_batches():
         base = plan[2]
         assert base[-1] >= NKVH * n
         # the budget is one workgroup per CU unless the batch alone exceeds it
-        # (or its runs would pass 16 granules)
-        floor = sum(NKVH * -(-(-(-L // granule(L))) // 16) for L in lens)
+        # (or its runs would pass 8 granules)
+        floor = sum(NKVH * -(-(-(-L // granule(L))) // 8) for L in lens)
         if NKVH * n < 256:
             assert base[-1] <= max(256, floor)
 
@@ -132,7 +132,7 @@ def test_decode_plan_knobs(monkeypatch):
     monkeypatch.setenv("QASR_DECODE_GRANULE", "256")
     monkeypatch.delenv("QASR_DECODE_MAX_GRANULES")
     plan = qasr_attn.plan_decode([8000, 8000], NKVH, 256)
-    assert plan[1] == [16, 16]  # whole entries, but a run holds at most 16 granules
+    assert plan[1] == [8, 8]  # whole entries, but a run holds at most 8 granules
     monkeypatch.setenv("QASR_DECODE_WGS", "4096")
     plan = qasr_attn.plan_decode(lens, NKVH, 256)
     assert plan[1] == [1, 1, 1]
