@@ -203,9 +203,13 @@ int qasr_prefill_layer(qasr_ctx* ctx, qasr_kv* kv, int layer, int slot, int kv_s
  * down_proj + residual; final RMSNorm, logits against the tied embedding and
  * the greedy argmax.  Rounding follows the reference: f32 math, one f16
  * rounding per op output (a residual add rounds x + dot once), f32 logits,
- * the first maximal index on ties.  The projections are rocBLAS f16 GEMMs
- * with f32 accumulation; their summation order differs from the reference's,
- * so logits agree to rounding, not bitwise.
+ * the first maximal index on ties.  The projections run this library's own
+ * MFMA kernels with f32 accumulation: the skinny decode-step kernels and, for
+ * prefill, the tiled GEMM of gemm.hip (QASR_PREFILL_GEMM=blas: rocBLAS
+ * instead); their summation order differs from the reference's, so logits
+ * agree to rounding, not bitwise.  The order is fixed per shape (it never
+ * depends on how many rows or slots a call carries), so a slot's or a
+ * prompt's results are the same bits alone and in any batch.
  *
  * Weights are device pointers owned by the caller and must outlive the
  * decoder; f16 bits, row-major [out][in] as in the checkpoint.  A projection
@@ -343,7 +347,7 @@ int qasr_mfma_probe(qasr_ctx* ctx, int mode, int wgs, int waves, int mfma_iters,
  * Decode (qasr_decode_attn / qasr_decode_step): `batch` (1..64) entries
  * attending lens[b] >= 1 keys, `nkvh` kv heads, a device of `cus` compute
  * units; the QASR_DECODE_WGS / _GRANULE / _MAX_GRANULES environment knobs
- * apply.  gran_out[b]: keys per granule of entry b (a multiple of 128 and a
+ * apply.  gran_out[b]: keys per granule of entry b (a multiple of 256 and a
  * function of lens[b] alone: the entry's output bits do not depend on its
  * batch mates); run_out[b]: granules per workgroup; wg_base_out[0..batch]:
  * entry b's workgroups are wg_base_out[b] .. wg_base_out[b+1]-1

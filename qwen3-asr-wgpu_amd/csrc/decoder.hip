@@ -16,12 +16,14 @@
 // and the first maximal index (458-485).
 //
 // The projections of a decode step run this file's skinny MFMA kernels; the
-// prefill projections are plain GEMMs and go to rocBLAS (f16 operands, f32
-// accumulation, one f16 rounding of the f32 result; a residual add is the
-// GEMM's beta = 1 term, so x + dot is rounded once as in batch_dot_acc), or
-// with QASR_PREFILL_GEMM=own to gemm.hip's MFMA kernel (same rounding points;
-// it measured 1.4-2.5x slower than the library at these shapes).  The
-// elementwise steps are small HIP kernels below.  Nothing here allocates per
+// prefill projections are plain GEMMs and run gemm.hip's MFMA kernel (f16
+// operands, f32 accumulation, one f16 rounding of the f32 result; with a
+// residual, x + dot is rounded once as in batch_dot_acc).  Its summation order
+// does not depend on the row count, so a prompt prefilled alone and inside a
+// batch gives the same bits (the library's stream-K kernels split K by the
+// row count).  QASR_PREFILL_GEMM=blas sends them to rocBLAS instead (beta = 1
+// for the residual; measured 1.4-2.5x faster at these shapes, not row
+// invariant).  The elementwise steps are small HIP kernels below.  Nothing here allocates per
 // call: the activation workspace is sized for max_rows at creation, and
 // rocBLAS gets a fixed workspace so that a step can be captured in a graph.
 
@@ -380,7 +382,7 @@ __device__ __forceinline__ qasr::half8v dequant8(uint32_t lo, uint32_t hi, float
 }
 
 // Prefill-side int8 projections: the layer's weights dequantized once into a
-// scratch f16 matrix for rocBLAS, out[n][k] = f16(q[n][k] * scale[n]).
+// scratch f16 matrix for the GEMM, out[n][k] = f16(q[n][k] * scale[n]).
 __global__ __launch_bounds__(256) void dequant_rows_kernel(const int8_t* __restrict__ q,
                                                            const float* __restrict__ scale,
                                                            int64_t n_rows, int k,
