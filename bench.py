@@ -561,7 +561,8 @@ def bench_prefill_one(model: str, rows: int, steps: int, warmup: int, seed: int 
 
 
 GEMM_SHAPES = [(4269, 4096, 2048, False), (4269, 2048, 2048, True), (4269, 12288, 2048, False),
-               (4269, 2048, 6144, True), (420, 2048, 6144, True), (16384, 12288, 2048, False)]
+               (4269, 2048, 6144, True), (420, 4096, 2048, False), (420, 2048, 2048, True),
+               (420, 12288, 2048, False), (420, 2048, 6144, True), (16384, 12288, 2048, False)]
 
 
 def bench_gemm(steps: int, warmup: int, seed: int = 31):

@@ -6,8 +6,8 @@
 // the reference's batched projections (cpu_decoder.rs:45-62 batch_dot_acc,
 // 398-449; dispatched on the GPU by decoder.rs:3580-4162).
 //
-// Block tile BM x BN (256 x 256, or 256 x 128 / 128 x 128 when the larger
-// grid would leave CUs idle), K steps of 64, four waves in a 2 x 2 grid, each
+// Block tile BM x BN (256 x 256 down to 64 x 64, chosen per shape by a cost
+// model: launch_gemm_f16), K steps of 64, four waves in a 2 x 2 grid, each
 // wave (BM/2) x (BN/2) as (BM/64) x (BN/64) tiles of v_mfma_f32_32x32x16_f16.
 // Per K step the wave runs four 16-k slices; the next slice's operand reads
 // are issued as one group ahead of the current slice's MFMAs, and the next
@@ -27,6 +27,8 @@
 // and B blocks in its L2.
 // Results are rounded and stored in place; with the residual they go
 // through LDS first, so C is read and written in 8-byte row pieces.
+
+#include <algorithm>
 
 #include "kernels.hpp"
 
@@ -271,12 +273,37 @@ bool gemm_f16_fits(int M, int N, int K) {
 hipError_t launch_gemm_f16(const f16* A, const f16* B, f16* C, int M, int N, int K, bool accumulate,
                            int cus, hipStream_t stream) {
     if (!gemm_f16_fits(M, N, K)) return hipErrorInvalidValue;
-    // 256 x 256 blocks when they give every CU a block, else 256 x 128, else
-    // 128 x 128.
-    const int64_t mb256 = (M + 255) / 256;
-    if (mb256 * (N / 256) >= cus) return launch_shape<256, 256>(A, B, C, M, N, K, accumulate, stream);
-    if (mb256 * (N / 128) >= cus || M > 128) return launch_shape<256, 128>(A, B, C, M, N, K, accumulate, stream);
-    return launch_shape<128, 128>(A, B, C, M, N, K, accumulate, stream);
+    // Block tile: the one with the least predicted time, rounds of
+    // workgroups x tile area x a per-area cost of the shape.  Tiles up to
+    // 128 x 128 fit two workgroups per CU (LDS), so a round is 2 x cus of
+    // them at twice the time.  The costs per unit area (256 x 256 = 1) come
+    // from one sweep over the 1.7B projections at 420 and 4,269 rows and a
+    // 16384 x 12288 x 2048 product (the best tile per shape measured from
+    // 256 x 256 down to 64 x 64; this model picks within 0.5% of it at every
+    // shape).  Every tile accumulates each output over K in the same order,
+    // so the choice never changes a result's bits.
+    struct Cand { int bm, bn, occ; float cost; };
+    constexpr Cand cands[] = {{256, 256, 1, 1.0f}, {128, 128, 2, 1.05f}, {64, 128, 2, 1.3f},
+                              {128, 64, 2, 1.3f}, {64, 64, 2, 1.6f}};
+    int best = 0;
+    double best_t = 0.0;
+    for (int i = 0; i < (int)(sizeof cands / sizeof cands[0]); ++i) {
+        const Cand& c = cands[i];
+        const int64_t tiles = (int64_t)((M + c.bm - 1) / c.bm) * (N / c.bn);
+        const int64_t slots = (int64_t)c.occ * std::max(1, cus);
+        const double t = (double)((tiles + slots - 1) / slots) * c.occ * c.bm * c.bn * c.cost;
+        if (i == 0 || t < best_t) {
+            best = i;
+            best_t = t;
+        }
+    }
+    switch (best) {
+        case 0: return launch_shape<256, 256>(A, B, C, M, N, K, accumulate, stream);
+        case 1: return launch_shape<128, 128>(A, B, C, M, N, K, accumulate, stream);
+        case 2: return launch_shape<64, 128>(A, B, C, M, N, K, accumulate, stream);
+        case 3: return launch_shape<128, 64>(A, B, C, M, N, K, accumulate, stream);
+        default: return launch_shape<64, 64>(A, B, C, M, N, K, accumulate, stream);
+    }
 }
 
 }  // namespace qasr
