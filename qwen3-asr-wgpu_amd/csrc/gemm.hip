@@ -29,6 +29,7 @@
 // through LDS first, so C is read and written in 8-byte row pieces.
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "kernels.hpp"
 
@@ -282,12 +283,16 @@ hipError_t launch_gemm_f16(const f16* A, const f16* B, f16* C, int M, int N, int
     // 256 x 256 down to 64 x 64; this model picks within 0.5% of it at every
     // shape).  Every tile accumulates each output over K in the same order,
     // so the choice never changes a result's bits.
+    // QASR_GEMM_TILE = 1..5 forces candidate 1..5 (the tests compare them).
     struct Cand { int bm, bn, occ; float cost; };
     constexpr Cand cands[] = {{256, 256, 1, 1.0f}, {128, 128, 2, 1.05f}, {64, 128, 2, 1.3f},
                               {128, 64, 2, 1.3f}, {64, 64, 2, 1.6f}};
+    constexpr int kCands = (int)(sizeof cands / sizeof cands[0]);
     int best = 0;
     double best_t = 0.0;
-    for (int i = 0; i < (int)(sizeof cands / sizeof cands[0]); ++i) {
+    const char* forced = std::getenv("QASR_GEMM_TILE");
+    const int f = forced ? std::atoi(forced) : 0;
+    for (int i = 0; i < kCands && !(f >= 1 && f <= kCands); ++i) {
         const Cand& c = cands[i];
         const int64_t tiles = (int64_t)((M + c.bm - 1) / c.bm) * (N / c.bn);
         const int64_t slots = (int64_t)c.occ * std::max(1, cus);
@@ -297,6 +302,7 @@ hipError_t launch_gemm_f16(const f16* A, const f16* B, f16* C, int M, int N, int
             best_t = t;
         }
     }
+    if (f >= 1 && f <= kCands) best = f - 1;
     switch (best) {
         case 0: return launch_shape<256, 256>(A, B, C, M, N, K, accumulate, stream);
         case 1: return launch_shape<128, 128>(A, B, C, M, N, K, accumulate, stream);

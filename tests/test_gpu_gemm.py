@@ -92,3 +92,46 @@ def g_ctx():
         import qasr_attn
         _CTX = qasr_attn.Context()
     return _CTX
+
+
+# Block tiles the launcher chooses from (QASR_GEMM_TILE = 1..5): 256x256,
+# 128x128, 64x128, 128x64, 64x64.
+TILES = [1, 2, 3, 4, 5]
+
+
+@pytest.mark.parametrize("m,n,k,accumulate", [(300, 512, 256, False), (4269, 2048, 2048, True),
+                                              (65, 1024, 3072, True)])
+def test_gemm_tile_choice_keeps_bits(gpu, m, n, k, accumulate, monkeypatch):
+    """Every block tile gives the same bits, so the per-shape tile choice
+    (a function of the row count) cannot make a row's result depend on how
+    many rows the call carries; the default choice is one of them, and the
+    shared result meets the fp32 reference's bound."""
+    import torch
+
+    import qasr_attn
+    from gpu_helpers import say
+
+    g = torch.Generator(device="cuda").manual_seed(7100 + m + n + k)
+    a = torch.randn((m, k), generator=g, device="cuda").to(torch.float16)
+    b = (torch.randn((n, k), generator=g, device="cuda") * 0.05).to(torch.float16)
+    c0 = torch.randn((m, n), generator=g, device="cuda").to(torch.float16)
+    outs = {}
+    for tile in [0] + TILES:
+        if tile:
+            monkeypatch.setenv("QASR_GEMM_TILE", str(tile))
+        else:
+            monkeypatch.delenv("QASR_GEMM_TILE", raising=False)
+        c = c0.clone()
+        say(f"gemm {m}x{n}x{k} tile {tile}")
+        qasr_attn.gemm_f16(g_ctx(), a, b, c, accumulate=accumulate)
+        outs[tile] = c.cpu().numpy()
+    monkeypatch.delenv("QASR_GEMM_TILE", raising=False)
+    for tile in TILES:
+        assert np.array_equal(outs[tile].view(np.uint16), outs[0].view(np.uint16)), tile
+    ref = torch.mm(a.float(), b.float().t().contiguous())
+    mag = torch.mm(a.float().abs(), b.float().abs().t().contiguous())
+    if accumulate:
+        ref, mag = ref + c0.float(), mag + c0.float().abs()
+    ref = ref.cpu().numpy().astype(np.float64)
+    bound = 0.5 * _f16_spacing(ref) + 2 * (k + 1) * 2.0 ** -24 * mag.cpu().numpy()
+    assert np.all(np.abs(outs[0].astype(np.float64) - ref) <= bound)
