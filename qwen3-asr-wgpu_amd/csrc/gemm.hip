@@ -14,9 +14,13 @@
 // step's first reads ahead of the last slice's, so no LDS latency is waited
 // for between MFMAs.
 // Both operand tiles go global -> LDS by direct copies (buffer_load ... lds,
-// one 1 KB block per wave instruction), double buffered: the copies of K
-// step t+2 are issued as soon as every wave is done with step t's buffers,
-// so one step is in flight while another is consumed.  LDS row layout (both
+// one 1 KB block per wave instruction) into NS buffers: the copies of K
+// step t+NS are issued as soon as every wave is done with step t's buffers,
+// so NS-1 steps are in flight while another is consumed.  Two stages for
+// the larger tiles (their LDS then still fits two workgroups per CU up to
+// 128 x 128); four for 64 x 64, whose steps are short and latency-bound
+// (420 x 2048 x 6144: 47.8 -> 30 us; three or four stages on the larger
+// tiles cost the second workgroup per CU and measured slower).  LDS row layout (both
 // operands): row r is 128 bytes (64 k), its 16-byte chunk c at slot
 // c ^ ((r >> 1) & 7), so an operand read (16 consecutive rows, one chunk)
 // covers 16 distinct 16-byte bank groups.  Rows past M are copied from row
@@ -48,7 +52,7 @@ __device__ __forceinline__ float16v mfma32(const half8v& a, const half8v& b, con
 
 __device__ __forceinline__ int slot_of(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
-template <int BM, int BN, bool ACC>
+template <int BM, int BN, int NS, bool ACC>
 __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __restrict__ A,
                                                                const f16* __restrict__ B,
                                                                f16* __restrict__ C, int M, int N,
@@ -57,10 +61,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
     constexpr int MT = WM / 32, NT = WN / 32;
     constexpr int ACOPY = BM * kRowBytes / 1024 / 4;  // copy instructions per wave and step
     constexpr int BCOPY = BN * kRowBytes / 1024 / 4;
-    // Both operand buffers in one array: the epilogue reuses all of it.
-    __shared__ __attribute__((aligned(16))) f16 smem[2 * (BM + BN) * kBK];
+    // NS stages of both operand buffers in one array: the epilogue reuses all
+    // of it.
+    static_assert(NS >= 2 && NS <= 4, "copy stages");
+    __shared__ __attribute__((aligned(16))) f16 smem[NS * (BM + BN) * kBK];
     f16(*As)[BM * kBK] = reinterpret_cast<f16(*)[BM * kBK]>(smem);
-    f16(*Bs)[BN * kBK] = reinterpret_cast<f16(*)[BN * kBK]>(smem + 2 * BM * kBK);
+    f16(*Bs)[BN * kBK] = reinterpret_cast<f16(*)[BN * kBK]>(smem + NS * BM * kBK);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -131,12 +137,21 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
 
     const int nk = K / kBK;
     constexpr int kStepCopies = ACOPY + BCOPY;
-    copy_step(0, 0);
-    if (nk > 1) copy_step(1, 1);
-    if (nk > 1)
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (kStepCopies & 15) | ((kStepCopies >> 4) << 14));
-    else
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    static_assert((NS - 1) * kStepCopies <= 63, "vmcnt range");
+    // Wait until at most `pending` steps' copies are in flight (the older
+    // ones have landed), and for every LDS read of this wave.
+    auto wait_steps = [&](int pending) {
+#define QASR_GEMM_WAIT(P) \
+    __builtin_amdgcn_s_waitcnt(0x0070 | (((P) * kStepCopies) & 15) | ((((P) * kStepCopies) >> 4) << 14))
+        if (NS > 3 && pending >= 3) QASR_GEMM_WAIT(NS > 3 ? 3 : 0);
+        else if (NS > 2 && pending == 2) QASR_GEMM_WAIT(NS > 2 ? 2 : 0);
+        else if (pending == 1) QASR_GEMM_WAIT(1);
+        else QASR_GEMM_WAIT(0);
+#undef QASR_GEMM_WAIT
+    };
+    const int npro = nk < NS ? nk : NS;  // steps copied ahead
+    for (int t = 0; t < npro; ++t) copy_step(t, t);
+    wait_steps(npro - 1);
     __syncthreads();
 
     // Operand registers of two k-slices: slice ks+1's reads are issued as
@@ -160,11 +175,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
     };
     constexpr int kSlices = kBK / 16;
     static_assert(kSlices == 4, "slices 0..2 then the step boundary under slice 3");
-    // K step t from buffer t & 1.  All but the last step end with the step
+    // K step t from buffer t % NS.  All but the last step end with the step
     // boundary (straight-line code, so the compiler's waits track exactly
     // which reads are outstanding).
     auto k_step = [&](int t, bool last) {
-        const int buf = t & 1;
+        const int buf = t % NS;
         const f16* as = As[buf];
         const f16* bs = Bs[buf];
         // Slice 0's reads were issued under the previous step's last MFMAs:
@@ -181,13 +196,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
         }
         // Slice 3's operands are in registers.  Once every wave has them
         // (all of its LDS reads of this buffer returned) and step t+1's
-        // copies have landed, refill this buffer with step t+2 and read
-        // step t+1's slice 0, both under slice 3's MFMAs.
+        // copies have landed (those of the steps after it may still fly),
+        // refill this buffer with step t+NS and read step t+1's slice 0,
+        // both under slice 3's MFMAs.
         if (!last) {
-            __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+            const int newest = t + NS - 1 < nk - 1 ? t + NS - 1 : nk - 1;  // last step copied
+            wait_steps(newest - (t + 1));
             __syncthreads();
-            if (t + 2 < nk) copy_step(t + 2, buf);
-            read_slice(As[buf ^ 1], Bs[buf ^ 1], 0, 0);
+            if (t + NS < nk) copy_step(t + NS, buf);
+            const int nb = (t + 1) % NS;
+            read_slice(As[nb], Bs[nb], 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
         mfma_slice(1);
@@ -223,7 +241,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
     constexpr int EP = WN + 8;      // padded row, floats
     constexpr int CPR = WN / 4;     // 4-column pieces per row
     constexpr int RPP = 64 / CPR;   // rows per pass of the wave
-    static_assert(4 * 32 * EP * 4 <= 2 * (BM + BN) * kBK * 2, "epilogue staging fits the operand buffers");
+    static_assert(4 * 32 * EP * 4 <= NS * (BM + BN) * kBK * 2, "epilogue staging fits the operand buffers");
     float* ep = reinterpret_cast<float*>(smem) + wave * (32 * EP);
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
@@ -253,14 +271,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
     }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int NS = 2>
 hipError_t launch_shape(const f16* A, const f16* B, f16* C, int M, int N, int K, bool accumulate,
                         hipStream_t stream) {
     const dim3 grid((unsigned)(((M + BM - 1) / BM) * (N / BN)));
     if (accumulate)
-        hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, true>), grid, dim3(kThreads), 0, stream, A, B, C, M, N, K);
+        hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, NS, true>), grid, dim3(kThreads), 0, stream, A, B, C, M, N, K);
     else
-        hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, false>), grid, dim3(kThreads), 0, stream, A, B, C, M, N, K);
+        hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, NS, false>), grid, dim3(kThreads), 0, stream, A, B, C, M, N, K);
     return hipGetLastError();
 }
 
@@ -308,7 +326,7 @@ hipError_t launch_gemm_f16(const f16* A, const f16* B, f16* C, int M, int N, int
         case 1: return launch_shape<128, 128>(A, B, C, M, N, K, accumulate, stream);
         case 2: return launch_shape<64, 128>(A, B, C, M, N, K, accumulate, stream);
         case 3: return launch_shape<128, 64>(A, B, C, M, N, K, accumulate, stream);
-        default: return launch_shape<64, 64>(A, B, C, M, N, K, accumulate, stream);
+        default: return launch_shape<64, 64, 4>(A, B, C, M, N, K, accumulate, stream);
     }
 }
 
