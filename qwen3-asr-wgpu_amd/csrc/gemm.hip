@@ -52,6 +52,14 @@ __device__ __forceinline__ float16v mfma32(const half8v& a, const half8v& b, con
 
 __device__ __forceinline__ int slot_of(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
+// s_waitcnt vmcnt(N) lgkmcnt(0): at most N vector memory operations of this
+// wave still in flight, and no LDS operation.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(0x0070 | (N & 15) | ((N >> 4) << 14));
+}
+
 template <int BM, int BN, int NS, bool ACC>
 __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __restrict__ A,
                                                                const f16* __restrict__ B,
@@ -141,13 +149,14 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
     // Wait until at most `pending` steps' copies are in flight (the older
     // ones have landed), and for every LDS read of this wave.
     auto wait_steps = [&](int pending) {
-#define QASR_GEMM_WAIT(P) \
-    __builtin_amdgcn_s_waitcnt(0x0070 | (((P) * kStepCopies) & 15) | ((((P) * kStepCopies) >> 4) << 14))
-        if (NS > 3 && pending >= 3) QASR_GEMM_WAIT(NS > 3 ? 3 : 0);
-        else if (NS > 2 && pending == 2) QASR_GEMM_WAIT(NS > 2 ? 2 : 0);
-        else if (pending == 1) QASR_GEMM_WAIT(1);
-        else QASR_GEMM_WAIT(0);
-#undef QASR_GEMM_WAIT
+        if (NS > 3 && pending >= 3)
+            wait_vm_lgkm0<(NS > 3 ? 3 : 0) * kStepCopies>();
+        else if (NS > 2 && pending == 2)
+            wait_vm_lgkm0<(NS > 2 ? 2 : 0) * kStepCopies>();
+        else if (pending == 1)
+            wait_vm_lgkm0<kStepCopies>();
+        else
+            wait_vm_lgkm0<0>();
     };
     const int npro = nk < NS ? nk : NS;  // steps copied ahead
     for (int t = 0; t < npro; ++t) copy_step(t, t);
@@ -296,10 +305,10 @@ hipError_t launch_gemm_f16(const f16* A, const f16* B, f16* C, int M, int N, int
     // workgroups x tile area x a per-area cost of the shape.  Tiles up to
     // 128 x 128 fit two workgroups per CU (LDS), so a round is 2 x cus of
     // them at twice the time.  The costs per unit area (256 x 256 = 1) come
-    // from one sweep over the 1.7B projections at 420 and 4,269 rows and a
+    // from sweeps over the 1.7B projections at 420 and 4,269 rows and a
     // 16384 x 12288 x 2048 product (the best tile per shape measured from
-    // 256 x 256 down to 64 x 64; this model picks within 0.5% of it at every
-    // shape).  Every tile accumulates each output over K in the same order,
+    // 256 x 256 down to 64 x 64; this model picks it, or one within a few
+    // percent, at every shape).  Every tile accumulates each output over K in the same order,
     // so the choice never changes a result's bits.
     // QASR_GEMM_TILE = 1..5 forces candidate 1..5 (the tests compare them).
     struct Cand { int bm, bn, occ; float cost; };
