@@ -62,18 +62,38 @@ def error_report(got_u16, ref_u16, vec: int = HD) -> dict:
     r = np.asarray(ref_u16, dtype=np.uint16).view(np.float16).astype(np.float64)
     assert g.shape == r.shape
     if g.size == 0:
-        return dict(max_abs=0.0, max_rel=0.0, max_rel_small=0.0, max_rel_vec=0.0)
+        return dict(max_abs=0.0, max_rel=0.0, max_rel_small=0.0, max_rel_vec=0.0, max_ulp=0.0,
+                    max_ulp_big=0.0)
     assert np.all(np.isfinite(r)), "reference has non-finite values"
     if not np.all(np.isfinite(g)):
         inf = float("inf")
-        return dict(max_abs=inf, max_rel=inf, max_rel_small=inf, max_rel_vec=inf)
+        return dict(max_abs=inf, max_rel=inf, max_rel_small=inf, max_rel_vec=inf, max_ulp=inf,
+                    max_ulp_big=inf)
     d = np.abs(g - r)
     ar = np.abs(r)
     dv, rv = d.reshape(-1, vec), r.reshape(-1, vec)
     vn = np.sqrt((dv * dv).sum(1)) / np.maximum(np.sqrt((rv * rv).sum(1)), 1e-30)
+    ulps = d / f16_ulp(r)
+    big = ar >= ULP_BIG_FLOOR
     return dict(max_abs=float(d.max()), max_rel=float((d / np.maximum(ar, REL_FLOOR)).max()),
                 max_rel_small=float((d / np.maximum(ar, REL_FLOOR_SMALL)).max()),
-                max_rel_vec=float(vn.max()))
+                max_rel_vec=float(vn.max()), max_ulp=float(ulps.max()),
+                max_ulp_big=float(ulps[big].max()) if big.any() else 0.0)
+
+
+# max_ulp_big: the largest difference in ulps over outputs of magnitude at
+# least this (where an absolute noise floor no longer dominates the ulp).
+ULP_BIG_FLOOR = 2.0 ** -4
+
+
+def f16_ulp(x):
+    """Spacing of binary16 at |x|: 2^(e - 10) for |x| in [2^e, 2^(e+1)), and
+    the subnormal spacing 2^-24 below 2^-14.  (max_ulp: the largest
+    difference in units of the reference's own last place; 1 is a single
+    final-rounding difference.)"""
+    ax = np.abs(np.asarray(x, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(ax, 2.0 ** -14)))
+    return np.exp2(e - 10)
 
 
 def assert_parity(got_u16, ref_u16, what: str = "", p_f16: bool = False):
@@ -84,7 +104,8 @@ def assert_parity(got_u16, ref_u16, what: str = "", p_f16: bool = False):
     REPORT.append(dict(what=what, p_f16=p_f16, **e))
     msg = (f"{what}: max_abs {e['max_abs']:.3e} (<= {ATOL}), max_rel {e['max_rel']:.3e}, "
            f"max_rel_small {e['max_rel_small']:.3e}, max_rel_vec {e['max_rel_vec']:.3e} "
-           f"(<= {RTOL})")
+           f"(<= {RTOL}), max_ulp {e['max_ulp']:.2f} ({e['max_ulp_big']:.2f} at |ref| >= "
+           f"{ULP_BIG_FLOOR})")
     assert e["max_abs"] <= ATOL and e["max_rel"] <= RTOL and e["max_rel_vec"] <= RTOL, msg
     if not p_f16:
         assert e["max_rel_small"] <= RTOL, msg
