@@ -41,8 +41,9 @@ def test_error_report_figures():
     assert abs(e["max_rel_small"] - abs(d16) / 1e-3) < 1e-9     # near zero: the 1e-3 floor
     assert e["max_ulp"] >= 1.0 and abs(e["max_ulp"] - abs(d16) / f16_ulp(np.float16(-1e-4))) < 1e-9
     assert e["max_ulp_big"] == 1.0  # the one-ulp difference at 3.0; the near-zero one is excluded
+    assert e["ref_at_max_abs"] == 3.0
     # per-head vector norm: row 0 differs by one ulp in one of its two nonzero entries
     r0 = np.sqrt(3.0 ** 2 + 0.5 ** 2)
     assert e["max_rel_vec"] >= 2.0 ** -9 / r0 - 1e-12
     same = error_report(_u16(ref), _u16(ref))
-    assert all(v == 0.0 for v in same.values())
+    assert all(v == 0.0 for k, v in same.items() if k != "ref_at_max_abs")

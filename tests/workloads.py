@@ -63,12 +63,12 @@ def error_report(got_u16, ref_u16, vec: int = HD) -> dict:
     assert g.shape == r.shape
     if g.size == 0:
         return dict(max_abs=0.0, max_rel=0.0, max_rel_small=0.0, max_rel_vec=0.0, max_ulp=0.0,
-                    max_ulp_big=0.0)
+                    max_ulp_big=0.0, ref_at_max_abs=0.0)
     assert np.all(np.isfinite(r)), "reference has non-finite values"
     if not np.all(np.isfinite(g)):
         inf = float("inf")
         return dict(max_abs=inf, max_rel=inf, max_rel_small=inf, max_rel_vec=inf, max_ulp=inf,
-                    max_ulp_big=inf)
+                    max_ulp_big=inf, ref_at_max_abs=inf)
     d = np.abs(g - r)
     ar = np.abs(r)
     dv, rv = d.reshape(-1, vec), r.reshape(-1, vec)
@@ -78,7 +78,8 @@ def error_report(got_u16, ref_u16, vec: int = HD) -> dict:
     return dict(max_abs=float(d.max()), max_rel=float((d / np.maximum(ar, REL_FLOOR)).max()),
                 max_rel_small=float((d / np.maximum(ar, REL_FLOOR_SMALL)).max()),
                 max_rel_vec=float(vn.max()), max_ulp=float(ulps.max()),
-                max_ulp_big=float(ulps[big].max()) if big.any() else 0.0)
+                max_ulp_big=float(ulps[big].max()) if big.any() else 0.0,
+                ref_at_max_abs=float(ar.flat[int(d.argmax())]))
 
 
 # max_ulp_big: the largest difference in ulps over outputs of magnitude at
