@@ -7,9 +7,12 @@
 // 398-449; dispatched on the GPU by decoder.rs:3580-4162).
 //
 // Block tile BM x BN (256 x 256 down to 64 x 64, chosen per shape by a cost
-// model: launch_gemm_f16), K steps of 64, four waves in a 2 x 2 grid, each
-// wave (BM/2) x (BN/2) as (BM/64) x (BN/64) tiles of v_mfma_f32_32x32x16_f16.
-// Per K step the wave runs four 16-k slices; the next slice's operand reads
+// model: launch_gemm_f16), K steps of 64, waves in a 2 x WGN grid (WGN = 2:
+// four waves, one per SIMD; WGN = 4: eight, two per SIMD, so one wave's
+// MFMAs run while the other waits), each wave (BM/2) x (BN/WGN) as tiles of
+// v_mfma_f32_32x32x16_f16.  Eight waves measured faster for 256 x 256
+// (16384 x 12288 x 2048: 764-820 against 820-861 us) and 128 x 128, four for
+// the smaller tiles.  Per K step the wave runs four 16-k slices; the next slice's operand reads
 // are issued as one group ahead of the current slice's MFMAs, and the next
 // step's first reads ahead of the last slice's, so no LDS latency is waited
 // for between MFMAs.
@@ -30,7 +33,10 @@
 // of a few row blocks, so the tiles an XCD runs at one time share a few A
 // and B blocks in its L2.
 // Results are rounded and stored in place; with the residual they go
-// through LDS first, so C is read and written in 8-byte row pieces.
+// through LDS first, so C is read and written in 8-byte row pieces, all of
+// a row tile's residual reads issued before its first store (one memory
+// round trip per row tile; 256 x 256 at 4269 x 2048 x 2048: 72 against
+// 83.5 us).
 
 #include <algorithm>
 #include <cstdlib>
@@ -43,7 +49,6 @@ namespace {
 
 constexpr int kBK = 64;          // k per step
 constexpr int kRowBytes = kBK * 2;  // 128 bytes of one row per step
-constexpr int kThreads = 256;
 constexpr int kGroupRows = 4;  // row blocks per group of an XCD's tile walk
 
 __device__ __forceinline__ float16v mfma32(const half8v& a, const half8v& b, const float16v& c) {
@@ -60,15 +65,19 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
     __builtin_amdgcn_s_waitcnt(0x0070 | (N & 15) | ((N >> 4) << 14));
 }
 
-template <int BM, int BN, int NS, bool ACC>
-__global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __restrict__ A,
-                                                               const f16* __restrict__ B,
-                                                               f16* __restrict__ C, int M, int N,
-                                                               int K) {
-    constexpr int WM = BM / 2, WN = BN / 2;
+template <int BM, int BN, int NS, bool ACC, int WGN>
+__global__ __launch_bounds__(128 * WGN, 1) void gemm_f16_kernel(const f16* __restrict__ A,
+                                                                const f16* __restrict__ B,
+                                                                f16* __restrict__ C, int M, int N,
+                                                                int K) {
+    constexpr int kWaves = 2 * WGN;  // 2 x WGN wave grid
+    constexpr int WM = BM / 2, WN = BN / WGN;
     constexpr int MT = WM / 32, NT = WN / 32;
-    constexpr int ACOPY = BM * kRowBytes / 1024 / 4;  // copy instructions per wave and step
-    constexpr int BCOPY = BN * kRowBytes / 1024 / 4;
+    static_assert(MT >= 1 && NT >= 1, "wave tile of whole 32 x 32 MFMA tiles");
+    constexpr int ACOPY = BM * kRowBytes / 1024 / kWaves;  // copy instructions per wave and step
+    constexpr int BCOPY = BN * kRowBytes / 1024 / kWaves;
+    static_assert(ACOPY * kWaves * 1024 == BM * kRowBytes && BCOPY * kWaves * 1024 == BN * kRowBytes,
+                  "whole 1 KB copy blocks per wave");
     // NS stages of both operand buffers in one array: the epilogue reuses all
     // of it.
     static_assert(NS >= 2 && NS <= 4, "copy stages");
@@ -77,7 +86,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
     f16(*Bs)[BN * kBK] = reinterpret_cast<f16(*)[BN * kBK]>(smem + NS * BM * kBK);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WGN, wn = wave % WGN;
     const int g = lane >> 5, l32 = lane & 31;
 
     // Block coordinates (see the XCD note above).
@@ -106,27 +115,27 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
 
     const u32x4v ares = make_rsrc_words(A, M * K * 2);
     const u32x4v bres = make_rsrc_words(B, N * K * 2);
-    // This thread's copy sources: instruction j of wave w fills LDS bytes
-    // [(4j + w) KB, +1 KB): 16-byte unit p = 64 (4j + w) + lane, row p / 8,
-    // slot p % 8, holding chunk slot ^ ((row >> 1) & 7).
+    // This thread's copy sources: instruction j of wave w (of W) fills LDS
+    // bytes [(W j + w) KB, +1 KB): 16-byte unit p = 64 (W j + w) + lane,
+    // row p / 8, slot p % 8, holding chunk slot ^ ((row >> 1) & 7).
     int aoff[ACOPY], boff[BCOPY];
 #pragma unroll
     for (int j = 0; j < ACOPY; ++j) {
-        const int p = 64 * (4 * j + wave) + lane, row = p >> 3;
+        const int p = 64 * (kWaves * j + wave) + lane, row = p >> 3;
         const int src = min(m0 + row, M - 1);
         aoff[j] = src * K * 2 + slot_of(row, p & 7) * 16;
     }
 #pragma unroll
     for (int j = 0; j < BCOPY; ++j) {
-        const int p = 64 * (4 * j + wave) + lane, row = p >> 3;
+        const int p = 64 * (kWaves * j + wave) + lane, row = p >> 3;
         boff[j] = (n0 + row) * K * 2 + slot_of(row, p & 7) * 16;
     }
     auto copy_step = [&](int t, int buf) {
         const int kb = t * kRowBytes;
 #pragma unroll
-        for (int j = 0; j < ACOPY; ++j) dma16(ares, aoff[j] + kb, lds_addr(&As[buf][(4 * j + wave) * 512]));
+        for (int j = 0; j < ACOPY; ++j) dma16(ares, aoff[j] + kb, lds_addr(&As[buf][(kWaves * j + wave) * 512]));
 #pragma unroll
-        for (int j = 0; j < BCOPY; ++j) dma16(bres, boff[j] + kb, lds_addr(&Bs[buf][(4 * j + wave) * 512]));
+        for (int j = 0; j < BCOPY; ++j) dma16(bres, boff[j] + kb, lds_addr(&Bs[buf][(kWaves * j + wave) * 512]));
     };
 
     // Operand reads: A tile i (rows wm WM + 32 i + l32) and B tile i (rows
@@ -250,7 +259,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
     constexpr int EP = WN + 8;      // padded row, floats
     constexpr int CPR = WN / 4;     // 4-column pieces per row
     constexpr int RPP = 64 / CPR;   // rows per pass of the wave
-    static_assert(4 * 32 * EP * 4 <= NS * (BM + BN) * kBK * 2, "epilogue staging fits the operand buffers");
+    static_assert(kWaves * 32 * EP * 4 <= NS * (BM + BN) * kBK * 2, "epilogue staging fits the operand buffers");
     float* ep = reinterpret_cast<float*>(smem) + wave * (32 * EP);
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
@@ -258,36 +267,45 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f16_kernel(const f16* __rest
         for (int j = 0; j < NT; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) ep[(8 * (e >> 2) + 4 * g + (e & 3)) * EP + 32 * j + l32] = acc[i][j][e];
+        // Every residual piece of the row tile is requested before the first
+        // store (rows past M read row M - 1 and are not stored), so the
+        // tile waits for one memory round trip, not one per piece.
+        constexpr int kIt = 32 / RPP;
+        half4v old[kIt];
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+            const int rr = it * RPP + lane / CPR, cc = (lane % CPR) * 4;
+            const int m = min(m0 + wm * WM + 32 * i + rr, M - 1);
+            old[it] = *reinterpret_cast<const half4v*>(C + (int64_t)m * N + n0 + wn * WN + cc);
+        }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int it = 0; it < 32 / RPP; ++it) {
+        for (int it = 0; it < kIt; ++it) {
             const int rr = it * RPP + lane / CPR, cc = (lane % CPR) * 4;
             const float4 v = *(const float4*)&ep[rr * EP + cc];
             const int m = m0 + wm * WM + 32 * i + rr;
             if (m >= M) continue;
-            half4v* cp = reinterpret_cast<half4v*>(C + (int64_t)m * N + n0 + wn * WN + cc);
-            const half4v old = *cp;
             half4v o;
-            o[0] = (f16)((float)old[0] + v.x);
-            o[1] = (f16)((float)old[1] + v.y);
-            o[2] = (f16)((float)old[2] + v.z);
-            o[3] = (f16)((float)old[3] + v.w);
-            *cp = o;
+            o[0] = (f16)((float)old[it][0] + v.x);
+            o[1] = (f16)((float)old[it][1] + v.y);
+            o[2] = (f16)((float)old[it][2] + v.z);
+            o[3] = (f16)((float)old[it][3] + v.w);
+            *reinterpret_cast<half4v*>(C + (int64_t)m * N + n0 + wn * WN + cc) = o;
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): reads done before the next tile's writes
         __builtin_amdgcn_wave_barrier();
     }
 }
 
-template <int BM, int BN, int NS = 2>
+template <int BM, int BN, int NS = 2, int WGN = 2>
 hipError_t launch_shape(const f16* A, const f16* B, f16* C, int M, int N, int K, bool accumulate,
                         hipStream_t stream) {
     const dim3 grid((unsigned)(((M + BM - 1) / BM) * (N / BN)));
     if (accumulate)
-        hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, NS, true>), grid, dim3(kThreads), 0, stream, A, B, C, M, N, K);
+        hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, NS, true, WGN>), grid, dim3(128 * WGN), 0, stream, A, B, C, M, N, K);
     else
-        hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, NS, false>), grid, dim3(kThreads), 0, stream, A, B, C, M, N, K);
+        hipLaunchKernelGGL((gemm_f16_kernel<BM, BN, NS, false, WGN>), grid, dim3(128 * WGN), 0, stream, A, B, C, M, N, K);
     return hipGetLastError();
 }
 
@@ -301,41 +319,48 @@ bool gemm_f16_fits(int M, int N, int K) {
 hipError_t launch_gemm_f16(const f16* A, const f16* B, f16* C, int M, int N, int K, bool accumulate,
                            int cus, hipStream_t stream) {
     if (!gemm_f16_fits(M, N, K)) return hipErrorInvalidValue;
-    // Block tile: the one with the least predicted time, rounds of
-    // workgroups x tile area x a per-area cost of the shape.  Tiles up to
-    // 128 x 128 fit two workgroups per CU (LDS), so a round is 2 x cus of
-    // them at twice the time.  The costs per unit area (256 x 256 = 1) come
-    // from sweeps over the 1.7B projections at 420 and 4,269 rows and a
-    // 16384 x 12288 x 2048 product (the best tile per shape measured from
-    // 256 x 256 down to 64 x 64; this model picks it, or one within a few
-    // percent, at every shape).  Every tile accumulates each output over K in the same order,
-    // so the choice never changes a result's bits.
+    // Block tile: the one with the least predicted time.  A candidate fits
+    // `occ` workgroups per CU (LDS); its tiles run in rounds of occ x cus,
+    // with c = min(occ, ceil(tiles / cus)) of them sharing a CU, and a round
+    // takes c x tile area x cost[c - 1], the measured time per unit area of
+    // one of c workgroups sharing a CU (small tiles alone on a CU wait on
+    // their latencies; a second or third one on the CU hides them).  The
+    // costs (256 x 256 = 52) come from sweeps of every candidate over the
+    // 1.7B projections at 420 and 4,269 rows and a 16384 x 12288 x 2048
+    // product; at each the model picks the fastest tile or one within about
+    // 12% of it.  Every tile accumulates each output over K in the same
+    // order, so the choice never changes a result's bits.
     // QASR_GEMM_TILE = 1..5 forces candidate 1..5 (the tests compare them).
-    struct Cand { int bm, bn, occ; float cost; };
-    constexpr Cand cands[] = {{256, 256, 1, 1.0f}, {128, 128, 2, 1.05f}, {64, 128, 2, 1.3f},
-                              {128, 64, 2, 1.3f}, {64, 64, 2, 1.6f}};
+    struct Cand { int bm, bn, occ; float cost[3]; };
+    constexpr Cand cands[] = {{256, 256, 1, {52.0f, 0.0f, 0.0f}},      // 8 waves
+                              {128, 128, 2, {72.0f, 60.0f, 0.0f}},     // 8 waves
+                              {64, 128, 3, {125.0f, 105.0f, 85.0f}},   // 4 waves
+                              {128, 64, 3, {125.0f, 105.0f, 85.0f}},   // 4 waves
+                              {64, 64, 2, {170.0f, 112.0f, 0.0f}}};    // 4 waves, 4 stages
     constexpr int kCands = (int)(sizeof cands / sizeof cands[0]);
+    const int64_t ncu = std::max(1, cus);
     int best = 0;
     double best_t = 0.0;
-    const char* forced = std::getenv("QASR_GEMM_TILE");
-    const int f = forced ? std::atoi(forced) : 0;
-    for (int i = 0; i < kCands && !(f >= 1 && f <= kCands); ++i) {
+    for (int i = 0; i < kCands; ++i) {
         const Cand& c = cands[i];
         const int64_t tiles = (int64_t)((M + c.bm - 1) / c.bm) * (N / c.bn);
-        const int64_t slots = (int64_t)c.occ * std::max(1, cus);
-        const double t = (double)((tiles + slots - 1) / slots) * c.occ * c.bm * c.bn * c.cost;
+        const int64_t rounds = (tiles + c.occ * ncu - 1) / (c.occ * ncu);
+        const int conc = (int)std::min<int64_t>(c.occ, (tiles + ncu - 1) / ncu);
+        const double t = (double)rounds * conc * c.bm * c.bn * c.cost[conc - 1];
         if (i == 0 || t < best_t) {
             best = i;
             best_t = t;
         }
     }
+    const char* forced = std::getenv("QASR_GEMM_TILE");
+    const int f = forced ? std::atoi(forced) : 0;
     if (f >= 1 && f <= kCands) best = f - 1;
     switch (best) {
-        case 0: return launch_shape<256, 256>(A, B, C, M, N, K, accumulate, stream);
-        case 1: return launch_shape<128, 128>(A, B, C, M, N, K, accumulate, stream);
-        case 2: return launch_shape<64, 128>(A, B, C, M, N, K, accumulate, stream);
-        case 3: return launch_shape<128, 64>(A, B, C, M, N, K, accumulate, stream);
-        default: return launch_shape<64, 64, 4>(A, B, C, M, N, K, accumulate, stream);
+        case 0: return launch_shape<256, 256, 2, 4>(A, B, C, M, N, K, accumulate, stream);
+        case 1: return launch_shape<128, 128, 2, 4>(A, B, C, M, N, K, accumulate, stream);
+        case 2: return launch_shape<64, 128, 2, 2>(A, B, C, M, N, K, accumulate, stream);
+        case 3: return launch_shape<128, 64, 2, 2>(A, B, C, M, N, K, accumulate, stream);
+        default: return launch_shape<64, 64, 4, 2>(A, B, C, M, N, K, accumulate, stream);
     }
 }
 

@@ -94,8 +94,8 @@ def g_ctx():
     return _CTX
 
 
-# Block tiles the launcher chooses from (QASR_GEMM_TILE = 1..5): 256x256,
-# 128x128, 64x128, 128x64, 64x64.
+# Block tiles the launcher chooses from (QASR_GEMM_TILE = 1..5): 256x256 and
+# 128x128 (eight waves), 64x128, 128x64, 64x64 (four).
 TILES = [1, 2, 3, 4, 5]
 
 
