@@ -6,13 +6,13 @@
 // the reference's batched projections (cpu_decoder.rs:45-62 batch_dot_acc,
 // 398-449; dispatched on the GPU by decoder.rs:3580-4162).
 //
-// Block tile BM x BN (256 x 256 down to 64 x 64, chosen per shape by a cost
+// Block tile BM x BN (256 x 256, 192 x 256 down to 64 x 64, chosen per shape by a cost
 // model: launch_gemm_f16), K steps of 64, waves in a 2 x WGN grid (WGN = 2:
 // four waves, one per SIMD; WGN = 4: eight, two per SIMD, so one wave's
 // MFMAs run while the other waits), each wave (BM/2) x (BN/WGN) as tiles of
 // v_mfma_f32_32x32x16_f16.  Eight waves measured faster for 256 x 256
-// (16384 x 12288 x 2048: 764-820 against 820-861 us) and 128 x 128, four for
-// the smaller tiles.  Per K step the wave runs four 16-k slices; the next slice's operand reads
+// (16384 x 12288 x 2048: 764-820 against 820-861 us), 192 x 256 and
+// 128 x 128, four for the smaller tiles.  Per K step the wave runs four 16-k slices; the next slice's operand reads
 // are issued as one group ahead of the current slice's MFMAs, and the next
 // step's first reads ahead of the last slice's, so no LDS latency is waited
 // for between MFMAs.
@@ -325,14 +325,17 @@ hipError_t launch_gemm_f16(const f16* A, const f16* B, f16* C, int M, int N, int
     // takes c x tile area x cost[c - 1], the measured time per unit area of
     // one of c workgroups sharing a CU (small tiles alone on a CU wait on
     // their latencies; a second or third one on the CU hides them).  The
-    // costs (256 x 256 = 52) come from sweeps of every candidate over the
+    // costs (256 x 256 = 58) come from sweeps of every candidate over the
     // 1.7B projections at 420 and 4,269 rows and a 16384 x 12288 x 2048
     // product; at each the model picks the fastest tile or one within about
-    // 12% of it.  Every tile accumulates each output over K in the same
-    // order, so the choice never changes a result's bits.
-    // QASR_GEMM_TILE = 1..5 forces candidate 1..5 (the tests compare them).
+    // 12% of it.  (192 x 256 is for N = 2048 at a few thousand rows: 4,269
+    // rows make 184 such tiles, one round, against 136 of 256 x 256.)
+    // Every tile accumulates each output over K in the same order, so the
+    // choice never changes a result's bits.
+    // QASR_GEMM_TILE = 1..6 forces candidate 1..6 (the tests compare them).
     struct Cand { int bm, bn, occ; float cost[3]; };
-    constexpr Cand cands[] = {{256, 256, 1, {52.0f, 0.0f, 0.0f}},      // 8 waves
+    constexpr Cand cands[] = {{256, 256, 1, {58.0f, 0.0f, 0.0f}},      // 8 waves
+                              {192, 256, 1, {62.0f, 0.0f, 0.0f}},      // 8 waves
                               {128, 128, 2, {72.0f, 60.0f, 0.0f}},     // 8 waves
                               {64, 128, 3, {125.0f, 105.0f, 85.0f}},   // 4 waves
                               {128, 64, 3, {125.0f, 105.0f, 85.0f}},   // 4 waves
@@ -357,9 +360,10 @@ hipError_t launch_gemm_f16(const f16* A, const f16* B, f16* C, int M, int N, int
     if (f >= 1 && f <= kCands) best = f - 1;
     switch (best) {
         case 0: return launch_shape<256, 256, 2, 4>(A, B, C, M, N, K, accumulate, stream);
-        case 1: return launch_shape<128, 128, 2, 4>(A, B, C, M, N, K, accumulate, stream);
-        case 2: return launch_shape<64, 128, 2, 2>(A, B, C, M, N, K, accumulate, stream);
-        case 3: return launch_shape<128, 64, 2, 2>(A, B, C, M, N, K, accumulate, stream);
+        case 1: return launch_shape<192, 256, 2, 4>(A, B, C, M, N, K, accumulate, stream);
+        case 2: return launch_shape<128, 128, 2, 4>(A, B, C, M, N, K, accumulate, stream);
+        case 3: return launch_shape<64, 128, 2, 2>(A, B, C, M, N, K, accumulate, stream);
+        case 4: return launch_shape<128, 64, 2, 2>(A, B, C, M, N, K, accumulate, stream);
         default: return launch_shape<64, 64, 4, 2>(A, B, C, M, N, K, accumulate, stream);
     }
 }

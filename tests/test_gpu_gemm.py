@@ -94,9 +94,9 @@ def g_ctx():
     return _CTX
 
 
-# Block tiles the launcher chooses from (QASR_GEMM_TILE = 1..5): 256x256 and
-# 128x128 (eight waves), 64x128, 128x64, 64x64 (four).
-TILES = [1, 2, 3, 4, 5]
+# Block tiles the launcher chooses from (QASR_GEMM_TILE = 1..6): 256x256,
+# 192x256 and 128x128 (eight waves), 64x128, 128x64, 64x64 (four).
+TILES = [1, 2, 3, 4, 5, 6]
 
 
 @pytest.mark.parametrize("m,n,k,accumulate", [(300, 512, 256, False), (4269, 2048, 2048, True),
