@@ -230,41 +230,54 @@ __global__ __launch_bounds__(128 * WGN, 1) void gemm_f16_kernel(const f16* __res
         __builtin_amdgcn_sched_barrier(0);
     };
     if constexpr (PP) {
-        // Ping-pong (the 256 x 256 tile): waves 0-3 (group 0) and 4-7
+        // Ping-pong (the 256 x 256 and 192 x 256 tiles): waves 0-3 (group 0) and 4-7
         // (group 1), one of each per SIMD, alternate strictly between a read
-        // phase (the operands of half a K step, two slices, LDS ->
-        // registers, and every other time the copies of a later step) and
-        // an MFMA phase, group 1 one phase behind, every phase ending at a
-        // workgroup barrier: while one wave of a SIMD reads, the other feeds
-        // the matrix core (16384 x 12288 x 2048: 729 against 800 us; no
-        // gain on 192 x 256, a loss on 128 x 128, whose phases are short).
-        // Half step j (step j / 2, slices 2 (j % 2), 2 (j % 2) + 1) is read
-        // in global phase 2j by group 0 and 2j + 1 by group 1 and multiplied
-        // one phase later.  At its read of half 2s (s >= 1) a wave copies
-        // step s + 1 into buffer (s + 1) % 2, which both groups finished
-        // reading (step s - 1) in phases 4s - 2 and 4s - 1; the step is read
-        // from phase 4s + 4 on, and every wave waits for its own copies
-        // (vmcnt) before the barrier that ends phase 4s + 3.  The K order of
-        // every output is that of the other tiles, so the bits are too.
+        // phase (a K step's operands, LDS -> registers, and the copies of
+        // the next step) and an MFMA phase (the step's 32 MFMAs), group 1 one
+        // phase behind, every phase ending at a workgroup barrier: while one
+        // wave of a SIMD reads, the other feeds the matrix core
+        // (16384 x 12288 x 2048, same box: 256 x 256 714-722 against 787-795
+        // us with the loop below, 192 x 256 801-805 against 827-831; half-
+        // step phases, with twice the barriers, measured in between; a loss
+        // on 128 x 128, whose phases are four MFMAs).  Step t is read in global phase
+        // 2t by group 0 and 2t + 1 by group 1 and multiplied one phase later.
+        // At its read of step t (t >= 1) a wave copies its share of step
+        // t + 1 into buffer (t + 1) % 2, which both groups finished reading
+        // (step t - 1) in phases 2t - 2 and 2t - 1; step t + 1 is read from
+        // phase 2t + 2 on, and every wave waits for its own copies (vmcnt)
+        // before the barrier that ends phase 2t + 1.  Group 1 thus waits in
+        // the phase it copies in; moving its copies into its MFMA phase one
+        // step earlier, so that they have two phases, measured 11% slower
+        // (the copy instructions then hold up the MFMA issue).  The K order
+        // of every output is that of the other tiles, so the bits are too.
         static_assert(NS == 2 && kWaves == 8, "ping-pong: two stages, two waves per SIMD");
         const int grp = __builtin_amdgcn_readfirstlane(wave >> 2);
-        auto read_half = [&](int j) {
-            const int buf = (j >> 1) & 1;
-            read_slice(As[buf], Bs[buf], 2 * (j & 1), 0);
-            read_slice(As[buf], Bs[buf], 2 * (j & 1) + 1, 1);
-        };
-        const int nh = 2 * nk;
+        half8v pa[kSlices][MT], pb[kSlices][NT];
         if (grp == 1) __syncthreads();
-        for (int j = 0; j < nh; ++j) {
-            if ((j & 1) == 0 && j >= 2 && (j >> 1) + 1 < nk) copy_step((j >> 1) + 1, ((j >> 1) + 1) & 1);
-            read_half(j);
-            if (grp == 1 && (j & 1)) wait_vm_lgkm0<0>();
+        for (int t = 0; t < nk; ++t) {
+            if (t >= 1 && t + 1 < nk) copy_step(t + 1, (t + 1) & 1);
+            const f16* as = As[t & 1];
+            const f16* bs = Bs[t & 1];
+#pragma unroll
+            for (int ks = 0; ks < kSlices; ++ks) {
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+                    pa[ks][i] = *(const half8v*)&as[arow[i] * kBK + slot_of(arow[i], 2 * ks + g) * 8];
+#pragma unroll
+                for (int i = 0; i < NT; ++i)
+                    pb[ks][i] = *(const half8v*)&bs[brow[i] * kBK + slot_of(brow[i], 2 * ks + g) * 8];
+            }
+            if (grp == 1) wait_vm_lgkm0<0>();
             __syncthreads();  // (lgkmcnt(0): this phase's reads are in registers)
             __builtin_amdgcn_sched_barrier(0);
-            mfma_slice(0);
-            mfma_slice(1);
+#pragma unroll
+            for (int ks = 0; ks < kSlices; ++ks)
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int j = 0; j < NT; ++j) acc[i][j] = mfma32(pa[ks][i], pb[ks][j], acc[i][j]);
             __builtin_amdgcn_sched_barrier(0);
-            if (grp == 0 && (j & 1)) wait_vm_lgkm0<0>();
+            if (grp == 0) wait_vm_lgkm0<0>();
             __syncthreads();
         }
         if (grp == 0) __syncthreads();
@@ -366,7 +379,7 @@ hipError_t launch_gemm_f16(const f16* A, const f16* B, f16* C, int M, int N, int
     // takes c x tile area x cost[c - 1], the measured time per unit area of
     // one of c workgroups sharing a CU (small tiles alone on a CU wait on
     // their latencies; a second or third one on the CU hides them).  The
-    // costs (256 x 256 = 53) come from sweeps of every candidate over the
+    // costs (256 x 256 = 52) come from sweeps of every candidate over the
     // 1.7B projections at 420 and 4,269 rows and a 16384 x 12288 x 2048
     // product; at each the model picks the fastest tile or one within about
     // 12% of it.  (192 x 256 is for N = 2048 at a few thousand rows: 4,269
@@ -375,8 +388,8 @@ hipError_t launch_gemm_f16(const f16* A, const f16* B, f16* C, int M, int N, int
     // choice never changes a result's bits.
     // QASR_GEMM_TILE = 1..6 forces candidate 1..6 (the tests compare them).
     struct Cand { int bm, bn, occ; float cost[3]; };
-    constexpr Cand cands[] = {{256, 256, 1, {53.0f, 0.0f, 0.0f}},      // 8 waves, ping-pong
-                              {192, 256, 1, {62.0f, 0.0f, 0.0f}},      // 8 waves
+    constexpr Cand cands[] = {{256, 256, 1, {52.0f, 0.0f, 0.0f}},      // 8 waves, ping-pong
+                              {192, 256, 1, {57.0f, 0.0f, 0.0f}},      // 8 waves, ping-pong
                               {128, 128, 2, {72.0f, 60.0f, 0.0f}},     // 8 waves
                               {64, 128, 3, {125.0f, 105.0f, 85.0f}},   // 4 waves
                               {128, 64, 3, {125.0f, 105.0f, 85.0f}},   // 4 waves
@@ -401,7 +414,7 @@ hipError_t launch_gemm_f16(const f16* A, const f16* B, f16* C, int M, int N, int
     if (f >= 1 && f <= kCands) best = f - 1;
     switch (best) {
         case 0: return launch_shape<256, 256, 2, 4, true>(A, B, C, M, N, K, accumulate, stream);
-        case 1: return launch_shape<192, 256, 2, 4>(A, B, C, M, N, K, accumulate, stream);
+        case 1: return launch_shape<192, 256, 2, 4, true>(A, B, C, M, N, K, accumulate, stream);
         case 2: return launch_shape<128, 128, 2, 4>(A, B, C, M, N, K, accumulate, stream);
         case 3: return launch_shape<64, 128, 2, 2>(A, B, C, M, N, K, accumulate, stream);
         case 4: return launch_shape<128, 64, 2, 2>(A, B, C, M, N, K, accumulate, stream);
