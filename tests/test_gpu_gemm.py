@@ -100,12 +100,15 @@ TILES = [1, 2, 3, 4, 5, 6]
 
 
 @pytest.mark.parametrize("m,n,k,accumulate", [(300, 512, 256, False), (4269, 2048, 2048, True),
-                                              (65, 1024, 3072, True)])
+                                              (65, 1024, 3072, True), (520, 768, 64, True),
+                                              (257, 512, 128, False)])
 def test_gemm_tile_choice_keeps_bits(gpu, m, n, k, accumulate, monkeypatch):
     """Every block tile gives the same bits, so the per-shape tile choice
     (a function of the row count) cannot make a row's result depend on how
     many rows the call carries; the default choice is one of them, and the
-    shared result meets the fp32 reference's bound."""
+    shared result meets the fp32 reference's bound.  K = 64 and 128 run the
+    large tiles' ping-pong loop over one and two K steps (its copies and
+    waits at their boundaries)."""
     import torch
 
     import qasr_attn
