@@ -321,6 +321,54 @@ __device__ __forceinline__ float merge_partials(const float* mlw, const float* o
     return Ls;
 }
 
+// The same merge for nsp <= NP partials with every load -- (m, l) and the
+// NC chunks of all NP records -- requested before the first use: one memory
+// round trip instead of two plus one per chunk.  Unused slots read partial
+// 0's record and weigh 0, and the sums run in the same order, so the result
+// has the bits of merge_partials (whose unused slots add exact zeros).
+template <int NP, int C0, int NC>
+__device__ __forceinline__ float merge_partials_burst(const float* mlw, const float* ow, int nsp,
+                                                      float16v (&o)[4]) {
+    float mi[NP], li[NP], x[NC][NP][8];
+#pragma unroll
+    for (int u = 0; u < NP; ++u) {
+        const float* rec = mlw + (int64_t)(u < nsp ? u : 0) * kPrefillItemMl;
+        mi[u] = load_dev(rec);
+        li[u] = load_dev(rec + 64);
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int u = 0; u < NP; ++u) {
+            const float* src = ow + (int64_t)(u < nsp ? u : 0) * kPrefillItemFloats + (C0 + c) * 8 * 64;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[c][u][e] = load_dev(src + e * 64);
+        }
+    float M = kNegInf;
+#pragma unroll
+    for (int u = 0; u < NP; ++u) M = fmaxf(M, u < nsp ? mi[u] : kNegInf);
+    float w[NP];
+    float Ls = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NP; ++u) {
+        w[u] = (u >= nsp || mi[u] == kNegInf) ? 0.0f : fast_exp2(mi[u] - M);
+        Ls = fmaf(u < nsp ? li[u] : 0.0f, w[u], Ls);
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        float acc[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < NP; ++u)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(u < nsp ? x[c][u][e] : 0.0f, w[u], acc[e]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[(C0 + c) >> 1][8 * ((C0 + c) & 1) + e] = acc[e];
+    }
+    return Ls;
+}
+
 // Kernel state the epilogue needs.
 // rec: this item's partial record; rec0: the record of split 0 of its (row
 // block, kv head) (the splits' records follow it); ctr: their arrival counter.
@@ -420,8 +468,9 @@ __device__ __forceinline__ void epilogue4(Wave& w, const EpiArgs& e) {
     const float* mlw = e.ws_ml + e.rec0 * kPrefillItemMl + rw * kPrefillWaveMl + lane;
     const float* ow = e.ws_o + e.rec0 * kPrefillItemFloats + rw * kPrefillWaveFloats + lane;
     float16v om[4];
-    const float Ls = e.nsp <= 2 ? merge_partials<2, 2 * KG, 2>(mlw, ow, e.nsp, om)
-                                : merge_partials<8, 2 * KG, 2>(mlw, ow, e.nsp, om);
+    const float Ls = e.nsp <= 2   ? merge_partials_burst<2, 2 * KG, 2>(mlw, ow, e.nsp, om)
+                     : e.nsp <= 4 ? merge_partials_burst<4, 2 * KG, 2>(mlw, ow, e.nsp, om)
+                                  : merge_partials<8, 2 * KG, 2>(mlw, ow, e.nsp, om);
     write_out(om[KG], Ls);
     if (e.tid == 0) ticket_reset(e.ctr);
 }
@@ -508,8 +557,9 @@ __device__ __forceinline__ void epilogue(Wave& w, const EpiArgs& e) {
     // wave merges its half of its row wave's 32 rows.
     const float* mlw = e.ws_ml + e.rec0 * kPrefillItemMl + rw * kPrefillWaveMl + lane;
     const float* ow = e.ws_o + e.rec0 * kPrefillItemFloats + rw * kPrefillWaveFloats + lane;
-    const float Ls = e.nsp <= 2 ? merge_partials<2, 4 * KG, 4>(mlw, ow, e.nsp, o)
-                                : merge_partials<8, 4 * KG, 4>(mlw, ow, e.nsp, o);
+    const float Ls = e.nsp <= 2   ? merge_partials_burst<2, 4 * KG, 4>(mlw, ow, e.nsp, o)
+                     : e.nsp <= 4 ? merge_partials_burst<4, 4 * KG, 4>(mlw, ow, e.nsp, o)
+                                  : merge_partials<8, 4 * KG, 4>(mlw, ow, e.nsp, o);
     write_out(Ls);
     if (e.tid == 0) ticket_reset(e.ctr);
 }
