@@ -6,16 +6,17 @@
 // the reference's batched projections (cpu_decoder.rs:45-62 batch_dot_acc,
 // 398-449; dispatched on the GPU by decoder.rs:3580-4162).
 //
-// Block tile BM x BN (256 x 256, 192 x 256 down to 64 x 64, chosen per shape by a cost
-// model: launch_gemm_f16), K steps of 64, waves in a 2 x WGN grid (WGN = 2:
+// Block tile BM x BN (256 x 256, 192 x 256 down to 64 x 64, chosen per
+// shape by a cost model: launch_gemm_f16), K steps of 64, waves in a 2 x WGN grid (WGN = 2:
 // four waves, one per SIMD; WGN = 4: eight, two per SIMD, so one wave's
 // MFMAs run while the other waits), each wave (BM/2) x (BN/WGN) as tiles of
 // v_mfma_f32_32x32x16_f16.  Eight waves measured faster for 256 x 256
 // (16384 x 12288 x 2048: 764-820 against 820-861 us), 192 x 256 and
-// 128 x 128, four for the smaller tiles.  Per K step the wave runs four 16-k slices; the next slice's operand reads
-// are issued as one group ahead of the current slice's MFMAs, and the next
-// step's first reads ahead of the last slice's, so no LDS latency is waited
-// for between MFMAs.
+// 128 x 128, four for the smaller tiles.  The two largest tiles run a
+// ping-pong schedule of their two wave groups (below); the others run four
+// 16-k slices per K step with the next slice's operand reads issued as one
+// group ahead of the current slice's MFMAs, and the next step's first reads
+// ahead of the last slice's, so no LDS latency is waited for between MFMAs.
 // Both operand tiles go global -> LDS by direct copies (buffer_load ... lds,
 // one 1 KB block per wave instruction) into NS buffers: the copies of K
 // step t+NS are issued as soon as every wave is done with step t's buffers,
@@ -23,8 +24,8 @@
 // the larger tiles (their LDS then still fits two workgroups per CU up to
 // 128 x 128); four for 64 x 64, whose steps are short and latency-bound
 // (420 x 2048 x 6144: 47.8 -> 30 us; three or four stages on the larger
-// tiles cost the second workgroup per CU and measured slower).  LDS row layout (both
-// operands): row r is 128 bytes (64 k), its 16-byte chunk c at slot
+// tiles cost the second workgroup per CU and measured slower).  LDS row
+// layout (both operands): row r is 128 bytes (64 k), its 16-byte chunk c at slot
 // c ^ ((r >> 1) & 7), so an operand read (16 consecutive rows, one chunk)
 // covers 16 distinct 16-byte bank groups.  Rows past M are copied from row
 // M - 1 (finite values; their outputs are not stored).
@@ -230,26 +231,28 @@ __global__ __launch_bounds__(128 * WGN, 1) void gemm_f16_kernel(const f16* __res
         __builtin_amdgcn_sched_barrier(0);
     };
     if constexpr (PP) {
-        // Ping-pong (the 256 x 256 and 192 x 256 tiles): waves 0-3 (group 0) and 4-7
-        // (group 1), one of each per SIMD, alternate strictly between a read
-        // phase (a K step's operands, LDS -> registers, and the copies of
-        // the next step) and an MFMA phase (the step's 32 MFMAs), group 1 one
-        // phase behind, every phase ending at a workgroup barrier: while one
-        // wave of a SIMD reads, the other feeds the matrix core
-        // (16384 x 12288 x 2048, same box: 256 x 256 714-722 against 787-795
-        // us with the loop below, 192 x 256 801-805 against 827-831; half-
-        // step phases, with twice the barriers, measured in between; a loss
-        // on 128 x 128, whose phases are four MFMAs).  Step t is read in global phase
-        // 2t by group 0 and 2t + 1 by group 1 and multiplied one phase later.
-        // At its read of step t (t >= 1) a wave copies its share of step
-        // t + 1 into buffer (t + 1) % 2, which both groups finished reading
-        // (step t - 1) in phases 2t - 2 and 2t - 1; step t + 1 is read from
-        // phase 2t + 2 on, and every wave waits for its own copies (vmcnt)
-        // before the barrier that ends phase 2t + 1.  Group 1 thus waits in
-        // the phase it copies in; moving its copies into its MFMA phase one
-        // step earlier, so that they have two phases, measured 11% slower
-        // (the copy instructions then hold up the MFMA issue).  The K order
-        // of every output is that of the other tiles, so the bits are too.
+        // Ping-pong (the 256 x 256 and 192 x 256 tiles): waves 0-3 (group 0)
+        // and 4-7 (group 1), one of each per SIMD, alternate strictly between
+        // a read phase (a K step's operands, LDS -> registers, and the copies
+        // of the next step) and an MFMA phase (the step's 32 or 24 MFMAs),
+        // group 1 one phase behind, every phase ending at a workgroup
+        // barrier: while one wave of a SIMD reads, the other feeds the matrix
+        // core.  16384 x 12288 x 2048, same box: 256 x 256 714-722 us
+        // against 787-795 with group 1's copies moved as described below,
+        // and ~800 with the pipelined loop; 192 x 256 801-805 against
+        // 827-831.  Half-step phases (twice the barriers) measured in
+        // between; 128 x 128 with them (four MFMAs a phase) was slower than
+        // its pipelined loop.  Step t is read in global phase 2t by group 0
+        // and 2t + 1 by group 1 and multiplied one phase later.  At its read
+        // of step t (t >= 1) a wave copies its share of step t + 1 into
+        // buffer (t + 1) % 2, which both groups finished reading (step t - 1)
+        // in phases 2t - 2 and 2t - 1; step t + 1 is read from phase 2t + 2
+        // on, and every wave waits for its own copies (vmcnt) before the
+        // barrier that ends phase 2t + 1.  Group 1 thus waits in the phase it
+        // copies in; moving its copies into its MFMA phase one step earlier,
+        // so that they have two phases, measured 11% slower (the copy
+        // instructions then hold up the MFMA issue).  The K order of every
+        // output is that of the other tiles, so the bits are too.
         static_assert(NS == 2 && kWaves == 8, "ping-pong: two stages, two waves per SIMD");
         const int grp = __builtin_amdgcn_readfirstlane(wave >> 2);
         half8v pa[kSlices][MT], pb[kSlices][NT];
