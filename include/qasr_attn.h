@@ -298,7 +298,9 @@ int qasr_dequant_i8(qasr_ctx* ctx, const void* q_dev, const float* scale_dev, in
  * cpu_decoder.rs:45-62).  a [m][k] (activation rows), b [n][k] (weight rows,
  * checkpoint layout) and c [m][n] are f16 device pointers on ctx's device,
  * 16-byte aligned; k a multiple of 64, n a multiple of 256, a and b each
- * under 2 GB. */
+ * under 2 GB.  Every output sums over k in one fixed order whatever m is,
+ * so a row's result does not depend on the other rows of the call (the
+ * block tile, chosen per shape, never changes a bit). */
 int qasr_gemm_f16(qasr_ctx* ctx, const void* a_dev, const void* b_dev, void* c_dev, int32_t m,
                   int32_t n, int32_t k, int accumulate, void* stream);
 
