@@ -127,6 +127,7 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     __shared__ __attribute__((aligned(16))) f16 s_raw[4][kHeadDim];  // q0, q1, k, v raw heads
     __shared__ __attribute__((aligned(16))) f16 s_tab[4][kHeadDim];  // q gain, k gain, cos, sin
     __shared__ float s_inv[3];
+    __shared__ __attribute__((aligned(16))) float s_sq[3][kHeadDim];  // f32 squares of q0, q1, k
     __shared__ float s_p[W][64];
     // Wave partials of the run's granules: (max, sum) per head and the
     // unnormalised output of both heads.
@@ -224,7 +225,20 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
 
     H8 q0, q1;
     if constexpr (FUSED) {
-        if (tid < 3 && (tid < 2 || owner)) s_inv[tid] = head_inv_rms_vec(s_raw[tid], P.eps);
+        // The squares (exact in f32) come from every thread at once; the
+        // serial path is then the reference's 128 dependent adds alone.
+        static_assert(W * 64 == 2 * kHeadDim, "one thread per q element");
+        {
+#pragma clang fp contract(off)
+            const float x = h2f(s_raw[tid >> 7][tid & 127]);
+            s_sq[tid >> 7][tid & 127] = x * x;
+            if (owner && tid < kHeadDim) {
+                const float xk = h2f(s_raw[2][tid]);
+                s_sq[2][tid] = xk * xk;
+            }
+        }
+        __syncthreads();
+        if (tid < 3 && (tid < 2 || owner)) s_inv[tid] = head_inv_rms_squares_all(s_sq[tid], P.eps);
         __syncthreads();
         if (tid < 256) {
             const int h = tid >> 7, j = tid & 127;
