@@ -136,8 +136,9 @@ def test_decode_plans_and_unfused_equal_fused(O, gpu, gran, wgs, gmax, monkeypat
 
 def test_decode_output_independent_of_batch_mates(O, gpu, monkeypatch):
     """--batch N == --batch 1 for attention: each entry decoded alone, inside
-    two different batches (other slots, other order) and under other
-    workgroup budgets gives the same bits, on the unfused and the fused path.
+    two different batches (other slots, other order), under other workgroup
+    budgets and with the split off gives the same bits, on the unfused and
+    the fused path.
     The granule plan depends on an entry's own length only; the batch and the
     device change only which workgroup runs which granules."""
     import qasr_attn
@@ -187,6 +188,11 @@ def test_decode_output_independent_of_batch_mates(O, gpu, monkeypatch):
         got = attn(slots, wgs)
         for k, s in enumerate(slots):
             assert np.array_equal(got[k:k + 1], alone[s]), (slots, wgs, s)
+    monkeypatch.setenv("QASR_DECODE_SPLIT", "0")  # every (entry, kv head) on one workgroup
+    got = attn(batch_b)
+    monkeypatch.delenv("QASR_DECODE_SPLIT")
+    for k, s in enumerate(batch_b):
+        assert np.array_equal(got[k:k + 1], alone[s]), ("unsplit", s)
     step_alone = {s: step([s]) for s in (3, 7, 11)}
     for slots in (batch_a, batch_b):
         got = step(slots, 100)

@@ -61,7 +61,7 @@ def check_decode_plan(lens, plan, nkvh=NKVH, gmin=0, gmax=32):
 @pytest.fixture(autouse=True)
 def _no_knobs(monkeypatch):
     for v in ("QASR_DECODE_WGS", "QASR_DECODE_GRANULE", "QASR_DECODE_MAX_GRANULES",
-              "QASR_PREFILL_TPS"):
+              "QASR_DECODE_SPLIT", "QASR_PREFILL_TPS"):
         monkeypatch.delenv(v, raising=False)
 
 
@@ -136,6 +136,23 @@ def test_decode_plan_knobs(monkeypatch):
     monkeypatch.setenv("QASR_DECODE_WGS", "4096")
     plan = qasr_attn.plan_decode(lens, NKVH, 256)
     assert plan[1] == [1, 1, 1]
+
+
+def test_decode_plan_unsplit(monkeypatch):
+    """QASR_DECODE_SPLIT=0: every (entry, kv head) on one workgroup (runs of
+    up to 8 granules, the LDS limit), same granules as the split plan."""
+    monkeypatch.setenv("QASR_DECODE_SPLIT", "0")
+    rng = np.random.default_rng(13)
+    for _ in range(50):
+        n = int(rng.integers(1, 65))
+        lens = [int(x) for x in rng.integers(1, 16385, size=n)]
+        gran, run, base = plan = qasr_attn.plan_decode(lens, NKVH, 256)
+        check_decode_plan(lens, plan)
+        for b, L in enumerate(lens):
+            assert run[b] == min(-(-L // gran[b]), 8)
+        monkeypatch.delenv("QASR_DECODE_SPLIT")
+        assert qasr_attn.plan_decode(lens, NKVH, 256)[0] == gran  # granules unchanged
+        monkeypatch.setenv("QASR_DECODE_SPLIT", "0")
 
 
 def test_decode_plan_refusals():
