@@ -256,6 +256,11 @@ __global__ __launch_bounds__(128 * WGN, 1) void gemm_f16_kernel(const f16* __res
         static_assert(NS == 2 && kWaves == 8, "ping-pong: two stages, two waves per SIMD");
         const int grp = __builtin_amdgcn_readfirstlane(wave >> 2);
         half8v pa[kSlices][MT], pb[kSlices][NT];
+        // The one-phase offset is a barrier that only group 1 executes at the
+        // start and only group 0 at the end.  The condition is uniform per
+        // wave (readfirstlane), and every wave executes 2 nk + 1 barriers in
+        // all, so each hardware barrier still gathers all eight waves: the
+        // k-th barrier of a group-0 wave meets the k-th of a group-1 wave.
         if (grp == 1) __syncthreads();
         for (int t = 0; t < nk; ++t) {
             if (t >= 1 && t + 1 < nk) copy_step(t + 1, (t + 1) & 1);
