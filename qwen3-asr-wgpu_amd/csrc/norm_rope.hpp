@@ -15,37 +15,10 @@
 
 namespace qasr {
 
-// The one serial chain of the stage: 128 dependent adds in ascending j.  Each
-// f16 square is exact in f32, so only the adds round -- in the reference's order.
-__device__ __forceinline__ float head_inv_rms_serial(const f16* raw, float eps) {
-#pragma clang fp contract(off)
-    float sum2 = 0.0f;
-#pragma unroll 16
-    for (int j = 0; j < kHeadDim; ++j) {
-        float f = h2f(raw[j]);
-        sum2 += f * f;
-    }
-    return 1.0f / sqrtf(sum2 / (float)kHeadDim + eps);
-}
-
-// The same chain over squares already in LDS (sq[j] = x_j*x_j in f32, exact):
-// only the 128 dependent adds remain on the serial path, read 4 at a time.
-__device__ __forceinline__ float head_inv_rms_squares(const float* sq, float eps) {
-#pragma clang fp contract(off)
-    float sum2 = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kHeadDim / 4; ++i) {
-        const float4 v = *(const float4*)(sq + 4 * i);
-        sum2 += v.x;
-        sum2 += v.y;
-        sum2 += v.z;
-        sum2 += v.w;
-    }
-    return 1.0f / sqrtf(sum2 / (float)kHeadDim + eps);
-}
-
-// The same chain with all 32 four-square reads issued before the adds (one
-// LDS latency instead of one per pair of reads); same adds, same order.
+// The one serial chain of the stage, over squares already in LDS (sq[j] =
+// x_j*x_j in f32, exact for an f16 x_j): only the 128 dependent adds in
+// ascending j round, in the reference's order.  All 32 four-square reads are
+// issued before the adds (one LDS latency, not one per read).
 __device__ __forceinline__ float head_inv_rms_squares_all(const float* sq, float eps) {
 #pragma clang fp contract(off)
     float4 v[kHeadDim / 4];
@@ -59,26 +32,6 @@ __device__ __forceinline__ float head_inv_rms_squares_all(const float* sq, float
         sum2 += v[i].z;
         sum2 += v[i].w;
     }
-    return 1.0f / sqrtf(sum2 / (float)kHeadDim + eps);
-}
-
-// The same chain read 16 bytes at a time (all 16 reads issued before the
-// adds): the squares are independent of each other, so only the 128
-// dependent adds in ascending j stay on the serial path -- same adds, same
-// order, same bits as head_inv_rms_serial.  `raw` is 16-byte aligned.
-__device__ __forceinline__ float head_inv_rms_vec(const f16* raw, float eps) {
-#pragma clang fp contract(off)
-    H8 v[kHeadDim / 8];
-#pragma unroll
-    for (int c = 0; c < kHeadDim / 8; ++c) v[c].u = *(const uint4*)(raw + 8 * c);
-    float sum2 = 0.0f;
-#pragma unroll
-    for (int c = 0; c < kHeadDim / 8; ++c)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float f = h2f(v[c].e[e]);
-            sum2 += f * f;
-        }
     return 1.0f / sqrtf(sum2 / (float)kHeadDim + eps);
 }
 
