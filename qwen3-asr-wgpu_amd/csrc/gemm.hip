@@ -86,7 +86,9 @@ __global__ __launch_bounds__(128 * WGN, 1) void gemm_f16_kernel(const f16* __res
     f16(*As)[BM * kBK] = reinterpret_cast<f16(*)[BM * kBK]>(smem);
     f16(*Bs)[BN * kBK] = reinterpret_cast<f16(*)[BN * kBK]>(smem + NS * BM * kBK);
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // The wave index in a scalar register: the copies' LDS addresses (M0)
+    // are then scalar arithmetic, not a vector add and a readfirstlane each.
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
     const int g = lane >> 5, l32 = lane & 31;
 
