@@ -587,6 +587,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     constexpr int GK = kTileKeys / NKG;       // keys per key group and tile: 64 or 32
     constexpr int NB = GK / 32;               // 32-key MFMA blocks per step
     const int wave = tid >> 6;       // 0..7: copy slot
+    // The same index in a scalar register, for the copies' LDS addresses
+    // (M0 then comes from scalar arithmetic instead of a readfirstlane of a
+    // vector address per copy).
+    const int cwave = __builtin_amdgcn_readfirstlane(wave);
     const int rw = wave % kRowWaves; // row wave
     const int kg = wave / kRowWaves; // key group
     const int n = lane & 31;  // query column within the wave's 32 rows
@@ -642,10 +646,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     // tile t_begin (8 per thread), the Q block (4), tile t_begin + 1 (8).
     const u32x4v qres = make_rsrc_words(a.q + kvh * kRep * kHeadDim,
                                         (a.s - 1) * ldq * 2 + kRep * kHeadDim * 2);
-    dma_tile(kres, vres, t_begin * kTileKeys, kend, krow, kchunk, vrow, vchunk, K0, V0, wave);
-    dma_q<RB>(qres, row0, a.s - 1, ldq * 2, Qs, wave, lane);
+    dma_tile(kres, vres, t_begin * kTileKeys, kend, krow, kchunk, vrow, vchunk, K0, V0, cwave);
+    dma_q<RB>(qres, row0, a.s - 1, ldq * 2, Qs, cwave, lane);
     const bool two = t_begin + 1 < t_end;
-    if (two) dma_tile(kres, vres, (t_begin + 1) * kTileKeys, kend, krow, kchunk, vrow, vchunk, K1, V1, wave);
+    if (two) dma_tile(kres, vres, (t_begin + 1) * kTileKeys, kend, krow, kchunk, vrow, vchunk, K1, V1, cwave);
 
     Wave w;
     w.g = g;
@@ -688,7 +692,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
         }
         tile_sync();
         if (t + 2 < t_end)
-            dma_tile(kres, vres, (t + 2) * kTileKeys, kend, krow, kchunk, vrow, vchunk, kt, vt, wave);
+            dma_tile(kres, vres, (t + 2) * kTileKeys, kend, krow, kchunk, vrow, vchunk, kt, vt, cwave);
     };
     // Tile t_begin and Q have landed (tile t_begin + 1 may be in flight).
     if (two)
