@@ -310,7 +310,12 @@ constexpr int64_t kScratchCounters = (int64_t)kScratchMaxKvHeads * qasr::kMaxLau
 static __device__ __align__(256) float scratch[kScratchO + kScratchMl + kScratchCounters];
 
 constexpr int kMaxDevices = 64;
-constexpr int kPrefillNoSplitTiles = 4;  // key ranges of up to 512 keys run unsplit
+// Key ranges of up to 1024 keys run unsplit, in 32-row blocks.  Measured
+// per layer, against 64-row blocks with key splits: 640 rows from 0 12.5
+// against 16.1 us, 1024 from 0 16.6 against 18.6, 256 at 512 13.0 against
+// 15.9, 64 at 960 15.6 against 15.5; past 1024 keys the splits win (2048
+// rows from 0: 37.3 against 39.3 us unsplit in 32-row blocks).
+constexpr int kPrefillNoSplitTiles = 8;
 std::mutex g_scratch_mu;
 float* g_scratch_dev[kMaxDevices] = {};
 

@@ -191,8 +191,13 @@ def test_prefill_plan_bench_configs(monkeypatch):
     assert p["sp_base"][-1] * NKVH == 256
     p = qasr_attn.plan_prefill(512, 0, NKVH)  # 4 tiles: never split
     assert p["rows_per_block"] == 32 and p["sp_base"][-1] == 16
-    p = qasr_attn.plan_prefill(513, 0, NKVH)  # 5 tiles: 64-row blocks, split
-    assert p["rows_per_block"] == 64
+    p = qasr_attn.plan_prefill(1024, 0, NKVH)  # 8 tiles: never split
+    assert p["rows_per_block"] == 32 and p["sp_base"][-1] == 32
+    p = qasr_attn.plan_prefill(300, 724, NKVH)  # 8 tiles at kv_start 724: never split
+    assert p["rows_per_block"] == 32 and p["sp_base"][-1] == 10
+    p = qasr_attn.plan_prefill(1025, 0, NKVH)  # 9 tiles: 64-row blocks, split
+    assert p["rows_per_block"] == 64 and p["sp_base"][-1] > p["nrb"]
+    check_prefill_plan(1025, 0, p)
     monkeypatch.setenv("QASR_PREFILL_TPS", "3")
     p = qasr_attn.plan_prefill(420, 0, NKVH)
     assert (p["rows_per_block"], p["tiles_per_split"]) == (64, 3)
