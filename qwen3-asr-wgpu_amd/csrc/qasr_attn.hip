@@ -352,26 +352,46 @@ int noalloc_max_rows(int nkvh) {
 }
 
 // The plan of one piece of `rows` (<= kMaxRowBlocks * kPrefillRows) rows at
-// kv_start `ks`, a function of (rows, ks, nkvh) alone.  Tiles per split:
-// about 256 work items, without splitting row blocks whose key range is
-// short.  A split's merge (publish, ticket, read back) is about three memory
-// round trips, as long as several latency-bound tiles: key ranges of up to
-// kPrefillNoSplitTiles tiles are never split.  Unsplit short ranges also take
-// 32-row blocks: twice the workgroups, half the work on the longest one.  A
-// forced split count (tps_forced > 0, QASR_PREFILL_TPS) keeps 64-row blocks.
+// kv_start `ks`, a function of (rows, ks, nkvh) alone.  Tiles per split: the
+// fewest that keep the work items within one workgroup per CU for 256 CUs
+// (every row block rounds its split count up, so that is checked row block
+// by row block); when even unsplit row blocks are more, none is split.  A
+// few items past 256 wait for a whole second round: 1500 rows at 2000, 304
+// items at 21 tiles per split, 81.5 us per layer, against 57.6 us for 256
+// items at 24.  A split's merge (publish, ticket, read back) is about three
+// memory round trips, as long as several latency-bound tiles: key ranges of
+// up to kPrefillNoSplitTiles tiles are never split.  Unsplit short ranges
+// also take 32-row blocks: twice the workgroups, half the work on the
+// longest one.  A forced split count (tps_forced > 0, QASR_PREFILL_TPS)
+// keeps 64-row blocks.
 qasr::PrefillPlan choose_prefill_plan(int rows, int ks, int nkvh, int tps_forced) {
     const int nrb = (rows + qasr::kPrefillRows - 1) / qasr::kPrefillRows;
     const int max_tiles = (ks + rows + qasr::kPrefillTileKeys - 1) / qasr::kPrefillTileKeys;
     int tps = tps_forced;
     int rb_rows = qasr::kPrefillRows;
     if (tps <= 0) {
-        const int64_t tiles_all = (int64_t)nrb * max_tiles;
-        const int64_t want = std::max<int64_t>(1, 256 / nkvh);
+        const int64_t want = std::max<int64_t>(1, 256 / nkvh);  // items per kv head
         if (max_tiles <= kPrefillNoSplitTiles) {
             tps = max_tiles;
             rb_rows = qasr::kPrefillRows / 2;
         } else {
-            tps = (int)std::max<int64_t>(2, (tiles_all + want - 1) / want);
+            // Items at t tiles per split: sum over row blocks of ceil(tiles / t),
+            // at least sum(tiles) / t, so t starts at sum(tiles) / want.
+            auto row_tiles = [&](int rb) {
+                const int kend = ks + std::min((rb + 1) * qasr::kPrefillRows, rows);
+                return (kend + qasr::kPrefillTileKeys - 1) / qasr::kPrefillTileKeys;
+            };
+            int64_t sum = 0;
+            for (int rb = 0; rb < nrb; ++rb) sum += row_tiles(rb);
+            tps = max_tiles;
+            for (int t = (int)std::max<int64_t>(2, (sum + want - 1) / want); t < max_tiles; ++t) {
+                int64_t n = 0;
+                for (int rb = 0; rb < nrb; ++rb) n += (row_tiles(rb) + t - 1) / t;
+                if (n <= want) {
+                    tps = t;
+                    break;
+                }
+            }
         }
     }
     return qasr::plan_prefill(rows, ks, nkvh, tps, rb_rows);

@@ -182,6 +182,31 @@ def test_prefill_plan_covers_every_tile_random_launches():
         check_prefill_plan(rows, kv_start, qasr_attn.plan_prefill(rows, kv_start, NKVH))
 
 
+def test_prefill_plan_fewest_tiles_per_split_within_256_items():
+    """A split plan has at most 256 items over the kv heads, and one tile per
+    split fewer would exceed that (the rounding of every row block counted);
+    a plan past 256 items splits nothing."""
+    rng = np.random.default_rng(7)
+    for _ in range(400):
+        rows = int(rng.integers(1, 4097))
+        kv_start = int(rng.integers(0, 12289))
+        p = qasr_attn.plan_prefill(rows, kv_start, NKVH)
+        check_prefill_plan(rows, kv_start, p)
+        if p["rows_per_block"] == 32:
+            continue
+        nrb, tps, items = p["nrb"], p["tiles_per_split"], p["sp_base"][-1]
+        tiles = [-(-(kv_start + min((rb + 1) * 64, rows)) // 128) for rb in range(nrb)]
+        if items > nrb:  # some row block split
+            assert items * NKVH <= 256, (rows, kv_start, tps, items)
+            if tps > 2:
+                fewer = sum(-(-t // (tps - 1)) for t in tiles)
+                assert fewer * NKVH > 256, (rows, kv_start, tps)
+        else:
+            assert tps >= max(tiles)
+    p = qasr_attn.plan_prefill(1500, 2000, NKVH)  # 21 tiles per split would make 304 items
+    assert (p["tiles_per_split"], p["sp_base"][-1] * NKVH) == (24, 256)
+
+
 def test_prefill_plan_bench_configs(monkeypatch):
     p = qasr_attn.plan_prefill(420, 0, NKVH)  # config 2
     assert (p["rows_per_block"], p["nrb"], p["tiles_per_split"]) == (32, 14, 4)
