@@ -342,10 +342,12 @@ __global__ void zero_u32_kernel(uint32_t* p, int n) {
 }
 
 // Longest prefill one qasr_prefill_attn_noalloc call takes.  A default plan
-// of r rows has at most 256 + nkvh * ceil(r / 64) work items (tiles per split
-// are chosen for about 256 items; each row block adds at most one by
-// rounding), so up to this many rows every default plan fits the scratch
-// array, and the no-allocation call runs exactly qasr_prefill_attn's items.
+// of r rows has at most 256 + nkvh * ceil(r / 64) work items: a split plan
+// at most 256, an unsplit 64-row one nkvh * ceil(r / 64), an unsplit 32-row
+// one (key ranges of at most 1024 keys, so r <= 1024) nkvh * ceil(r / 32) <=
+// 2 nkvh * ceil(r / 64) <= 256 + nkvh * ceil(r / 64) for nkvh <= 16.  Up to
+// this many rows every default plan fits the scratch array, and the
+// no-allocation call runs exactly qasr_prefill_attn's items.
 int noalloc_max_rows(int nkvh) {
     const int64_t rbs = std::min<int64_t>(qasr::kMaxRowBlocks, (kScratchItems - 256) / nkvh);
     return qasr::kPrefillRows * (int)rbs;
