@@ -154,17 +154,25 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
 
     // Entry of this workgroup = number of later entry starts at or before it:
     // lane i tests wg_base[i + 1], one load per lane and a ballot, no search.
-    static_assert(kMaxBatch <= 64, "one lane per entry");
-    const int b = __popcll(__ballot(lane + 1 < P.batch && P.wg_base[lane + 1] <= wg));
-    const int L = P.len[b];
-    const int G = P.gran[b];
-    const int run = P.run[b];
+    // Lane i reads every plan field of entry i in that same round trip (the
+    // argument arrays hold kMaxBatch = 64 entries, so every read is in
+    // bounds, and unconditional, so no branch holds back the other argument
+    // loads); entry b's fields are then lane reads, not a second dependent
+    // load before the first K/V request.
+    static_assert(kMaxBatch == 64, "one lane per entry");
+    const int e_len = P.len[lane], e_gran = P.gran[lane], e_run = P.run[lane];
+    const int e_slot = P.slot[lane], e_wg0 = P.wg_base[lane], e_wg1 = P.wg_base[lane + 1];
+    const int e_part = P.part_base[lane];
+    const int b = __popcll(__ballot(lane + 1 < P.batch && e_wg1 <= wg));
+    const int L = __builtin_amdgcn_readlane(e_len, b);
+    const int G = __builtin_amdgcn_readlane(e_gran, b);
+    const int run = __builtin_amdgcn_readlane(e_run, b);
     const int ngr = (L + G - 1) / G;        // granules of the entry (per kv head)
     const int nw = (ngr + run - 1) / run;   // workgroups per kv head
     // kv head minor: workgroup i runs on XCD i mod 8, so with 8 kv heads every
     // XCD gets one run of each size.  Runs end at the entry's end: the last
     // holds the (possibly short) last granule, the first any remainder.
-    const int rel = wg - P.wg_base[b];
+    const int rel = wg - __builtin_amdgcn_readlane(e_wg0, b);
     const int kvh = rel % g.nkvh;
     const int r = rel / g.nkvh;
     const int g1 = ngr - (nw - 1 - r) * run;
@@ -176,7 +184,8 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     const int npass = (nkeys + 2 * kWgKeys - 1) / (2 * kWgKeys) * 2;  // even
     const int nqh = P.nqh;
     const int h0 = kvh * kRep;
-    f16* Kc = g.base + P.slot[b] * g.slot_stride + layer * g.layer_stride + kvh * g.head_stride;
+    f16* Kc = g.base + __builtin_amdgcn_readlane(e_slot, b) * g.slot_stride + layer * g.layer_stride +
+              kvh * g.head_stride;
     f16* Vc = Kc + g.kv_stride;
     // Resources start at the run's first key and end at its last.
     const int rbytes = nkeys * (kHeadDim * 2);
@@ -194,6 +203,14 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     // count while the newer one stays in flight.
     const int pos = L - 1;
     const bool owner = FUSED && (r == nw - 1);
+    // The query-input pointers are kernel arguments too: held in scalar
+    // registers here, their loads join the plan's round trip above instead
+    // of a round trip of their own inside the copy branches below (which the
+    // K/V requests follow).
+    if constexpr (FUSED)
+        asm volatile("" ::"s"(qin), "s"(q_gain), "s"(k_gain), "s"(cos_tab), "s"(sin_tab));
+    else
+        asm volatile("" ::"s"(qin));
     if constexpr (FUSED) {
         const int64_t tot = (int64_t)(nqh + 2 * g.nkvh) * kHeadDim;
         const f16* qkv_row = qin + b * tot;
@@ -345,7 +362,7 @@ __attribute__((amdgpu_waves_per_eu(kDecodeWavesPerEU, 8))) void decode_attn_kern
     // head): part0 + granule.
     const int h = tid >> 7, j = tid & 127;
     f16* ob = out + (int64_t)b * nqh * kHeadDim + h0 * kHeadDim;
-    const int64_t part0 = (int64_t)P.part_base[b] + (int64_t)kvh * ngr;
+    const int64_t part0 = (int64_t)__builtin_amdgcn_readlane(e_part, b) + (int64_t)kvh * ngr;
 
     // Partial merge a <- a (+) b of two row states (each lane: (m, l) of the
     // head of its parity, 8 dims of both heads): M = max, then each side
