@@ -598,26 +598,44 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
 
     // Piece = number of later piece starts at or before this workgroup (one
     // lane per piece, a ballot); then kv head minor, and the row block from
-    // the piece's item table (one lane per row block, a ballot).
-    static_assert(kMaxPrefillPieces <= 64 && kMaxRowBlocks <= 64, "one lane per piece / row block");
-    const int pc = __popcll(__ballot(lane + 1 < S.n && S.item_base[lane + 1] <= (int)blockIdx.x));
-    const int local = blockIdx.x - S.item_base[pc];
+    // the piece's item table (one lane per row block, a ballot).  Each lookup
+    // is one round trip: lane i reads piece i's fields (the argument arrays
+    // hold 64 pieces) and then row block i's table entries (indices clamped
+    // to the piece's nrb, inside its table), and the chosen piece's and row
+    // block's fields are lane reads, not further dependent loads.
+    static_assert(kMaxPrefillPieces == 64 && kMaxRowBlocks <= 64, "one lane per piece / row block");
+    const int p_ib0 = S.item_base[lane], p_ib1 = S.item_base[lane + 1], p_part = S.part_base[lane];
+    const int p_rbb = S.rb_base[lane], p_nrb = S.nrb[lane], p_tps = S.tps[lane];
+    const int p_ks = S.kv_start[lane], p_rows = S.rows[lane], p_rowb = S.row_base[lane];
+    const int64_t p_kvo = S.kv_off[lane];
+    // Loaded with the others (not under the lane + 1 < S.n test), and the
+    // argument pointers with them (not after the second lookup).
+    asm volatile("" ::"v"(p_ib1), "s"(a.q), "s"(a.out), "s"(a.k), "s"(a.v));
+    const int pc = __popcll(__ballot(lane + 1 < S.n && p_ib1 <= (int)blockIdx.x));
+    const int local = blockIdx.x - __builtin_amdgcn_readlane(p_ib0, pc);
     const int kvh = local % a.nkvh;
     const int rem = local / a.nkvh;
-    const int* sp = S.sp + S.rb_base[pc] + pc;
-    const int nrb = S.nrb[pc];
-    const int rb = __popcll(__ballot(lane + 1 < nrb && sp[lane + 1] <= rem));
-    const int split = rem - sp[rb];
-    const int nsp = sp[rb + 1] - sp[rb];
-    const int tps = S.tps[pc];
-    const int64_t rec0 = (int64_t)S.part_base[pc] + (int64_t)kvh * sp[nrb] + sp[rb];
-    uint32_t* ctr = counters + (int64_t)(S.rb_base[pc] + rb) * a.nkvh + kvh;
-    a.s = S.rows[pc];
-    a.kv_start = S.kv_start[pc];
-    a.q += (int64_t)S.row_base[pc] * a.nqh * kHeadDim;
-    a.out += (int64_t)S.row_base[pc] * a.nqh * kHeadDim;
-    a.k += S.kv_off[pc];
-    a.v += S.kv_off[pc];
+    const int rb_base = __builtin_amdgcn_readlane(p_rbb, pc);
+    const int nrb = __builtin_amdgcn_readlane(p_nrb, pc);
+    const int* sp = S.sp + rb_base + pc;
+    const int sp0 = sp[min(lane, nrb)], sp1 = sp[min(lane + 1, nrb)];
+    const int rb = __popcll(__ballot(lane + 1 < nrb && sp1 <= rem));
+    const int sp_rb = __builtin_amdgcn_readlane(sp0, rb);
+    const int split = rem - sp_rb;
+    const int nsp = __builtin_amdgcn_readlane(sp1, rb) - sp_rb;
+    const int tps = __builtin_amdgcn_readlane(p_tps, pc);
+    const int64_t rec0 = (int64_t)__builtin_amdgcn_readlane(p_part, pc) +
+                         (int64_t)kvh * __builtin_amdgcn_readlane(sp1, nrb - 1) + sp_rb;
+    uint32_t* ctr = counters + (int64_t)(rb_base + rb) * a.nkvh + kvh;
+    a.s = __builtin_amdgcn_readlane(p_rows, pc);
+    a.kv_start = __builtin_amdgcn_readlane(p_ks, pc);
+    const int row_base = __builtin_amdgcn_readlane(p_rowb, pc);
+    const int64_t kv_off = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(p_kvo >> 32), pc) << 32) |
+                                     (uint32_t)__builtin_amdgcn_readlane((int)p_kvo, pc));
+    a.q += (int64_t)row_base * a.nqh * kHeadDim;
+    a.out += (int64_t)row_base * a.nqh * kHeadDim;
+    a.k += kv_off;
+    a.v += kv_off;
     const int row0 = rb * RB;
     const int kend = a.kv_start + min(row0 + RB, a.s);  // keys < kend
     const int ntiles = (kend + kTileKeys - 1) / kTileKeys;
