@@ -617,15 +617,21 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     const int rem = local / a.nkvh;
     const int rb_base = __builtin_amdgcn_readlane(p_rbb, pc);
     const int nrb = __builtin_amdgcn_readlane(p_nrb, pc);
-    const int* sp = S.sp + rb_base + pc;
-    const int sp0 = sp[min(lane, nrb)], sp1 = sp[min(lane + 1, nrb)];
-    const int rb = __popcll(__ballot(lane + 1 < nrb && sp1 <= rem));
-    const int sp_rb = __builtin_amdgcn_readlane(sp0, rb);
+    // A piece with one item per row block (no split) needs no item table:
+    // its row block is the item.  Otherwise a second round trip reads it.
+    const int pitems = __builtin_amdgcn_readlane(p_ib1, pc) - __builtin_amdgcn_readlane(p_ib0, pc);
+    int rb = rem, sp_rb = rem, nsp = 1, sp_nrb = nrb;
+    if (pitems != a.nkvh * nrb) {
+        const int* sp = S.sp + rb_base + pc;
+        const int sp0 = sp[min(lane, nrb)], sp1 = sp[min(lane + 1, nrb)];
+        rb = __popcll(__ballot(lane + 1 < nrb && sp1 <= rem));
+        sp_rb = __builtin_amdgcn_readlane(sp0, rb);
+        nsp = __builtin_amdgcn_readlane(sp1, rb) - sp_rb;
+        sp_nrb = __builtin_amdgcn_readlane(sp1, nrb - 1);
+    }
     const int split = rem - sp_rb;
-    const int nsp = __builtin_amdgcn_readlane(sp1, rb) - sp_rb;
     const int tps = __builtin_amdgcn_readlane(p_tps, pc);
-    const int64_t rec0 = (int64_t)__builtin_amdgcn_readlane(p_part, pc) +
-                         (int64_t)kvh * __builtin_amdgcn_readlane(sp1, nrb - 1) + sp_rb;
+    const int64_t rec0 = (int64_t)__builtin_amdgcn_readlane(p_part, pc) + (int64_t)kvh * sp_nrb + sp_rb;
     uint32_t* ctr = counters + (int64_t)(rb_base + rb) * a.nkvh + kvh;
     a.s = __builtin_amdgcn_readlane(p_rows, pc);
     a.kv_start = __builtin_amdgcn_readlane(p_ks, pc);
