@@ -207,6 +207,19 @@ def test_prefill_plan_fewest_tiles_per_split_within_256_items():
     assert (p["tiles_per_split"], p["sp_base"][-1] * NKVH) == (24, 256)
 
 
+def test_prefill_plan_fits_the_noalloc_scratch_up_to_its_row_limit():
+    """qasr_prefill_attn_noalloc runs qasr_prefill_attn's own plan out of a
+    512-item scratch; its header's limit, s <= 64 * min(64, 256 / nkvh) rows,
+    must keep every default plan within it, for every kv-head count."""
+    rng = np.random.default_rng(8)
+    for nkvh in (1, 2, 4, 8, 16):
+        limit = 64 * min(64, 256 // nkvh)
+        for rows in [1, 64, 65, 1024, limit] + [int(x) for x in rng.integers(1, limit + 1, 60)]:
+            for kv_start in [0, 500, 7680, int(rng.integers(0, 12289))]:
+                p = qasr_attn.plan_prefill(rows, kv_start, nkvh)
+                assert p["sp_base"][-1] * nkvh <= 512, (nkvh, rows, kv_start, p["tiles_per_split"])
+
+
 def test_prefill_plan_bench_configs(monkeypatch):
     p = qasr_attn.plan_prefill(420, 0, NKVH)  # config 2
     assert (p["rows_per_block"], p["nrb"], p["tiles_per_split"]) == (32, 14, 4)
