@@ -359,7 +359,7 @@ int qasr_plan_decode(int batch, const int32_t* lens, int nkvh, int cus, int32_t*
                      int32_t* run_out, int32_t* wg_base_out);
 
 /* Prefill (qasr_prefill_attn, one launch of 1..4096 rows at kv_start):
- * *rows_per_block (64, or 32 for unsplit short key ranges), *nrb row
+ * *rows_per_block (64; 32 or 16 for unsplit short key ranges), *nrb row
  * blocks, *tiles_per_split 128-key tiles per split (QASR_PREFILL_TPS
  * applies), sp_base_out[0..nrb]: row block rb's items are sp_base_out[rb] ..
  * sp_base_out[rb+1]-1 within each kv head (sp_base_out[nrb] items per kv

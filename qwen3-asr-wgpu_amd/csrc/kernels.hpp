@@ -101,7 +101,7 @@ struct PrefillArgs {
 constexpr int kMaxRowBlocks = 64;  // row blocks of one piece (4096 rows)
 constexpr int kPrefillRows = 64;
 struct PrefillPlan {
-    int32_t rows_per_block;  // kPrefillRows, or kPrefillRows / 2 for unsplit short key ranges
+    int32_t rows_per_block;  // kPrefillRows, or kPrefillRows / 2 or / 4 for unsplit short key ranges
     int32_t nrb;
     int32_t tps;
     int32_t items_per_kvh;
@@ -153,7 +153,7 @@ struct PrefillSegs {
 
 PrefillPlan plan_prefill(int s, int kv_start, int nkvh, int tiles_per_split,
                          int rows_per_block = kPrefillRows);
-// rows_per_block: 64 or 32, the block size every piece of S was planned with.
+// rows_per_block: 64, 32 or 16, the block size every piece of S was planned with.
 hipError_t launch_prefill_attn(const PrefillArgs& a, int rows_per_block, const PrefillSegs& S,
                                const PrefillWs& ws, hipStream_t stream);
 

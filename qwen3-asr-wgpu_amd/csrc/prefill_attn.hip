@@ -94,12 +94,14 @@ __device__ __forceinline__ int swz16(int r) { return ((r & 3) << 2) | ((r >> 2) 
 // transposing read of 4 consecutive rows x 32 dims is then 256 contiguous
 // bytes, and every operand address is a per-lane base plus a constant.
 //
-// Both tiles arrive by direct global -> LDS copies: instruction j of wave w
-// (of 8) writes LDS bytes [(8j + w) KB, +1 KB), lane l at +16 l.
-//   K: row 32j + 4w + l/16, slot l%16 = chunk (l%16) ^ swz16(4w + l/16);
-//   V: slab j, rows 16w + l/4, dims 32j + 8(l%4) .. +8.
-// Per thread the global source row is fixed within the tile (plus 32 j for K;
-// V instruction j reads the next 64 bytes of the same row).
+// Both tiles arrive by direct global -> LDS copies of one KB per wave
+// instruction, lane l at +16 l.  With NW waves (8, or 4 for 16-row blocks):
+//   K: instruction j of wave w writes KB NW j + w: rows 4 (NW j + w) + l/16,
+//      slot l%16 = chunk (l%16) ^ swz16(4w + l/16) (swz16 has period 16);
+//   V: slab j (32 dims, 8 KB of 16-row KBs), row group w + NW i: KB
+//      8j + w + NW i, rows 16 (w + NW i) + l/4, dims 32j + 8(l%4) .. +8.
+// Per thread the global source row is fixed within the tile (plus 4 NW j for
+// K; V instruction j reads the next 64 bytes of the same row).
 // The copies are issued as inline asm (M0 = LDS destination): the compiler
 // then does not wait for them before unrelated LDS reads of the other
 // buffers; the kernel waits for them itself (vmcnt(0)) before each barrier.
@@ -109,36 +111,45 @@ __device__ __forceinline__ int swz16(int r) { return ((r & 3) << 2) | ((r >> 2) 
 // whereas an out-of-range copy would leave whatever the LDS held before.
 // t0: first key of the tile; krow/vrow, kchunk/vchunk: this thread's row
 // within the tile and byte offset within the row (see the layout above).
+template <int NW>
 __device__ __forceinline__ void dma_tile(u32x4v kr, u32x4v vr, int t0, int kend, int krow,
                                          int kchunk, int vrow, int vchunk, const f16* kdst,
                                          const f16* vdst, int wave) {
+    static_assert((NW == 8 || NW == 4) && kTileKeys == 128, "copy pattern: 32 + 32 one-KB blocks per tile");
     const int last = kend - 1;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int rk = min(t0 + krow + 32 * j, last);
-        dma16(kr, rk * 256 + kchunk, lds_addr(kdst + (8 * j + wave) * 512));
+    for (int j = 0; j < 32 / NW; ++j) {
+        const int rk = min(t0 + krow + 4 * NW * j, last);
+        dma16(kr, rk * 256 + kchunk, lds_addr(kdst + (NW * j + wave) * 512));
     }
-    const int rv = min(t0 + vrow, last);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) dma16(vr, rv * 256 + vchunk + j * 64, lds_addr(vdst + (8 * j + wave) * 512));
+    for (int i = 0; i < 8 / NW; ++i) {
+        const int rv = min(t0 + vrow + 16 * NW * i, last);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            dma16(vr, rv * 256 + vchunk + j * 64, lds_addr(vdst + (8 * j + wave + NW * i) * 512));
+    }
 }
-static_assert(kAllWaves == 8 && kTileKeys == 128, "copy pattern: 32 one-KB blocks per tile over 8 waves");
+// Copy instructions per thread and tile.
+template <int NW>
+constexpr int kTileCopies = 32 / NW + 4 * (8 / NW);
 
 // Q block: 64 rows x the kv head's 2 q heads (512 contiguous bytes per row),
-// copied like the tiles (instruction j of wave w: LDS KB 8j + w, lane l at
-// +16 l, i.e. row 2(8j + w) + l/32, slot l%32).  Slot c of row r holds
+// copied like the tiles (instruction j of wave w of NW: LDS KB NW j + w, lane
+// l at +16 l, i.e. row 2(NW j + w) + l/32, slot l%32).  Slot c of row r holds
 // 16-byte chunk c ^ (r & 15), so the operand read (16 consecutive rows, one
 // chunk each) hits 16 different slots.  Rows past the block's last row are
 // read from row s-1 (finite values; their outputs are not written).
 constexpr int kQBlockHalves = kRowsPerBlock * kRep * kHeadDim;  // 32 KB
-template <int RB>  // rows of the block: RB / 16 instructions per wave
+template <int RB, int NW>  // rows of the block: RB / (2 NW) instructions per wave
 __device__ __forceinline__ void dma_q(u32x4v qr, int row0, int last_row, int ldq_bytes, const f16* qdst,
                                       int wave, int lane) {
+    static_assert(RB % (2 * NW) == 0, "whole KBs per wave");
 #pragma unroll
-    for (int j = 0; j < RB / 16; ++j) {
-        const int r = 2 * (8 * j + wave) + (lane >> 5);
+    for (int j = 0; j < RB / (2 * NW); ++j) {
+        const int r = 2 * (NW * j + wave) + (lane >> 5);
         const int c = (lane & 31) ^ (r & 15);
-        dma16(qr, min(row0 + r, last_row) * ldq_bytes + c * 16, lds_addr(qdst + (8 * j + wave) * 512));
+        dma16(qr, min(row0 + r, last_row) * ldq_bytes + c * 16, lds_addr(qdst + (NW * j + wave) * 512));
     }
 }
 
@@ -568,9 +579,12 @@ __device__ __forceinline__ void epilogue(Wave& w, const EpiArgs& e) {
 // key group kg = wave >> 2 taking keys 64 kg .. +64 of every tile.  NKG = 4
 // (short key ranges): 32-row blocks, rw = wave & 1 (the 2 q heads), kg =
 // wave >> 1 taking keys 32 kg .. +32 -- half the work per workgroup and
-// twice the workgroups.
-template <int NKG>
-__global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
+// twice the workgroups.  NKG = 4 on NW = 4 waves: 16-row blocks, one row
+// wave whose 32 MFMA columns hold both q heads (column n: head n / 16, row
+// n % 16) and kg = wave -- one wave per SIMD, a quarter of the 64-row
+// block's work per workgroup.
+template <int NKG, int NW = kAllWaves>
+__global__ __launch_bounds__(NW * 64, 1) void prefill_attn_kernel(
     PrefillArgs a, PrefillSegs S, float* __restrict__ ws_o, float* __restrict__ ws_ml,
     uint32_t* __restrict__ counters) {
     // 160 KB: K and V tiles, double buffered, and the Q block.
@@ -582,8 +596,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    constexpr int kRowWaves = kAllWaves / NKG;
-    constexpr int RB = 16 * kRowWaves;        // rows per block: 64 or 32
+    static_assert(NW == kAllWaves || (NW == 4 && NKG == 4), "wave counts");
+    constexpr int kRowWaves = NW / NKG;
+    constexpr int RB = 16 * kRowWaves;        // rows per block: 64, 32 or 16
+    constexpr bool PACK = kRowWaves == 1;     // both q heads in one wave's columns
     constexpr int GK = kTileKeys / NKG;       // keys per key group and tile: 64 or 32
     constexpr int NB = GK / 32;               // 32-key MFMA blocks per step
     const int wave = tid >> 6;       // 0..7: copy slot
@@ -648,15 +664,18 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     const int t_begin = split * tps;
     const int t_end = min(t_begin + tps, ntiles);
 
-    const int head = kvh * kRep + (rw & 1);
-    const int wrow0 = row0 + (rw >> 1) * 32;  // first row of this wave
-    const int r = wrow0 + n;                    // this lane's query row
+    // This lane's q head (of the kv head's kRep) and row within the block.
+    const int hsel = PACK ? (n >> 4) : (rw & 1);
+    const int rin = PACK ? (n & 15) : (rw >> 1) * 32 + n;
+    const int head = kvh * kRep + hsel;
+    const int wrow0 = row0 + (PACK ? 0 : (rw >> 1) * 32);  // first row of this wave
+    const int r = row0 + rin;                   // this lane's query row
     const bool row_ok = r < a.s;
     const int ldq = a.nqh * kHeadDim;
     // Key range of the wave's rows: a half tile from key k0 on is masked when
     // k0 + 63 > first_pos and skipped when k0 > last_pos.
     const int first_pos = a.kv_start + wrow0;
-    const int last_pos = first_pos + 31;
+    const int last_pos = first_pos + (PACK ? 15 : 31);
 
     const u32x4v kres = make_rsrc_words(a.k + kvh * a.head_stride, kend * kHeadDim * 2);
     const u32x4v vres = make_rsrc_words(a.v + kvh * a.head_stride, kend * kHeadDim * 2);
@@ -667,13 +686,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
     const int vchunk = (lane & 3) * 16;
 
     // Every copy is issued here in this order and waited for by count:
-    // tile t_begin (8 per thread), the Q block (4), tile t_begin + 1 (8).
+    // tile t_begin (kTileCopies<NW> per thread), the Q block, tile t_begin + 1.
     const u32x4v qres = make_rsrc_words(a.q + kvh * kRep * kHeadDim,
                                         (a.s - 1) * ldq * 2 + kRep * kHeadDim * 2);
-    dma_tile(kres, vres, t_begin * kTileKeys, kend, krow, kchunk, vrow, vchunk, K0, V0, cwave);
-    dma_q<RB>(qres, row0, a.s - 1, ldq * 2, Qs, cwave, lane);
+    dma_tile<NW>(kres, vres, t_begin * kTileKeys, kend, krow, kchunk, vrow, vchunk, K0, V0, cwave);
+    dma_q<RB, NW>(qres, row0, a.s - 1, ldq * 2, Qs, cwave, lane);
     const bool two = t_begin + 1 < t_end;
-    if (two) dma_tile(kres, vres, (t_begin + 1) * kTileKeys, kend, krow, kchunk, vrow, vchunk, K1, V1, cwave);
+    if (two) dma_tile<NW>(kres, vres, (t_begin + 1) * kTileKeys, kend, krow, kchunk, vrow, vchunk, K1, V1, cwave);
 
     Wave w;
     w.g = g;
@@ -716,21 +735,26 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_attn_kernel(
         }
         tile_sync();
         if (t + 2 < t_end)
-            dma_tile(kres, vres, (t + 2) * kTileKeys, kend, krow, kchunk, vrow, vchunk, kt, vt, cwave);
+            dma_tile<NW>(kres, vres, (t + 2) * kTileKeys, kend, krow, kchunk, vrow, vchunk, kt, vt, cwave);
     };
     // Tile t_begin and Q have landed (tile t_begin + 1 may be in flight).
-    if (two)
-        __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
-    else
+    static_assert(kTileCopies<NW> == 8 || kTileCopies<NW> == 16, "vmcnt encodings below");
+    if (two) {
+        if constexpr (kTileCopies<NW> == 8)
+            __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+        else
+            __builtin_amdgcn_s_waitcnt(0x4F70);  // vmcnt(16)
+    } else {
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    }
     __syncthreads();
     {
-        // Q^T operand, k-step ks: chunk 16*(head&1) + 2*ks + g of row n.
-        const int qr = (rw >> 1) * 32 + n;
+        // Q^T operand, k-step ks: chunk 16*hsel + 2*ks + g of the lane's row.
+        const int qr = rin;
         const f16* qrow = Qs + qr * (kRep * kHeadDim);
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
-            const int c = (((rw & 1) * 16 + 2 * ks + g) ^ (qr & 15));
+            const int c = ((hsel * 16 + 2 * ks + g) ^ (qr & 15));
             w.qb[ks] = *(const half8v*)(qrow + c * 8);
         }
     }
@@ -787,7 +811,10 @@ hipError_t launch_prefill_attn(const PrefillArgs& a, int rows_per_block, const P
     const int rbs = S.rb_base[last] + S.nrb[last];
     const int64_t recs = (int64_t)S.part_base[last] + (int64_t)a.nkvh * S.sp[S.rb_base[last] + last + S.nrb[last]];
     if (rbs > kMaxLaunchRowBlocks || recs > ws.items) return hipErrorInvalidValue;
-    if (rows_per_block == kRowsPerBlock / 2)
+    if (rows_per_block == kRowsPerBlock / 4)
+        hipLaunchKernelGGL((prefill_attn_kernel<4, 4>), dim3(items), dim3(4 * 64), 0, stream, a, S,
+                           ws.o, ws.ml, ws.counters);
+    else if (rows_per_block == kRowsPerBlock / 2)
         hipLaunchKernelGGL((prefill_attn_kernel<4>), dim3(items), dim3(kThreads), 0, stream, a, S,
                            ws.o, ws.ml, ws.counters);
     else if (rows_per_block == kRowsPerBlock)

@@ -343,9 +343,10 @@ __global__ void zero_u32_kernel(uint32_t* p, int n) {
 
 // Longest prefill one qasr_prefill_attn_noalloc call takes.  A default plan
 // of r rows has at most 256 + nkvh * ceil(r / 64) work items: a split plan
-// at most 256, an unsplit 64-row one nkvh * ceil(r / 64), an unsplit 32-row
-// one (key ranges of at most 1024 keys, so r <= 1024) nkvh * ceil(r / 32) <=
-// 2 nkvh * ceil(r / 64) <= 256 + nkvh * ceil(r / 64) for nkvh <= 16.  Up to
+// at most 256, an unsplit 16-row one too, an unsplit 64-row one
+// nkvh * ceil(r / 64), an unsplit 32-row one (key ranges of at most 1024
+// keys, so r <= 1024) nkvh * ceil(r / 32) <= 2 nkvh * ceil(r / 64) <= 256 +
+// nkvh * ceil(r / 64) for nkvh <= 16.  Up to
 // this many rows every default plan fits the scratch array, and the
 // no-allocation call runs exactly qasr_prefill_attn's items.
 int noalloc_max_rows(int nkvh) {
@@ -363,8 +364,8 @@ int noalloc_max_rows(int nkvh) {
 // items at 24.  A split's merge (publish, ticket, read back) is about three
 // memory round trips, as long as several latency-bound tiles: key ranges of
 // up to kPrefillNoSplitTiles tiles are never split.  Unsplit short ranges
-// also take 32-row blocks: twice the workgroups, half the work on the
-// longest one.  A forced split count (tps_forced > 0, QASR_PREFILL_TPS)
+// also take 16-row blocks when their items fit 256, else 32-row blocks:
+// more workgroups, less work on the longest one.  A forced split count (tps_forced > 0, QASR_PREFILL_TPS)
 // keeps 64-row blocks.
 qasr::PrefillPlan choose_prefill_plan(int rows, int ks, int nkvh, int tps_forced) {
     const int nrb = (rows + qasr::kPrefillRows - 1) / qasr::kPrefillRows;
@@ -374,8 +375,13 @@ qasr::PrefillPlan choose_prefill_plan(int rows, int ks, int nkvh, int tps_forced
     if (tps <= 0) {
         const int64_t want = std::max<int64_t>(1, 256 / nkvh);  // items per kv head
         if (max_tiles <= kPrefillNoSplitTiles) {
+            // Unsplit: 16-row blocks (one wave per SIMD, both q heads in its
+            // MFMA columns) while their items fit one workgroup per CU for
+            // 256 CUs, else 32-row blocks.
             tps = max_tiles;
-            rb_rows = qasr::kPrefillRows / 2;
+            const int64_t nrb16 = (rows + qasr::kPrefillRows / 4 - 1) / (qasr::kPrefillRows / 4);
+            rb_rows = nrb16 <= qasr::kMaxRowBlocks && nrb16 * nkvh <= 256 ? qasr::kPrefillRows / 4
+                                                                          : qasr::kPrefillRows / 2;
         } else {
             // Items at t tiles per split: sum over row blocks of ceil(tiles / t),
             // at least sum(tiles) / t, so t starts at sum(tiles) / want.
@@ -473,7 +479,7 @@ int run_prefill_segments(qasr_ctx* ctx, qasr_kv* kv, int layer, const qasr_segme
     const qasr::CacheGeom g = geom(kv);
     const int64_t cap = noalloc ? kScratchItems : std::numeric_limits<int64_t>::max();
     std::vector<PrefillLaunch> launches;
-    for (const int rpb : {qasr::kPrefillRows, qasr::kPrefillRows / 2}) {
+    for (const int rpb : {qasr::kPrefillRows, qasr::kPrefillRows / 2, qasr::kPrefillRows / 4}) {
         PrefillLaunch* L = nullptr;
         for (const Piece& pc : pieces) {
             if (pc.P.rows_per_block != rpb) continue;

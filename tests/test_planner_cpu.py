@@ -163,14 +163,14 @@ def test_decode_plan_refusals():
 
 def check_prefill_plan(rows, kv_start, p):
     rpb, nrb, tps, sp = p["rows_per_block"], p["nrb"], p["tiles_per_split"], p["sp_base"]
-    assert rpb in (32, 64) and tps >= 1
+    assert rpb in (16, 32, 64) and tps >= 1
     assert nrb == -(-rows // rpb)
     assert sp[0] == 0 and len(sp) == nrb + 1
     for rb in range(nrb):
         kend = kv_start + min((rb + 1) * rpb, rows)
         tiles = -(-kend // 128)
         assert sp[rb + 1] - sp[rb] == -(-tiles // tps), (rows, kv_start, rb)
-    if rpb == 32:  # 32-row blocks only for unsplit key ranges
+    if rpb < 64:  # 32- and 16-row blocks only for unsplit key ranges
         assert all(sp[rb + 1] - sp[rb] == 1 for rb in range(nrb))
 
 
@@ -192,7 +192,7 @@ def test_prefill_plan_fewest_tiles_per_split_within_256_items():
         kv_start = int(rng.integers(0, 12289))
         p = qasr_attn.plan_prefill(rows, kv_start, NKVH)
         check_prefill_plan(rows, kv_start, p)
-        if p["rows_per_block"] == 32:
+        if p["rows_per_block"] < 64:
             continue
         nrb, tps, items = p["nrb"], p["tiles_per_split"], p["sp_base"][-1]
         tiles = [-(-(kv_start + min((rb + 1) * 64, rows)) // 128) for rb in range(nrb)]
@@ -221,18 +221,20 @@ def test_prefill_plan_fits_the_noalloc_scratch_up_to_its_row_limit():
 
 
 def test_prefill_plan_bench_configs(monkeypatch):
-    p = qasr_attn.plan_prefill(420, 0, NKVH)  # config 2
-    assert (p["rows_per_block"], p["nrb"], p["tiles_per_split"]) == (32, 14, 4)
-    assert p["sp_base"] == list(range(15))
+    p = qasr_attn.plan_prefill(420, 0, NKVH)  # config 2: 16-row blocks, 216 items
+    assert (p["rows_per_block"], p["nrb"], p["tiles_per_split"]) == (16, 27, 4)
+    assert p["sp_base"] == list(range(28))
     p = qasr_attn.plan_prefill(512, 7680, NKVH)  # config 4's last chunk: 4 splits of 16 tiles
     assert (p["rows_per_block"], p["nrb"], p["tiles_per_split"]) == (64, 8, 16)
     assert p["sp_base"][-1] * NKVH == 256
-    p = qasr_attn.plan_prefill(512, 0, NKVH)  # 4 tiles: never split
-    assert p["rows_per_block"] == 32 and p["sp_base"][-1] == 16
+    p = qasr_attn.plan_prefill(512, 0, NKVH)  # 4 tiles: never split; 32 x 8 16-row items fit 256
+    assert p["rows_per_block"] == 16 and p["sp_base"][-1] == 32
+    p = qasr_attn.plan_prefill(520, 0, NKVH)  # 33 x 8 16-row items would not: 32-row blocks
+    assert p["rows_per_block"] == 32 and p["sp_base"][-1] == 17
     p = qasr_attn.plan_prefill(1024, 0, NKVH)  # 8 tiles: never split
     assert p["rows_per_block"] == 32 and p["sp_base"][-1] == 32
     p = qasr_attn.plan_prefill(300, 724, NKVH)  # 8 tiles at kv_start 724: never split
-    assert p["rows_per_block"] == 32 and p["sp_base"][-1] == 10
+    assert p["rows_per_block"] == 16 and p["sp_base"][-1] == 19
     p = qasr_attn.plan_prefill(1025, 0, NKVH)  # 9 tiles: 64-row blocks, split
     assert p["rows_per_block"] == 64 and p["sp_base"][-1] > p["nrb"]
     check_prefill_plan(1025, 0, p)
