@@ -600,6 +600,7 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_attn_kernel(
     constexpr int kRowWaves = NW / NKG;
     constexpr int RB = 16 * kRowWaves;        // rows per block: 64, 32 or 16
     constexpr bool PACK = kRowWaves == 1;     // both q heads in one wave's columns
+    static_assert(!PACK || kRep == 2, "two q heads x 16 rows fill a wave's 32 MFMA columns");
     constexpr int GK = kTileKeys / NKG;       // keys per key group and tile: 64 or 32
     constexpr int NB = GK / 32;               // 32-key MFMA blocks per step
     const int wave = tid >> 6;       // 0..7: copy slot

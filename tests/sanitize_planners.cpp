@@ -69,7 +69,7 @@ void prefill_case(int rows, int kv_start, int nkvh) {
     const int rc = qasr_plan_prefill(rows, kv_start, nkvh, &rpb, &nrb, &tps, sp.data());
     check(rc == QASR_OK, "qasr_plan_prefill refused valid rows", rows, kv_start);
     if (rc != QASR_OK) return;
-    check(rpb == 64 || rpb == 32, "rows per block", rpb);
+    check(rpb == 64 || rpb == 32 || rpb == 16, "rows per block", rpb);
     check(nrb >= 1 && nrb <= 64 && (int64_t)nrb * rpb >= rows && (int64_t)(nrb - 1) * rpb < rows,
           "row blocks", nrb, rows);
     check(tps >= 1, "tiles per split", tps);
@@ -80,6 +80,7 @@ void prefill_case(int rows, int kv_start, int nkvh) {
         const int64_t splits = (int64_t)sp[rb + 1] - sp[rb];
         check(splits >= 1 && splits * tps >= tiles && (splits - 1) * tps < tiles, "splits of a row block", rb,
               splits);
+        check(rpb == 64 || splits == 1, "a 32- or 16-row block split", rb, splits);
     }
     check(sp[66] == -1, "wrote past 65 bases");
 }
