@@ -476,6 +476,22 @@ int run_prefill_segments(qasr_ctx* ctx, qasr_kv* kv, int layer, const qasr_segme
         }
         r0 += segs[i].rows;
     }
+    // Many short pieces in one launch (the batched prefill): their 16-row
+    // blocks would make several rounds of one-wave-per-SIMD workgroups, so
+    // they run as 32-row blocks (eight waves) instead.  Both kernels give
+    // every row the same bits: the same MFMAs per output column, the same
+    // four 32-key groups combined in the same order, masks and rescales per
+    // lane, and a skipped all-masked half tile only adds zeros.  So a
+    // segment's output still does not depend on its batch mates.
+    {
+        int64_t items16 = 0;
+        for (const Piece& pc : pieces)
+            if (pc.P.rows_per_block == qasr::kPrefillRows / 4) items16 += (int64_t)nkvh * pc.P.items_per_kvh;
+        if (items16 > 256)
+            for (Piece& pc : pieces)
+                if (pc.P.rows_per_block == qasr::kPrefillRows / 4)
+                    pc.P = qasr::plan_prefill(pc.rows, pc.ks, nkvh, pc.P.tps, qasr::kPrefillRows / 2);
+    }
     const qasr::CacheGeom g = geom(kv);
     const int64_t cap = noalloc ? kScratchItems : std::numeric_limits<int64_t>::max();
     std::vector<PrefillLaunch> launches;

@@ -205,6 +205,37 @@ def test_prefill_attn_batch_equals_single_segment_calls(O, gpu, tps, monkeypatch
     g.close()
 
 
+def test_prefill_attn_batch_of_many_short_segments_equals_single_calls(O, gpu):
+    """Short segments alone run 16-row blocks (four waves, both q heads in
+    one wave's MFMA columns); twelve of them in one batched call run 32-row
+    blocks (eight waves, one q head per wave).  Every segment must still get
+    its lone call's bits."""
+    import qasr_attn
+    from gpu_helpers import dev, empty, host, say
+
+    from oracle import Rng
+
+    rng = Rng(SEED_BASE + 482)
+    lay = Layer(rng)
+    segments = [(i, ks, rows) for i, (ks, rows) in enumerate(
+        [(0, 420), (0, 150), (100, 300), (0, 512), (37, 1), (0, 33), (200, 250), (0, 400),
+         (5, 90), (0, 320), (64, 448), (0, 17)])]
+    for _, ks, rows in segments:  # each alone plans 16-row blocks
+        assert qasr_attn.plan_prefill(rows, ks, 8)["rows_per_block"] == 16, (ks, rows)
+    g, _, _, q = _segments_setup(O, rng, lay, segments, cap_for(1024))
+    say(f"prefill_attn_batch over {len(segments)} short segments")
+    out_b = empty(q.shape[0], QDIM)
+    qasr_attn.prefill_attn_batch(g.ctx, g.kv, 0, segments, dev(q), out_b)
+    got = host(out_b)
+    r0 = 0
+    for slot, kv_start, rows in segments:
+        out_s = empty(rows, QDIM)
+        qasr_attn.prefill_attn(g.ctx, g.kv, 0, slot, kv_start, rows, dev(q[r0:r0 + rows]), out_s)
+        assert np.array_equal(got[r0:r0 + rows], host(out_s)), f"segment {slot}"
+        r0 += rows
+    g.close()
+
+
 def test_prefill_attn_batch_long_segments_against_oracle(O, gpu):
     """Key ranges up to 2048 in one batched call (each segment on its own
     plan, some with key splits) against the oracle, segment by segment."""
