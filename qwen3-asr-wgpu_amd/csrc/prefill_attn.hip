@@ -32,6 +32,9 @@
 // buffered: the first two tiles and Q are requested together at the start,
 // and the copy of tile t+2 goes into tile t's buffers as soon as every wave is
 // done with them, so one tile is always in flight while another is consumed.
+// In 16-row blocks of more than 4 tiles each wave copies only the keys it
+// reads and waits for its own copies, so the loop has no barrier and two
+// tiles can be in flight.
 // Every copy is inline asm waited for by count, so nothing the compiler
 // inserts waits for a copy issued later.
 // When the key range of a row block is split, each item publishes its partial
@@ -133,6 +136,30 @@ __device__ __forceinline__ void dma_tile(u32x4v kr, u32x4v vr, int t0, int kend,
 // Copy instructions per thread and tile.
 template <int NW>
 constexpr int kTileCopies = 32 / NW + 4 * (8 / NW);
+
+// The same tile layout copied by 16-row blocks (four waves, key group =
+// wave): wave w copies exactly the 32 keys it reads, K rows 32w .. +31 (KBs
+// 8w + j, rows 32w + 4j + l/16) and V rows 32w .. +31 of every slab (KB
+// 8j + 2w + i, rows 32w + 16i + l/4), 16 instructions like dma_tile<4>.  A
+// wave then waits for its own copies only (vmcnt), with no workgroup
+// barrier, and keeps two tiles in flight.
+__device__ __forceinline__ void dma_slice(u32x4v kr, u32x4v vr, int t0, int kend, const f16* kdst,
+                                          const f16* vdst, int wave, int lane) {
+    const int last = kend - 1;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int row = 32 * wave + 4 * j + (lane >> 4);
+        dma16(kr, min(t0 + row, last) * 256 + ((lane & 15) ^ swz16(row)) * 16,
+              lds_addr(kdst + (8 * wave + j) * 512));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int rv = min(t0 + 32 * wave + 16 * i + (lane >> 2), last);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            dma16(vr, rv * 256 + (lane & 3) * 16 + j * 64, lds_addr(vdst + (8 * j + 2 * wave + i) * 512));
+    }
+}
 
 // Q block: 64 rows x the kv head's 2 q heads (512 contiguous bytes per row),
 // copied like the tiles (instruction j of wave w of NW: LDS KB NW j + w, lane
@@ -582,8 +609,9 @@ __device__ __forceinline__ void epilogue(Wave& w, const EpiArgs& e) {
 // twice the workgroups.  NKG = 4 on NW = 4 waves: 16-row blocks, one row
 // wave whose 32 MFMA columns hold both q heads (column n: head n / 16, row
 // n % 16) and kg = wave -- one wave per SIMD, a quarter of the 64-row
-// block's work per workgroup.
-template <int NKG, int NW = kAllWaves>
+// block's work per workgroup.  SLICE (16-row blocks only): each wave copies
+// the keys it reads and the loop has no barrier (dma_slice).
+template <int NKG, int NW = kAllWaves, bool SLICE = false>
 __global__ __launch_bounds__(NW * 64, 1) void prefill_attn_kernel(
     PrefillArgs a, PrefillSegs S, float* __restrict__ ws_o, float* __restrict__ ws_ml,
     uint32_t* __restrict__ counters) {
@@ -597,6 +625,7 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_attn_kernel(
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     static_assert(NW == kAllWaves || (NW == 4 && NKG == 4), "wave counts");
+    static_assert(!SLICE || NW == 4, "per-wave copies: 16-row blocks");
     constexpr int kRowWaves = NW / NKG;
     constexpr int RB = 16 * kRowWaves;        // rows per block: 64, 32 or 16
     constexpr bool PACK = kRowWaves == 1;     // both q heads in one wave's columns
@@ -690,10 +719,16 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_attn_kernel(
     // tile t_begin (kTileCopies<NW> per thread), the Q block, tile t_begin + 1.
     const u32x4v qres = make_rsrc_words(a.q + kvh * kRep * kHeadDim,
                                         (a.s - 1) * ldq * 2 + kRep * kHeadDim * 2);
-    dma_tile<NW>(kres, vres, t_begin * kTileKeys, kend, krow, kchunk, vrow, vchunk, K0, V0, cwave);
+    auto copy_tile = [&](int t, const f16* kt, const f16* vt) {
+        if constexpr (SLICE)
+            dma_slice(kres, vres, t * kTileKeys, kend, kt, vt, cwave, lane);
+        else
+            dma_tile<NW>(kres, vres, t * kTileKeys, kend, krow, kchunk, vrow, vchunk, kt, vt, cwave);
+    };
+    copy_tile(t_begin, K0, V0);
     dma_q<RB, NW>(qres, row0, a.s - 1, ldq * 2, Qs, cwave, lane);
     const bool two = t_begin + 1 < t_end;
-    if (two) dma_tile<NW>(kres, vres, (t_begin + 1) * kTileKeys, kend, krow, kchunk, vrow, vchunk, K1, V1, cwave);
+    if (two) copy_tile(t_begin + 1, K1, V1);
 
     Wave w;
     w.g = g;
@@ -722,7 +757,18 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_attn_kernel(
     // once every wave is done with its buffers and tile t+1 has landed, the
     // copy of tile t+2 into them.  Two tiles per iteration, so every LDS
     // address is a per-lane base plus a constant.
+    // SLICE: each wave reads and copies only its own key group's rows
+    // (dma_slice), so it waits for its own copies of tile t (those of tile
+    // t + 1 may stay in flight) and, once its own reads of the buffers have
+    // returned, copies tile t + 2 into them, with no barrier.
     auto run = [&](const f16* kt, const f16* vt, int t) {
+        if constexpr (SLICE) {
+            static_assert(kTileCopies<NW> == 16, "vmcnt(16) below");
+            if (t + 1 < t_end)
+                asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+            else
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
         const int k0 = t * kTileKeys + kg * GK;
         if (k0 <= last_pos) {  // some key visible to some row
             const f16* kh = kt + kg * GK * kHeadDim;
@@ -734,9 +780,15 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_attn_kernel(
                 step_s<true, NB>(w, kh, k0, pb);
             step_pv<NB>(w, vh, pb);
         }
-        tile_sync();
-        if (t + 2 < t_end)
-            dma_tile<NW>(kres, vres, (t + 2) * kTileKeys, kend, krow, kchunk, vrow, vchunk, kt, vt, cwave);
+        if constexpr (SLICE) {
+            if (t + 2 < t_end) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                copy_tile(t + 2, kt, vt);
+            }
+        } else {
+            tile_sync();
+            if (t + 2 < t_end) copy_tile(t + 2, kt, vt);
+        }
     };
     // Tile t_begin and Q have landed (tile t_begin + 1 may be in flight).
     static_assert(kTileCopies<NW> == 8 || kTileCopies<NW> == 16, "vmcnt encodings below");
@@ -770,6 +822,9 @@ __global__ __launch_bounds__(NW * 64, 1) void prefill_attn_kernel(
     // are free now); from here on both waves of a pair share the epilogue
     // work half and half.
     EpiArgs e{a, ws_o, ws_ml, ctr, K0, K1, V0, V1, Qs, rec0 + split, rec0, nsp, rw, r, head, row_ok, g, lane, tid};
+    // Every wave is done with the tile buffers (the SLICE loop has no
+    // barrier) and has no copy in flight (its last tile waited for vmcnt(0)).
+    if constexpr (SLICE) __syncthreads();
     if constexpr (NKG == 2) {
         if (kg == 0)
             epilogue<0>(w, e);
@@ -812,7 +867,16 @@ hipError_t launch_prefill_attn(const PrefillArgs& a, int rows_per_block, const P
     const int rbs = S.rb_base[last] + S.nrb[last];
     const int64_t recs = (int64_t)S.part_base[last] + (int64_t)a.nkvh * S.sp[S.rb_base[last] + last + S.nrb[last]];
     if (rbs > kMaxLaunchRowBlocks || recs > ws.items) return hipErrorInvalidValue;
-    if (rows_per_block == kRowsPerBlock / 4)
+    // 16-row blocks (never split): the per-wave copy loop once some item has
+    // more than 4 tiles (at 8 tiles 11.2 against 11.9 us; up to 4 tiles
+    // about 0.05 us slower than the barrier loop, whose copies keep up).
+    int max_tiles = 0;
+    for (int p = 0; p < S.n; ++p)
+        max_tiles = std::max(max_tiles, (S.kv_start[p] + S.rows[p] + kTileKeys - 1) / kTileKeys);
+    if (rows_per_block == kRowsPerBlock / 4 && max_tiles > 4)
+        hipLaunchKernelGGL((prefill_attn_kernel<4, 4, true>), dim3(items), dim3(4 * 64), 0, stream, a, S,
+                           ws.o, ws.ml, ws.counters);
+    else if (rows_per_block == kRowsPerBlock / 4)
         hipLaunchKernelGGL((prefill_attn_kernel<4, 4>), dim3(items), dim3(4 * 64), 0, stream, a, S,
                            ws.o, ws.ml, ws.counters);
     else if (rows_per_block == kRowsPerBlock / 2)

@@ -46,7 +46,7 @@ def test_config2_prefill_420(O, gpu):
 
 
 @pytest.mark.parametrize("kv_start,s", [(0, 1), (0, 31), (0, 64), (0, 65), (0, 200), (5, 1),
-                                        (100, 3), (640, 129), (1000, 600), (3000, 64)])
+                                        (100, 3), (640, 129), (724, 300), (1000, 600), (3000, 64)])
 def test_prefill_ragged_against_oracle(O, gpu, kv_start, s):
     from gpu_helpers import Gpu
 
